@@ -1,0 +1,95 @@
+// Device helpers shared by the attention kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/a8attn.h"
+
+namespace a8 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kLog2e = 1.4426950408889634f;
+
+// bf16 word -> fp32 (exact).
+__device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 word, round to nearest even; NaN -> 0x7fc0. This is bit-for-bit the conversion of
+// torch's c10::BFloat16 (and of a plain IEEE RNE narrowing for every non-NaN input).
+__device__ __forceinline__ uint32_t f2bf_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Two fp32 -> one dword of two bf16 (lo in bits 0..15) through the hardware's RNE conversion
+// (v_cvt_pk_bf16_f32). Used where values are finite by construction (softmax weights, outputs).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  __bf16 a = (__bf16)lo, b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+__device__ __forceinline__ u32x4 ld16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
+__device__ __forceinline__ void st16(void *p, u32x4 v) { *reinterpret_cast<u32x4 *>(p) = v; }
+__device__ __forceinline__ void st8(void *p, u32x2 v) { *reinterpret_cast<u32x2 *>(p) = v; }
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// D = A(16x32) * B(32x16) + C, bf16 in, fp32 accumulate. Lane l supplies A[l%16][8*(l/16)+j] and
+// B[8*(l/16)+j][l%16] (j = 0..7) and receives D[4*(l/16)+i][l%16] (i = 0..3). Only the pairing of A
+// and B slots matters for the sum over k, so callers may map any 32 reduction indices onto the
+// (lane group, slot) pairs as long as A and B use the same map.
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Cross-lane reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float max_over_groups(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float sum_over_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Orders LDS traffic between the lanes of one wave: the hardware serves one wave's LDS
+// instructions in issue order, so only the compiler's reordering has to be stopped.
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// 8x8 transpose of bf16 words held as 8 rows x 16 bytes: out[c] collects element c of every row
+// (row j in slot j). Each output dword pairs rows (2e, 2e+1).
+__device__ __forceinline__ void transpose8x8_bf16(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int dw = c >> 1;
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t a = in[2 * e][dw], b = in[2 * e + 1][dw];
+      o[e] = (c & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+    }
+    out[c] = o;
+  }
+}
+
+// Records the message for a negative status on the calling host thread and returns `code`
+// (defined in capi.hip).
+int set_error(int code, const char *fmt, ...);
+
+}  // namespace a8

@@ -1,0 +1,323 @@
+// Split-K flash-decoding over the slot KV cache, GQA (a8_decode_attn, a8_decode_choose).
+//
+// Semantics follow serve/fast_kernels.py:193-290: query row b (one token, nq heads) attends keys
+// [0, lens[b]) of cache row rowmap[b] (b when no rowmap); kv head kh serves q heads
+// [kh*group, (kh+1)*group). The row's keys are cut into nsplit ranges of
+// per = ceil(ceil(L/nsplit)/64)*64 keys (fast_kernels.py:207-209); each range produces a partial
+// (acc, m, l) with an online softmax in fp32 and bf16 softmax weights in the P.V product, and the
+// combine step merges the partials: w = exp(m - M) (0 for an empty range), out = sum(w acc)/sum(w l).
+//
+// MI355X design (the kernel streams ~512 B of K+V per key per row-layer from HBM; it is HBM bound):
+//   * One workgroup = one (row, kv head, split); its `waves` wavefronts take the split's 64-key
+//     tiles round-robin, each with its own online softmax, and merge through LDS at the end.
+//   * K tiles are loaded straight into MFMA operand registers with 128-bit loads (one key row is
+//     8 lanes x 16 B); S^T = K . Q^T runs on v_mfma_f32_16x16x32_bf16 with the group's q heads
+//     (<= 16) as the 16 columns. The key rows of each 16x16 S^T tile are permuted so that the
+//     C-layout of S^T is directly the B-operand layout of P^T (lane group g owns keys 8g..8g+7 of
+//     each 32-key chunk) -- no shuffles between the two products.
+//   * V tiles are loaded as 8 keys x 16 B per lane (each load instruction reads 8 whole 128-byte
+//     key rows), transposed 8x8 in registers and written to a wave-private LDS tile V^T[d][key],
+//     from where O^T += V^T . P^T reads 128-bit MFMA operands.
+//   * Softmax statistics live per lane (column = q head); the max is reduced across the four
+//     16-lane groups with cross-lane shuffles, the row sum is kept per lane group and reduced once.
+//   * Exponentials are exp2 on pre-scaled scores (scale * log2 e folded into one multiply); m is
+//     kept in the same log2 units in the workspace, which only this file's kernels read.
+#include "a8_common.h"
+
+namespace a8 {
+
+constexpr int kVRow = 72;  // LDS row of a transposed V tile: 64 keys + 8 pad (144 B, 16-B aligned)
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_decode_split(
+    const uint16_t *__restrict__ q, int64_t s_qb, int64_t s_qh,
+    const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+    int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
+    uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
+    float *__restrict__ ml_ws, int nq, int group, int ns, float scale_log2) {
+  __shared__ __attribute__((aligned(16))) uint16_t lds[NW * 64 * kVRow];
+  const int sp = blockIdx.x, kh = blockIdx.y, row = blockIdx.z;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r16 = lane & 15, g = lane >> 4;
+
+  int L = lens[row];
+  const int crow = rowmap ? rowmap[row] : row;
+  if (crow < 0 || crow >= cache_rows) L = 0;  // no such cache row: attend nothing
+  L = min(max(L, 0), cache_len);
+  const int per = ((L + ns - 1) / ns + 63) / 64 * 64;
+  const int lo = sp * per;
+  const int hi = min(lo + per, L);
+
+  // B operand of S^T = K.Q^T: column r16 = q head kh*group + r16, reduction slot (g, j) = dim 8g+j
+  // (first MFMA) and 32+8g+j (second MFMA).
+  u32x4 qB0 = {0u, 0u, 0u, 0u}, qB1 = {0u, 0u, 0u, 0u};
+  if (r16 < group) {
+    const uint16_t *qp = q + (int64_t)row * s_qb + (int64_t)(kh * group + r16) * s_qh + 8 * g;
+    qB0 = ld16(qp);
+    qB1 = ld16(qp + 32);
+  }
+  float m = kNegInf, lsum = 0.f;
+  f32x4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t cbase = (int64_t)(crow < 0 || crow >= cache_rows ? 0 : crow) * s_kb + (int64_t)kh * s_kh;
+  const uint16_t *kb = kc + cbase, *vb = vc + cbase;
+  uint16_t *vt = lds + w * 64 * kVRow;
+  const int kg = lane >> 3, dc = lane & 7;
+
+  for (int t0 = lo + 64 * w; t0 < hi; t0 += 64 * NW) {
+    const int last = hi - 1;  // keys past the range are clamped here and masked out below
+    u32x4 ka[2][2][2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int key = min(t0 + 32 * c + 8 * (r16 >> 2) + 4 * t + (r16 & 3), last);
+        const uint16_t *kp = kb + (int64_t)key * s_ks + 8 * g;
+        ka[c][t][0] = ld16(kp);
+        ka[c][t][1] = ld16(kp + 32);
+      }
+    u32x4 vr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int key = min(t0 + 8 * kg + j, last);
+      vr[j] = ld16(vb + (int64_t)key * s_ks + 8 * dc);
+    }
+
+    // S^T tile (c, t): row 4g+i <-> key t0 + 32c + 8g + 4t + i, column r16 <-> q head.
+    f32x4 s[2][2];
+    float mt = kNegInf;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f32x4 a = mfma16x16x32(ka[c][t][0], qB0, f32x4{0.f, 0.f, 0.f, 0.f});
+        a = mfma16x16x32(ka[c][t][1], qB1, a);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = t0 + 32 * c + 8 * g + 4 * t + i;
+          const float v = key < hi ? a[i] * scale_log2 : kNegInf;
+          a[i] = v;
+          mt = fmaxf(mt, v);
+        }
+        s[c][t] = a;
+      }
+    mt = max_over_groups(mt);
+    const float mn = fmaxf(m, mt);
+    const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
+    float ps = 0.f;
+    u32x4 pB[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = fast_exp2(s[c][t][i] - mn);
+          ps += p[i];
+        }
+        pB[c][2 * t] = pack_bf16x2(p[0], p[1]);
+        pB[c][2 * t + 1] = pack_bf16x2(p[2], p[3]);
+      }
+    lsum = lsum * alpha + ps;
+    m = mn;
+
+    u32x4 vtr[8];
+    transpose8x8_bf16(vr, vtr);
+#pragma unroll
+    for (int dd = 0; dd < 8; ++dd) st16(vt + (8 * dc + dd) * kVRow + 8 * kg, vtr[dd]);
+    wave_lds_fence();
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      o[dt] *= alpha;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x4 vA = ld16(vt + (16 * dt + r16) * kVRow + 32 * c + 8 * g);
+        o[dt] = mfma16x16x32(vA, pB[c], o[dt]);
+      }
+    }
+    wave_lds_fence();
+  }
+  lsum = sum_over_groups(lsum);
+
+  // Lane (r16, g) holds O^T[d = 16dt + 4g + i][head r16].
+  if (NW == 1) {
+    if (r16 >= group) return;
+    const int hq = kh * group + r16;
+    if (ns == 1) {
+      uint16_t *op = out + (int64_t)row * s_ob + (int64_t)hq * s_oh + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        st8(op + 16 * dt, u32x2{pack_bf16x2(o[dt][0] / lsum, o[dt][1] / lsum),
+                                pack_bf16x2(o[dt][2] / lsum, o[dt][3] / lsum)});
+    } else {
+      const int64_t pi = ((int64_t)row * nq + hq) * ns + sp;
+      float *ap = acc_ws + pi * 64 + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4 *>(ap + 16 * dt) = o[dt];
+      if (g == 0) {
+        ml_ws[pi * 2] = m;
+        ml_ws[pi * 2 + 1] = lsum;
+      }
+    }
+    return;
+  }
+
+  // Merge the waves' partials through LDS (the V tiles are dead now).
+  __syncthreads();
+  float *mb = reinterpret_cast<float *>(lds);  // [NW][16]
+  float *lb = mb + NW * 16;                     // [NW][16]
+  float *ob = lb + NW * 16;                     // [NW][16 heads][64 dims]
+  if (g == 0) {
+    mb[w * 16 + r16] = m;
+    lb[w * 16 + r16] = lsum;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4 *>(ob + (w * 16 + r16) * 64 + 16 * dt + 4 * g) = o[dt];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < group * 64; idx += 64 * NW) {
+    const int head = idx >> 6, d = idx & 63;
+    float M = kNegInf;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) M = fmaxf(M, mb[v * 16 + head]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float mv = mb[v * 16 + head];
+      const float wt = (mv == kNegInf) ? 0.f : fast_exp2(mv - M);
+      num += wt * ob[(v * 16 + head) * 64 + d];
+      den += wt * lb[v * 16 + head];
+    }
+    const int hq = kh * group + head;
+    if (ns == 1) {
+      out[(int64_t)row * s_ob + (int64_t)hq * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
+    } else {
+      const int64_t pi = ((int64_t)row * nq + hq) * ns + sp;
+      acc_ws[pi * 64 + d] = num;
+      if (d == 0) {
+        ml_ws[pi * 2] = M;
+        ml_ws[pi * 2 + 1] = den;
+      }
+    }
+  }
+}
+
+// One wave per (row, q head), lane = dim: merges the row's nsplit partials
+// (fast_kernels.py:238-253).
+__global__ __launch_bounds__(256) void k_decode_combine(const float *__restrict__ acc_ws,
+                                                        const float *__restrict__ ml_ws,
+                                                        uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh,
+                                                        int b, int nq, int ns) {
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= b * nq) return;
+  const int row = pair / nq, h = pair - row * nq, d = threadIdx.x & 63;
+  const float *ml = ml_ws + (int64_t)pair * ns * 2;
+  const float *acc = acc_ws + (int64_t)pair * ns * 64;
+  float M = kNegInf;
+  for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, ml[2 * sp]);
+  float num = 0.f, den = 0.f;
+  for (int sp = 0; sp < ns; ++sp) {
+    const float mv = ml[2 * sp];
+    const float wt = (mv == kNegInf) ? 0.f : fast_exp2(mv - M);
+    num += wt * acc[sp * 64 + d];
+    den += wt * ml[2 * sp + 1];
+  }
+  out[(int64_t)row * s_ob + (int64_t)h * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
+}
+
+static inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <int NW>
+static void launch_split(int ns, int nkv, int b, hipStream_t st, const uint16_t *q, int64_t s_qb, int64_t s_qh,
+                         const uint16_t *kc, const uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                         int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap, uint16_t *out,
+                         int64_t s_ob, int64_t s_oh, float *acc_ws, float *ml_ws, int nq, int group,
+                         float scale_log2) {
+  hipLaunchKernelGGL(k_decode_split<NW>, dim3(ns, nkv, b), dim3(64 * NW), 0, st, q, s_qb, s_qh, kc, vc, s_kb,
+                     s_kh, s_ks, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, nq, group,
+                     ns, scale_log2);
+}
+
+}  // namespace a8
+
+extern "C" int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
+                              const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                              int cache_rows, int cache_len,
+                              const int32_t *lens, const int32_t *rowmap,
+                              void *out, int64_t s_ob, int64_t s_oh,
+                              float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                              int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
+                              int phases, void *stream) {
+  using namespace a8;
+  if (hd != 64) return set_error(A8_EUNSUP, "decode_attn: head_dim %d not supported (64 only)", hd);
+  if (b < 0 || nq <= 0 || nkv <= 0 || nq % nkv || cache_rows < 0 || cache_len < 0 || nsplit < 1 || b > 65535)
+    return set_error(A8_EINVAL, "decode_attn: bad sizes b=%d nq=%d nkv=%d nsplit=%d", b, nq, nkv, nsplit);
+  const int group = nq / nkv;
+  if (group > 16) return set_error(A8_EUNSUP, "decode_attn: GQA group %d > 16 not supported", group);
+  if (waves != 1 && waves != 2 && waves != 4 && waves != 8)
+    return set_error(A8_EINVAL, "decode_attn: waves must be 1, 2, 4 or 8 (got %d)", waves);
+  if (b == 0) return 0;
+  if (!q || !kc || !vc || !lens || !out) return set_error(A8_EINVAL, "decode_attn: null pointer");
+  if (nsplit > 1 && (!acc_ws || !ml_ws || (int64_t)b * nsplit > ws_row_splits))
+    return set_error(A8_EWSPACE, "decode_attn: workspace holds %lld row-splits, need b*nsplit = %lld",
+                     (long long)ws_row_splits, (long long)b * nsplit);
+  if (!al16(q) || !al16(kc) || !al16(vc) || !al16(out) || (nsplit > 1 && !al16(acc_ws)) ||
+      (s_qb | s_qh | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
+    return set_error(A8_EALIGN, "decode_attn: pointers must be 16-byte aligned and strides multiples of 8");
+  const hipStream_t st = (hipStream_t)stream;
+  const float sl2 = scale * kLog2e;
+  const auto *qq = (const uint16_t *)q;
+  const auto *kk = (const uint16_t *)kc;
+  const auto *vv = (const uint16_t *)vc;
+  auto *oo = (uint16_t *)out;
+  if (phases & 1) {
+    switch (waves) {
+      case 1: launch_split<1>(nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
+                              lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2); break;
+      case 2: launch_split<2>(nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
+                              lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2); break;
+      case 4: launch_split<4>(nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
+                              lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2); break;
+      default: launch_split<8>(nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
+                               lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2); break;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  if ((phases & 2) && nsplit > 1) {
+    const unsigned grid = (unsigned)(((int64_t)b * nq + 3) / 4);
+    hipLaunchKernelGGL(k_decode_combine, dim3(grid), dim3(256), 0, st, acc_ws, ml_ws, oo, s_ob, s_oh, b, nq,
+                       nsplit);
+    return (int)hipGetLastError();
+  }
+  return 0;
+}
+
+// Launch-shape policy. A workgroup streams one split of one (row, kv head); the GPU wants about
+// kResidentWaves waves per CU in flight to cover HBM latency, and a wave wants at least
+// kMinTilesPerWave 64-key tiles so its prologue is amortised.
+extern "C" int a8_decode_choose(int b, int nkv, int cache_len, int nsplit_req, int nsplit_max,
+                                int64_t cap_row_splits, int n_cu, int *nsplit_out, int *waves_out) {
+  using namespace a8;
+  constexpr int kResidentWaves = 12, kMinTilesPerWave = 2;
+  if (b < 1 || nkv < 1 || cache_len < 0 || n_cu < 1 || !nsplit_out || !waves_out)
+    return set_error(A8_EINVAL, "decode_choose: bad arguments b=%d nkv=%d n_cu=%d", b, nkv, n_cu);
+  const int tiles = cache_len > 0 ? (cache_len + 63) / 64 : 1;
+  const int64_t units = (int64_t)b * nkv;
+  int64_t want = ((int64_t)n_cu * kResidentWaves + units - 1) / units;
+  const int64_t max_waves = (tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
+  if (want > max_waves) want = max_waves;
+  if (want < 1) want = 1;
+  int nw = want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1;
+  int64_t ns = (want + nw - 1) / nw;
+  if (ns < nsplit_req) ns = nsplit_req;
+  if (nsplit_max >= 1 && ns > nsplit_max) ns = nsplit_max;
+  if (ns > tiles) ns = tiles;
+  if (cap_row_splits >= 1 && ns > cap_row_splits / b) ns = cap_row_splits / b;
+  if (ns < 1) ns = 1;
+  *nsplit_out = (int)ns;
+  *waves_out = nw;
+  return 0;
+}

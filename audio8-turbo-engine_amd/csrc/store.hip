@@ -1,0 +1,132 @@
+// Fused qkv bias + rotate_half RoPE + K/V store (a8_bias_rope_store).
+//
+// Semantics follow serve/fast_kernels.py:139-187 (_bias_rope_store_kernel / bias_rope_store):
+// per token row r and head h of the fused [q | k | v] row,
+//   x  = f32(qkv[r, h*64 + d]) + f32(bias[h*64 + d])
+//   q/k: o[d] = bf16(x[d]*cos[pos, d] + sign(d) * x[(d+32) % 64] * sin[pos, d]),  sign = -1 for d < 32
+//   v:   o[d] = bf16(x[d])
+// q goes to qo[r, h]; k / v go to kc / vc[slot[r], h', pos[r] % ring].
+//
+// MI355X layout: one thread owns the partner pair of 16-byte chunks (d = 8c..8c+7 and 32+8c..)
+// of one head, so rotate_half needs no cross-lane traffic and every global access is a 128-bit
+// load/store; 4 consecutive lanes cover one 128-byte head row. The work is ~1 MB per layer at 192
+// slots: the kernel is launch-latency bound and sized as a single flat grid.
+#include "a8_common.h"
+
+namespace a8 {
+
+__global__ __launch_bounds__(256) void k_bias_rope_store(
+    const uint16_t *__restrict__ qkv, int64_t s_qkv, const uint16_t *__restrict__ bias,
+    const uint16_t *__restrict__ cos_tab, const uint16_t *__restrict__ sin_tab, int64_t s_cs, int n_tab,
+    const int32_t *__restrict__ pos, const int32_t *__restrict__ slot, int R,
+    uint16_t *__restrict__ qo, int64_t s_qo_r, int64_t s_qo_h,
+    uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+    int cache_rows, int cache_len, int nq, int nkv, int ring) {
+#pragma clang fp contract(off)
+  const int H = nq + 2 * nkv;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)R * H * 4) return;
+  const int r = (int)(t / (H * 4));
+  const int rem = (int)(t - (int64_t)r * H * 4);
+  const int h = rem >> 2, c = rem & 3;
+
+  const int p = pos[r];
+  if (p < 0 || p >= n_tab) return;  // position outside the RoPE tables: the row writes nothing
+  const int64_t sl = slot[r];
+  const int sidx = p % ring;
+  const bool store_ok = sl >= 0 && sl < cache_rows && sidx < cache_len;
+
+  const uint16_t *src = qkv + (int64_t)r * s_qkv + h * 64;
+  const u32x4 wlo = ld16(src + 8 * c), whi = ld16(src + 32 + 8 * c);
+  float xl[8], xh[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    xl[2 * e] = bf_lo(wlo[e]); xl[2 * e + 1] = bf_hi(wlo[e]);
+    xh[2 * e] = bf_lo(whi[e]); xh[2 * e + 1] = bf_hi(whi[e]);
+  }
+  if (bias) {
+    const u32x4 blo = ld16(bias + h * 64 + 8 * c), bhi = ld16(bias + h * 64 + 32 + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xl[2 * e] += bf_lo(blo[e]); xl[2 * e + 1] += bf_hi(blo[e]);
+      xh[2 * e] += bf_lo(bhi[e]); xh[2 * e + 1] += bf_hi(bhi[e]);
+    }
+  }
+
+  u32x4 olo, ohi;
+  if (h >= nq + nkv) {  // v head: bias only
+    if (!store_ok) return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      olo[e] = f2bf_rne(xl[2 * e]) | (f2bf_rne(xl[2 * e + 1]) << 16);
+      ohi[e] = f2bf_rne(xh[2 * e]) | (f2bf_rne(xh[2 * e + 1]) << 16);
+    }
+    uint16_t *dst = vc + sl * s_kb + (int64_t)(h - nq - nkv) * s_kh + (int64_t)sidx * s_ks;
+    st16(dst + 8 * c, olo);
+    st16(dst + 32 + 8 * c, ohi);
+    return;
+  }
+
+  const uint16_t *crow = cos_tab + (int64_t)p * s_cs, *srow = sin_tab + (int64_t)p * s_cs;
+  const u32x4 clo = ld16(crow + 8 * c), chi = ld16(crow + 32 + 8 * c);
+  const u32x4 slo = ld16(srow + 8 * c), shi = ld16(srow + 32 + 8 * c);
+  float ol[8], oh[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int j = 2 * e + k;
+      const float cl = k ? bf_hi(clo[e]) : bf_lo(clo[e]), ch = k ? bf_hi(chi[e]) : bf_lo(chi[e]);
+      const float sn_l = k ? bf_hi(slo[e]) : bf_lo(slo[e]), sn_h = k ? bf_hi(shi[e]) : bf_lo(shi[e]);
+      // d < 32: partner x[d+32] with sign -1; d >= 32: partner x[d-32] with sign +1.
+      // Two roundings for the products, one for the sum (contraction is off in this function).
+      ol[j] = xl[j] * cl + (-xh[j]) * sn_l;
+      oh[j] = xh[j] * ch + xl[j] * sn_h;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    olo[e] = f2bf_rne(ol[2 * e]) | (f2bf_rne(ol[2 * e + 1]) << 16);
+    ohi[e] = f2bf_rne(oh[2 * e]) | (f2bf_rne(oh[2 * e + 1]) << 16);
+  }
+  uint16_t *dst;
+  if (h < nq) {
+    dst = qo + (int64_t)r * s_qo_r + (int64_t)h * s_qo_h;
+  } else {
+    if (!store_ok) return;
+    dst = kc + sl * s_kb + (int64_t)(h - nq) * s_kh + (int64_t)sidx * s_ks;
+  }
+  st16(dst + 8 * c, olo);
+  st16(dst + 32 + 8 * c, ohi);
+}
+
+static inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace a8
+
+extern "C" int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bias,
+                                  const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab,
+                                  const int32_t *pos, const int32_t *slot, int R,
+                                  void *qo, int64_t s_qo_r, int64_t s_qo_h,
+                                  void *kc, void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                                  int cache_rows, int cache_len,
+                                  int nq, int nkv, int hd, int ring, void *stream) {
+  using namespace a8;
+  if (hd != 64) return set_error(A8_EUNSUP, "bias_rope_store: head_dim %d not supported (64 only)", hd);
+  if (R < 0 || nq <= 0 || nkv <= 0 || ring <= 0 || n_tab < 0 || cache_rows < 0 || cache_len < 0)
+    return set_error(A8_EINVAL, "bias_rope_store: bad sizes R=%d nq=%d nkv=%d ring=%d n_tab=%d", R, nq, nkv,
+                     ring, n_tab);
+  if (R == 0) return 0;
+  if (!qkv || !cos_tab || !sin_tab || !pos || !slot || !qo || !kc || !vc)
+    return set_error(A8_EINVAL, "bias_rope_store: null pointer");
+  if (!al16(qkv) || !al16(cos_tab) || !al16(sin_tab) || !al16(qo) || !al16(kc) || !al16(vc) ||
+      (bias && !al16(bias)) || (s_qkv | s_cs | s_qo_r | s_qo_h | s_kb | s_kh | s_ks) & 7)
+    return set_error(A8_EALIGN, "bias_rope_store: pointers must be 16-byte aligned and strides multiples of 8");
+  const int64_t threads = (int64_t)R * (nq + 2 * nkv) * 4;
+  const unsigned grid = (unsigned)((threads + 255) / 256);
+  hipLaunchKernelGGL(k_bias_rope_store, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t *)qkv, s_qkv, (const uint16_t *)bias, (const uint16_t *)cos_tab,
+                     (const uint16_t *)sin_tab, s_cs, n_tab, pos, slot, R, (uint16_t *)qo, s_qo_r, s_qo_h,
+                     (uint16_t *)kc, (uint16_t *)vc, s_kb, s_kh, s_ks, cache_rows, cache_len, nq, nkv, ring);
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,236 @@
+"""The engine's attention operators on MI355X: drop-ins for the attention part of the reference's
+operator module (serve/fast_kernels.py of lvt1693/audio8-turbo-engine), with the same names,
+signatures, argument meaning, tensor layouts and error behaviour.
+
+    bias_rope_store(...)                    fast_kernels.py:179-187   (kernel 139-176)
+    DecodeAttention(...) / __call__(...)    fast_kernels.py:256-290   (kernels 193-253)
+    PrefillPlan(...)                        fast_kernels.py:335-347
+    prefill_attention(...)                  fast_kernels.py:350-358   (kernel 296-332)
+
+Every call validates dtypes, devices and strides on the host, then enqueues hand-written gfx950 HIP
+kernels on torch's current stream through the C ABI of liba8attn.so (include/a8attn.h). Nothing is
+allocated or synchronised inside a call, so a sequence of calls can be captured into a HIP graph
+(torch.cuda.graph) and replayed. There is no CPU or framework fallback: if the library is missing
+or a launch fails, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_BF16 = torch.bfloat16
+_I32 = torch.int32
+
+
+def _need(cond: bool, msg: str, exc=ValueError):
+    if not cond:
+        raise exc(msg)
+
+
+def _check_bf16(name: str, t: torch.Tensor, dims: int):
+    _need(isinstance(t, torch.Tensor), f"{name} must be a tensor", TypeError)
+    _need(t.dtype == _BF16, f"{name} must be bfloat16 (got {t.dtype})", TypeError)
+    _need(t.dim() == dims, f"{name} must have {dims} dims (got shape {tuple(t.shape)})")
+    _need(t.stride(-1) == 1 or t.shape[-1] == 1, f"{name}: the last dim must be contiguous")
+
+
+def _check_i32(name: str, t: torch.Tensor, n: int):
+    _need(isinstance(t, torch.Tensor), f"{name} must be a tensor", TypeError)
+    _need(t.dtype == _I32, f"{name} must be int32 (got {t.dtype})", TypeError)
+    _need(t.dim() == 1 and t.is_contiguous(), f"{name} must be a contiguous 1-D tensor")
+    _need(t.shape[0] >= n, f"{name} has {t.shape[0]} entries, {n} needed")
+
+
+def _check_device(**tensors):
+    """Every tensor on one HIP device (the kernels dereference all of them there)."""
+    devs = {t.device for t in tensors.values() if t is not None}
+    for name, t in tensors.items():
+        _need(t is None or t.is_cuda, f"{name} must be on a HIP device (got {t.device if t is not None else None})")
+    _need(len(devs) == 1, f"all tensors must be on one device (got {sorted(map(str, devs))})")
+
+
+def _check_cache(kc: torch.Tensor, vc: torch.Tensor, nkv: int, hd: int):
+    _check_bf16("kc", kc, 4)
+    _check_bf16("vc", vc, 4)
+    _need(kc.shape == vc.shape, f"kc {tuple(kc.shape)} and vc {tuple(vc.shape)} must have the same shape")
+    # the reference kernels address vc with kc's strides (fast_kernels.py:170, 186, 224-225)
+    _need(kc.stride() == vc.stride(), f"kc and vc must share strides ({kc.stride()} vs {vc.stride()})")
+    _need(kc.shape[1] == nkv and kc.shape[3] == hd,
+          f"cache shape {tuple(kc.shape)} does not match [rows, {nkv}, S, {hd}]")
+
+
+def bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv, hd, ring=1 << 30):
+    """qkv: [R, (nq+2nkv)*hd]; bias: [(nq+2nkv)*hd] or None. Writes rotated q to qo [R, nq, hd] and k / v
+    into kc / vc [Bslots, nkv, S, hd] at [slot, :, pos % ring] (fast_kernels.py:179-187).
+
+    Per row r, head h: x = f32(qkv) + f32(bias); q / k get rotate_half RoPE from the bf16 cos / sin tables
+    in fp32 and are rounded once to bf16; v is rounded from x. Rows whose position is outside the tables, or
+    whose slot / position is outside the cache, store nothing (the reference leaves that undefined)."""
+    R = qkv.shape[0]
+    width = (nq + 2 * nkv) * hd
+    _check_bf16("qkv", qkv, 2)
+    _need(qkv.shape[1] >= width, f"qkv has {qkv.shape[1]} columns, {width} needed")
+    if bias is not None:
+        _check_bf16("bias", bias, 1)
+        _need(bias.shape[0] >= width, f"bias has {bias.shape[0]} entries, {width} needed")
+    _check_bf16("cos_tab", cos_tab, 2)
+    _check_bf16("sin_tab", sin_tab, 2)
+    _need(cos_tab.shape == sin_tab.shape and cos_tab.stride() == sin_tab.stride(),
+          "cos_tab and sin_tab must have the same shape and strides")
+    _need(cos_tab.shape[1] >= hd, f"RoPE tables have {cos_tab.shape[1]} columns, {hd} needed")
+    _check_i32("pos", pos, R)
+    _check_i32("slot", slot, R)
+    _check_bf16("qo", qo, 3)
+    _need(qo.shape[0] >= R and qo.shape[1] == nq and qo.shape[2] == hd,
+          f"qo shape {tuple(qo.shape)} does not match [{R}, {nq}, {hd}]")
+    _check_cache(kc, vc, nkv, hd)
+    _need(isinstance(ring, int) and 1 <= ring < 2 ** 31, f"ring must be an int in [1, 2^31) (got {ring})")
+    _check_device(qkv=qkv, bias=bias, cos_tab=cos_tab, sin_tab=sin_tab, pos=pos, slot=slot, qo=qo, kc=kc, vc=vc)
+    if R == 0:
+        return qo
+    lib = _lib.load()
+    st = lib.a8_bias_rope_store(
+        qkv.data_ptr(), qkv.stride(0), bias.data_ptr() if bias is not None else None,
+        cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.stride(0), cos_tab.shape[0],
+        pos.data_ptr(), slot.data_ptr(), R,
+        qo.data_ptr(), qo.stride(0), qo.stride(1),
+        kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
+        nq, nkv, hd, ring, _lib.stream_of(qkv))
+    _lib.check(st, "bias_rope_store")
+    return qo
+
+
+def _next_pow2(x: int) -> int:
+    return 1 << max(0, (int(x) - 1).bit_length())
+
+
+class DecodeAttention:
+    """Workspace-owning split-K decode attention. The scratch buffers are flat and sized in
+    (query row x split) units, so one instance serves both decode (few rows, many splits) and
+    packed rows (many rows, one split) with fixed addresses for graph capture
+    (fast_kernels.py:256-269).
+
+    Launch shape: the reference's `nsplit` argument is honoured as a lower bound on the number of key
+    splits; the split count and the wavefronts per split are chosen for the GPU's compute-unit count by
+    a8_decode_choose (policy "auto"). policy = "caller" uses exactly the caller's nsplit. Split
+    boundaries are not part of the contract: every choice computes the same softmax."""
+
+    def __init__(self, cap_row_splits, nq, nkv, hd, nsplit_max, device, scale=None):
+        self.nq, self.nkv, self.hd = nq, nkv, hd
+        self.group = nq // nkv
+        self.gp = max(16, _next_pow2(self.group))
+        self.nsplit_max = int(nsplit_max)
+        self.cap = int(cap_row_splits)
+        self.scale = scale if scale is not None else hd ** -0.5
+        self.acc_flat = torch.empty(self.cap * nq * hd, dtype=torch.float32, device=device)
+        self.ml_flat = torch.empty(self.cap * nq * 2, dtype=torch.float32, device=device)
+        dev = torch.device(device)
+        self.n_cu = torch.cuda.get_device_properties(dev).multi_processor_count if dev.type == "cuda" else 1
+        self.policy = "auto"
+        self.force_shape = None  # (nsplit, waves) pins the launch shape (tuning / tests)
+        self._shapes = {}
+
+    def launch_shape(self, b: int, cache_len: int, nsplit: int):
+        """(key splits, wavefronts per split) for b rows over a cache of cache_len positions."""
+        if self.force_shape is not None:
+            ns, nw = self.force_shape
+            return max(1, min(int(ns), self.cap // max(b, 1))), int(nw)
+        key = (b, cache_len, nsplit, self.policy)
+        hit = self._shapes.get(key)
+        if hit is not None:
+            return hit
+        ns, nw = ctypes.c_int(0), ctypes.c_int(0)
+        nmax = nsplit if self.policy == "caller" else self.nsplit_max
+        st = _lib.load().a8_decode_choose(b, self.nkv, cache_len, nsplit, nmax, self.cap, self.n_cu,
+                                          ctypes.byref(ns), ctypes.byref(nw))
+        _lib.check(st, "decode_choose")
+        self._shapes[key] = (ns.value, nw.value)
+        return self._shapes[key]
+
+    def __call__(self, q, kc, vc, lens, out, nsplit=1, bn=64, rowmap=None, phases=3):
+        """q: [b, nq, hd]; kc/vc: [rows, nkv, S, hd]; query row i reads cache row rowmap[i]
+        (identity when rowmap is None); lens: [b] int32 (keys [0, lens) attended); out: [b, nq, hd]
+        (fast_kernels.py:271-290). `phases` (1 = split kernel, 2 = combine kernel, 3 = both) exists
+        so a profiler can time the two kernels apart; callers leave it at 3."""
+        b = q.shape[0]
+        nsplit = max(1, min(int(nsplit), self.nsplit_max))
+        assert b * nsplit <= self.cap, (b, nsplit, self.cap)
+        _need(bn == 64, f"bn={bn}: only 64-key tiles are implemented", NotImplementedError)
+        _need(q.dtype == _BF16, f"q must be bfloat16 (got {q.dtype}); fp32 queries are not implemented",
+              NotImplementedError if q.dtype == torch.float32 else TypeError)
+        _check_bf16("q", q, 3)
+        _need(q.shape[1] == self.nq and q.shape[2] == self.hd,
+              f"q shape {tuple(q.shape)} does not match [b, {self.nq}, {self.hd}]")
+        _check_cache(kc, vc, self.nkv, self.hd)
+        _check_i32("lens", lens, b)
+        if rowmap is not None:
+            _check_i32("rowmap", rowmap, b)
+        _check_bf16("out", out, 3)
+        _need(out.shape[0] >= b and out.shape[1] == self.nq and out.shape[2] == self.hd,
+              f"out shape {tuple(out.shape)} does not match [{b}, {self.nq}, {self.hd}]")
+        _check_device(q=q, kc=kc, vc=vc, lens=lens, rowmap=rowmap, out=out, workspace=self.acc_flat)
+        if b == 0:
+            return out
+        ns, nw = self.launch_shape(b, kc.shape[2], nsplit)
+        st = _lib.load().a8_decode_attn(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
+            lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap,
+            b, self.nq, self.nkv, self.hd, ns, nw, float(self.scale), int(phases), _lib.stream_of(q))
+        _lib.check(st, "decode_attention")
+        return out
+
+
+class PrefillPlan:
+    """Query-block schedule for a packed prefill: request i's rows [r0_i, r0_i+n_i) sit at
+    positions [p0_i, p0_i+n_i) of cache row slot_i (keys [0, p0_i) are an already-stored prefix)
+    (fast_kernels.py:335-347)."""
+    BM = 64
+
+    def __init__(self, r0s, ns, slots, p0s, device):
+        q0, cnt, sl, ps = [], [], [], []
+        for r0, n, s, p0 in zip(r0s, ns, slots, p0s):
+            for off in range(0, n, self.BM):
+                q0.append(r0 + off)
+                cnt.append(min(self.BM, n - off))
+                sl.append(s)
+                ps.append(p0 + off)
+        t = torch.tensor([q0, cnt, sl, ps], dtype=torch.int32)
+        if torch.device(device).type == "cuda":
+            t = t.pin_memory().to(device, non_blocking=True)
+        self.q0, self.n, self.slot, self.pos0 = t[0], t[1], t[2], t[3]
+        self.nblk = len(q0)
+
+
+def prefill_attention(q, kc, vc, plan, out, group, scale=None):
+    """q/out: [R, nq, hd] packed rows; kc/vc: [rows, nkv, S, hd] (fast_kernels.py:350-358).
+    `plan` is a PrefillPlan or any object with int32 device tensors q0, n, slot, pos0, an int nblk and
+    BM = 64 (the graph-mode plan of fast_engine.py:825-826)."""
+    _check_bf16("q", q, 3)
+    nq, hd = q.shape[1], q.shape[2]
+    scale = scale if scale is not None else hd ** -0.5
+    _need(group >= 1 and nq % group == 0, f"group {group} does not divide nq {nq}")
+    _check_cache(kc, vc, nq // group, hd)
+    _check_bf16("out", out, 3)
+    _need(out.shape[0] >= q.shape[0] and out.shape[1:] == q.shape[1:],
+          f"out shape {tuple(out.shape)} does not match q {tuple(q.shape)}")
+    bm = int(getattr(plan, "BM", PrefillPlan.BM))
+    nblk = int(plan.nblk)
+    for name in ("q0", "n", "slot", "pos0"):
+        _check_i32(f"plan.{name}", getattr(plan, name), nblk)
+    _check_device(q=q, kc=kc, vc=vc, out=out, **{f"plan.{k}": getattr(plan, k) for k in ("q0", "n", "slot", "pos0")})
+    if nblk == 0 or q.shape[0] == 0:
+        return out
+    st = _lib.load().a8_prefill_attn(
+        q.data_ptr(), q.stride(0), q.stride(1), q.shape[0],
+        kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
+        out.data_ptr(), out.stride(0), out.stride(1),
+        plan.q0.data_ptr(), plan.n.data_ptr(), plan.slot.data_ptr(), plan.pos0.data_ptr(), nblk, bm,
+        nq, group, hd, float(scale), _lib.stream_of(q))
+    _lib.check(st, "prefill_attention")
+    return out

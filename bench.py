@@ -1,0 +1,198 @@
+"""Benchmark of the MI355X attention hot path: BASELINE.json's metric on its peak-load config.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu-baseline]
+
+A step is one decode tick of the slow AR's attention: 24 layers x (bias_rope_store -> split-K decode
+attention) over 192 slots at KV length 2048 (config 3), captured once as a HIP graph and replayed. Inputs
+(per-layer fused qkv rows, biases, 24 distinct layer caches = 4.5 GiB, so no layer's KV is served from the
+256 MB MALL on the next replay) are resident in HBM before the timed region.
+
+Prints ONE JSON line: value = algorithmic HBM bytes of the tick / tick time (GB/s), plus µs per layer, the
+roofline of the dominant kernel (the decode kernel, timed live with HIP events on its stream over a graph of
+24 decode launches) and the CPU baseline (the CPU oracle on a bounded sample of the same workload).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode-attn µs/layer + achieved HBM GB/s (% peak) at 192 slots, KV 2048"
+HBM_PEAK_GBS = 8000.0
+NQ, NKV, HD, LAYERS = 14, 2, 64, 24
+W = (NQ + 2 * NKV) * HD
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--config", default="C3", choices=["C2", "C3"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
+    p.add_argument("--shape", default=None, help="force the decode launch shape as NSPLIT,WAVES")
+    return p.parse_args()
+
+
+def build_workload(a8, torch, cfg, dev, seed=0):
+    """Per-layer inputs and caches of config 3 (or config 2) on the device."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    if cfg == "C3":
+        b, S = 192, 2048
+        lens = torch.full((b,), 2048, dtype=torch.int32)
+    else:
+        b, S = 64, 4096
+        lens = torch.randint(128, 2049, (b,), generator=torch.Generator().manual_seed(seed), dtype=torch.int32)
+    st = a8.AttnStack(LAYERS, NQ, NKV, HD, 10000.0, max_rows=max(16 * b, 8192), cache_rows=b + 1, cache_len=S,
+                      max_pos=S, dev=dev)
+    for i in range(LAYERS):
+        st.kc[i].normal_(generator=g)
+        st.vc[i].normal_(generator=g)
+    pos = (lens - 1).to(dev)
+    slot = torch.arange(b, dtype=torch.int32, device=dev)
+    qkv = [torch.randn(b, W, generator=g, device=dev).to(torch.bfloat16) for _ in range(LAYERS)]
+    bias = [(torch.randn(W, generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(LAYERS)]
+    q = torch.empty(b, NQ, HD, dtype=torch.bfloat16, device=dev)
+    outs = [torch.empty(b, NQ, HD, dtype=torch.bfloat16, device=dev) for _ in range(LAYERS)]
+    return dict(st=st, b=b, S=S, lens_h=lens, lens=lens.to(dev), pos=pos, slot=slot, qkv=qkv, bias=bias, q=q,
+                outs=outs)
+
+
+def capture(torch, fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, steps, warmup):
+    """ms per replay: warmup replays, then `steps` replays between two events on the launching stream."""
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def cpu_baseline(w, budget_s):
+    """The CPU oracle (torch on the host cores) on one layer of the same workload: store + decode for all
+    slots, repeated until the budget is spent (at least 3 reps); median per layer."""
+    import torch
+    from oracle import attn_ref as ref
+
+    torch.set_num_threads(torch.get_num_threads())
+    st = w["st"]
+    b, S = w["b"], w["S"]
+    kc, vc = st.kc[0].cpu(), st.vc[0].cpu()
+    qkv, bias = w["qkv"][0].cpu(), w["bias"][0].cpu()
+    pos, slot, lens = w["pos"].cpu(), w["slot"].cpu(), w["lens"].cpu()
+    cos, sin = ref.rope_tables(10000.0, HD, S)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        q = torch.empty(b, NQ, HD, dtype=torch.bfloat16)
+        t0 = time.perf_counter()
+        ref.bias_rope_store(qkv, bias, cos, sin, pos, slot, q, kc, vc, NQ, NKV, HD)
+        ref.decode_attention(q, kc, vc, lens, nsplit=1)
+        times.append(time.perf_counter() - t0)
+    per_layer = statistics.median(times)
+    nbytes = ref.decode_bytes(w["lens_h"].tolist(), NQ, NKV, HD)
+    return {"value": round(nbytes / per_layer / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "us_per_layer": round(per_layer * 1e6, 1),
+            "sample": f"1 of {LAYERS} layers (store + decode, {b} slots, same inputs), {len(times)} reps, median"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}). Each GPU "
+              "serves its own slots with no exchange, so N GPUs give N times the one-GPU value.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import __graft_entry__
+    __graft_entry__.ensure_built()
+    a8 = __graft_entry__.load_package()
+    from oracle import attn_ref as ref_counts  # byte counts only (the timed GPU path never touches it)
+
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    w = build_workload(a8, torch, args.config, dev)
+    st, b = w["st"], w["b"]
+    if args.shape:
+        st.attn.force_shape = tuple(int(x) for x in args.shape.split(","))
+    nsplit_req = a8.ref_nsplit(b, NKV)
+    ns, nw = st.attn.launch_shape(b, w["S"], nsplit_req)
+
+    def tick():
+        st.forward(w["qkv"], w["bias"], w["pos"], w["slot"], w["lens"], nsplit=nsplit_req, rowmap=False, q=w["q"],
+                   outs=w["outs"])
+
+    def decode_only():
+        for i in range(LAYERS):
+            st.attn(w["q"], st.kc[i], st.vc[i], w["lens"], w["outs"][i], nsplit=nsplit_req)
+
+    def store_only():
+        for i in range(LAYERS):
+            a8.bias_rope_store(w["qkv"][i], w["bias"][i], st.cos, st.sin, w["pos"], w["slot"], w["q"], st.kc[i],
+                               st.vc[i], NQ, NKV, HD)
+
+    g_tick = capture(torch, tick)
+    ms = time_graph(torch, g_tick, args.steps, args.warmup)
+    g_dec = capture(torch, decode_only)
+    ms_dec = time_graph(torch, g_dec, args.steps, args.warmup)
+    g_sto = capture(torch, store_only)
+    ms_sto = time_graph(torch, g_sto, args.steps, args.warmup)
+
+    lens = w["lens_h"].tolist()
+    layer_bytes = ref_counts.decode_bytes(lens, NQ, NKV, HD)                  # store + decode, algorithmic
+    dec_bytes = ref_counts.decode_bytes(lens, NQ, NKV, HD, with_store=False)  # K+V read + q in + out
+    us_layer = ms * 1e3 / LAYERS
+    gbs = layer_bytes * LAYERS / (ms * 1e-3) / 1e9
+    dec_us = ms_dec * 1e3 / LAYERS
+    dec_gbs = dec_bytes / (dec_us * 1e-6) / 1e9
+    line = {
+        "metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"{args.config}: {b} slots x KV {max(lens)}" + (" (U[128,2048])" if args.config == "C2"
+                   else "") + f", GQA {NQ}/{NKV} hd {HD}, {LAYERS} layers x (bias_rope_store + split-K decode) "
+                   "as one HIP graph tick", "slots": b, "kv_len": max(lens), "cache_len": w["S"], "layers": LAYERS,
+                   "decode_launch": {"nsplit": ns, "waves": nw}},
+        "us_per_layer": round(us_layer, 3),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "decode_us_per_layer": round(dec_us, 3),
+        "store_us_per_layer": round(ms_sto * 1e3 / LAYERS, 3),
+        "roofline": {"bound": "hbm", "kernel": "k_decode_split" + ("" if ns == 1 else " + k_decode_combine"),
+                     "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": dec_bytes, "us_per_launch": round(dec_us, 3)},
+        "device": {"name": props.name, "arch": getattr(props, "gcnArchName", ""), "cus": props.multi_processor_count},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,139 @@
+/*
+ * a8attn.h -- C ABI of the MI355X (gfx950) attention hot path of the Audio8 streaming TTS engine.
+ *
+ * Three operators, each a drop-in for one function of the reference's operator module
+ * (serve/fast_kernels.py of lvt1693/audio8-turbo-engine):
+ *
+ *   a8_bias_rope_store   fused qkv bias + rotate_half RoPE + K/V store into the slot cache
+ *   a8_decode_attn       split-K flash-decoding over the slot cache (GQA), split + combine
+ *   a8_prefill_attn      packed variable-length causal prefill attention over cache rows
+ *
+ * Conventions shared by every entry point:
+ *   - All tensors are bf16 (stored as 16-bit words) unless the argument says otherwise; index
+ *     tensors are int32. Every pointer is a device pointer (hipMalloc'ed or a view into one).
+ *   - Strides are in ELEMENTS, as torch reports them. The last (head_dim) axis is contiguous.
+ *   - The slot cache is [cache_rows, nkv, cache_len, hd] with strides (s_kb, s_kh, s_ks, 1); K and
+ *     V caches share strides (the reference kernels address both with the K strides). Row strides
+ *     may be non-dense (the codec's byte-arena views).
+ *   - Vector loads are 16 bytes wide: base pointers must be 16-byte aligned and every stride a
+ *     multiple of 8 elements. Violations return A8_EALIGN without launching anything.
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream). Entry points only
+ *     enqueue work: no allocation, no synchronisation, so they are safe under stream capture.
+ *   - Return value: 0 on success, a negative A8_E* code for a rejected argument (nothing launched;
+ *     a8_last_error() has the message), or a positive hipError_t from the launch.
+ *   - Device-side index data the host cannot see (pos, slot, lens, rowmap, plan entries) is
+ *     bounds-checked in the kernels: a row whose slot / cache row lies outside [0, cache_rows),
+ *     or whose position lies outside the cos/sin table or the cache, writes nothing instead of
+ *     writing out of bounds (the reference leaves those cases undefined).
+ */
+#ifndef A8ATTN_H
+#define A8ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define A8_EINVAL  (-1) /* shape / count argument out of range */
+#define A8_EALIGN  (-2) /* pointer or stride not 16-byte aligned */
+#define A8_EUNSUP  (-3) /* configuration this build does not implement (e.g. head_dim != 64) */
+#define A8_EWSPACE (-4) /* decode workspace too small for b * nsplit row-splits */
+
+/* Library version string, e.g. "a8attn 0.1.0 gfx950". No reference counterpart. */
+const char *a8_version(void);
+
+/* Message for the last negative status returned on the calling thread ("" if none). */
+const char *a8_last_error(void);
+
+/* File name of the HIP runtime this library is bound to (dladdr of hipLaunchKernel). Lets a
+ * Python host check that it shares torch's runtime (same soname, loaded once). */
+const char *a8_hip_runtime_path(void);
+
+/*
+ * Fused qkv bias + rotate_half RoPE + K/V store.
+ * Replaces serve/fast_kernels.py:179-187 (bias_rope_store) and its kernel
+ * _bias_rope_store_kernel (fast_kernels.py:139-176).
+ *
+ * qkv     [R, (nq + 2*nkv) * hd] row stride s_qkv; columns contiguous
+ * bias    [(nq + 2*nkv) * hd] or NULL
+ * cos_tab, sin_tab [n_tab, hd] row stride s_cs (rotate_half tables, see a1 _rope_tables)
+ * pos, slot [R] int32
+ * qo      [R, nq, hd] strides (s_qo_r, s_qo_h, 1)            <- rotated q
+ * kc, vc  slot cache                                         <- rotated k / biased v at
+ *                                                               [slot[r], h, pos[r] % ring, :]
+ * Per row r and head h: x = f32(qkv) + f32(bias); q/k: o = bf16(x*cos + sign*x[(d+hd/2)%hd]*sin)
+ * with sign = -1 for d < hd/2, evaluated without fused multiply-add; v: bf16(x).
+ * hd must be 64.
+ */
+int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bias,
+                       const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab,
+                       const int32_t *pos, const int32_t *slot, int R,
+                       void *qo, int64_t s_qo_r, int64_t s_qo_h,
+                       void *kc, void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                       int cache_rows, int cache_len,
+                       int nq, int nkv, int hd, int ring, void *stream);
+
+/*
+ * Split-K flash-decoding, GQA (group = nq / nkv <= 16), one query token per row.
+ * Replaces serve/fast_kernels.py:271-290 (DecodeAttention.__call__) with its kernels
+ * _dec_attn_split_kernel (193-235) and _dec_attn_combine_kernel (238-253).
+ *
+ * q       [b, nq, hd] strides (s_qb, s_qh, 1)
+ * kc, vc  slot cache; query row i reads cache row rowmap[i] (i when rowmap == NULL)
+ * lens    [b] int32: keys [0, lens[i]) are attended
+ * out     [b, nq, hd] strides (s_ob, s_oh, 1)
+ * acc_ws  fp32 workspace, >= ws_row_splits * nq * hd floats (DecodeAttention.acc_flat)
+ * ml_ws   fp32 workspace, >= ws_row_splits * nq * 2 floats  (DecodeAttention.ml_flat)
+ * nsplit  key-range splits per row (>= 1; b * nsplit <= ws_row_splits). With nsplit == 1 the
+ *         split kernel writes `out` directly and no combine runs.
+ * waves   wavefronts per workgroup that share one split's key range: 1, 2, 4 or 8.
+ * phases  bit 0: run the split kernel, bit 1: run the combine kernel (3 = both; the normal value).
+ *         Running them separately lets a caller time each kernel.
+ * Rows with lens == 0 produce NaN (0/0), exactly as the reference's combine does.
+ */
+int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
+                   const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                   int cache_rows, int cache_len,
+                   const int32_t *lens, const int32_t *rowmap,
+                   void *out, int64_t s_ob, int64_t s_oh,
+                   float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                   int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
+                   int phases, void *stream);
+
+/*
+ * Launch-shape policy for a8_decode_attn on this GPU: picks (nsplit, waves) so that
+ * b * nkv * nsplit workgroups fill n_cu compute units for keys up to cache_len.
+ * nsplit_req is the caller's request (the reference's per-bucket heuristic, fast_engine.py:776):
+ * the result is never below it. The result respects nsplit_max and b * nsplit <= cap_row_splits.
+ * Replaces the nsplit heuristic of serve/fast_engine.py:776, re-derived for 256 CUs.
+ */
+int a8_decode_choose(int b, int nkv, int cache_len, int nsplit_req, int nsplit_max,
+                     int64_t cap_row_splits, int n_cu, int *nsplit_out, int *waves_out);
+
+/*
+ * Packed causal prefill attention over keys already stored in cache rows.
+ * Replaces serve/fast_kernels.py:350-358 (prefill_attention) and its kernel
+ * _prefill_attn_kernel (296-332); the block plan is the reference's PrefillPlan
+ * (fast_kernels.py:335-347) or the graph-mode plan of fast_engine.py:820-853.
+ *
+ * q, out  [R, nq, hd] packed rows, strides (s_qr, s_qh, 1) / (s_or, s_oh, 1)
+ * kc, vc  slot cache
+ * bq0, bn, bslot, bpos0 [nblk] int32: block j covers packed rows [bq0, bq0 + bn) (bn <= bm) at
+ *         positions [bpos0, bpos0 + bn) of cache row bslot; keys [0, bpos0 + bn) are attended with
+ *         key <= query position. Blocks with bn <= 0 are no-ops (graph-mode padding).
+ * group   q heads per kv head (nq / nkv); bm must be 64; hd must be 64.
+ */
+int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
+                    const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                    int cache_rows, int cache_len,
+                    void *out, int64_t s_or, int64_t s_oh,
+                    const int32_t *bq0, const int32_t *bn, const int32_t *bslot,
+                    const int32_t *bpos0, int nblk, int bm,
+                    int nq, int group, int hd, float scale, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* A8ATTN_H */

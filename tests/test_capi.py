@@ -1,0 +1,120 @@
+"""The C-ABI library on the host (no GPU needed): it loads, exports every symbol include/a8attn.h declares,
+rejects bad arguments before launching anything, and its launch-shape policy keeps its contract."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "a8attn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(a8_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    assert set(declared_functions()) == {"a8_version", "a8_last_error", "a8_hip_runtime_path", "a8_bias_rope_store",
+                                         "a8_decode_attn", "a8_decode_choose", "a8_prefill_attn"}
+
+
+def test_library_exports_every_declared_symbol(a8):
+    lib = a8.load_library()
+    raw = ctypes.CDLL(a8.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+    assert lib.a8_version().decode().startswith("a8attn")
+    assert "libamdhip64" in lib.a8_hip_runtime_path().decode()
+    from audio8_turbo_engine_amd import _lib
+    assert set(_lib.SIGNATURES) == set(declared_functions())
+
+
+def _store_args(**kw):
+    a = dict(qkv=16, s_qkv=1152, bias=None, cos=16, sin=16, s_cs=64, n_tab=8, pos=16, slot=16, R=1, qo=16,
+             s_qo_r=896, s_qo_h=64, kc=16, vc=16, s_kb=1024, s_kh=512, s_ks=64, rows=1, S=8, nq=14, nkv=2, hd=64,
+             ring=1 << 30, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_store_rejects_before_launch(a8):
+    lib = a8.load_library()
+    assert lib.a8_bias_rope_store(*_store_args(hd=128)) == -3
+    assert b"head_dim 128" in lib.a8_last_error()
+    assert lib.a8_bias_rope_store(*_store_args(ring=0)) == -1
+    assert lib.a8_bias_rope_store(*_store_args(qkv=24)) == -2          # misaligned pointer
+    assert lib.a8_bias_rope_store(*_store_args(s_qkv=1151)) == -2      # stride not a multiple of 8
+    assert lib.a8_bias_rope_store(*_store_args(qo=None)) == -1
+    assert lib.a8_bias_rope_store(*_store_args(R=0)) == 0              # nothing to do, nothing launched
+
+
+def _decode_args(**kw):
+    a = dict(q=16, s_qb=896, s_qh=64, kc=16, vc=16, s_kb=1024, s_kh=512, s_ks=64, rows=1, S=8, lens=16,
+             rowmap=None, out=16, s_ob=896, s_oh=64, acc=16, ml=16, ws=4, b=1, nq=14, nkv=2, hd=64, nsplit=1,
+             waves=4, scale=0.125, phases=3, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_decode_rejects_before_launch(a8):
+    lib = a8.load_library()
+    assert lib.a8_decode_attn(*_decode_args(hd=128)) == -3
+    assert lib.a8_decode_attn(*_decode_args(nq=34, nkv=2)) == -3        # group 17 > 16
+    assert lib.a8_decode_attn(*_decode_args(nq=15)) == -1               # nq not a multiple of nkv
+    assert lib.a8_decode_attn(*_decode_args(waves=3)) == -1
+    assert lib.a8_decode_attn(*_decode_args(nsplit=0)) == -1
+    assert lib.a8_decode_attn(*_decode_args(b=3, nsplit=2, ws=5)) == -4  # workspace: 6 row-splits needed
+    assert lib.a8_decode_attn(*_decode_args(out=8)) == -2
+    assert lib.a8_decode_attn(*_decode_args(b=0)) == 0
+
+
+def _prefill_args(**kw):
+    a = dict(q=16, s_qr=896, s_qh=64, R=4, kc=16, vc=16, s_kb=1024, s_kh=512, s_ks=64, rows=1, S=8, out=16,
+             s_or=896, s_oh=64, bq0=16, bn=16, bslot=16, bpos0=16, nblk=1, bm=64, nq=14, group=7, hd=64,
+             scale=0.125, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_prefill_rejects_before_launch(a8):
+    lib = a8.load_library()
+    assert lib.a8_prefill_attn(*_prefill_args(bm=32)) == -3
+    assert lib.a8_prefill_attn(*_prefill_args(hd=80)) == -3
+    assert lib.a8_prefill_attn(*_prefill_args(group=5)) == -1
+    assert lib.a8_prefill_attn(*_prefill_args(s_qr=900)) == -2
+    assert lib.a8_prefill_attn(*_prefill_args(nblk=0)) == 0
+
+
+def _choose(lib, b, nkv=2, S=2048, req=1, nmax=16, cap=8192, n_cu=256):
+    ns, nw = ctypes.c_int(), ctypes.c_int()
+    assert lib.a8_decode_choose(b, nkv, S, req, nmax, cap, n_cu, ctypes.byref(ns), ctypes.byref(nw)) == 0
+    return ns.value, nw.value
+
+
+def test_decode_choose_contract(a8):
+    lib = a8.load_library()
+    for b in (1, 2, 4, 16, 64, 128, 192, 384, 1000):
+        for S in (2, 10, 64, 385, 2048, 4096):
+            for req in (1, 3, 16):
+                for nmax in (1, 4, 16):
+                    for cap in (b, 2 * b, 16 * b, 8192):
+                        ns, nw = _choose(lib, b, S=S, req=req, nmax=nmax, cap=cap)
+                        assert ns >= 1 and nw in (1, 2, 4, 8)
+                        assert ns <= nmax and b * ns <= max(cap, b)
+                        assert ns <= max(1, -(-S // 64))            # no more splits than 64-key tiles
+                        if ns < req:                                 # only the caps may cut the request
+                            assert ns in (nmax, cap // b, max(1, -(-S // 64)))
+    # the peak-load config fills the GPU with >= 8 waves per CU
+    ns, nw = _choose(lib, 192)
+    assert 192 * 2 * ns * nw >= 8 * 256
+    # tiny caches: one wave, one split
+    assert _choose(lib, 384, S=10, nmax=1) == (1, 1)
+    with pytest.raises(ctypes.ArgumentError):
+        lib.a8_decode_choose(1, 2, 8, 1, 1, 8, 256, None, "x")
+    assert lib.a8_decode_choose(0, 2, 8, 1, 1, 8, 256, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int())) == -1

@@ -1,0 +1,130 @@
+"""GPU parity of packed causal prefill attention (prefill_attention -> a8_prefill_attn) against the golden
+vectors and the CPU oracle, incl. config 4 at full size (voice-prefix KV copied into the slots, then
+store + prefill) and the graph-mode plan with padding blocks. Bar: max-abs <= 2e-2."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import bf16_from_bits, golden, randn_bf16
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+NQ, NKV, HD = 14, 2, 64
+TOL = 2e-2
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def maxabs(a, b):
+    return (a.float().cpu() - b.float().cpu()).abs().max().item()
+
+
+def test_prefill_golden(a8, dev):
+    say("case: prefill golden")
+    z = golden("prefill.npz")
+    q, kc, vc = bf16_from_bits(z["q"]), bf16_from_bits(z["kc"]), bf16_from_bits(z["vc"])
+    reqs = z["reqs"]
+    ns = [int(n) for _, _, n in reqs]
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    plan = a8.PrefillPlan(r0s, ns, [int(s) for s, _, _ in reqs], [int(p) for _, p, _ in reqs], dev)
+    out = torch.zeros_like(q, device=dev)
+    a8.prefill_attention(q.to(dev), kc.to(dev), vc.to(dev), plan, out, 7)
+    torch.cuda.synchronize()
+    assert maxabs(out, torch.from_numpy(z["out"].astype(np.float32))) <= TOL
+
+
+def _c4(g, n_req=64, lo=40, hi=400, p0=300, voices=4):
+    ns = torch.randint(lo, hi + 1, (n_req,), generator=g).tolist()
+    S = p0 + hi + 4
+    prefix_k = [randn_bf16(g, NKV, p0, HD) for _ in range(voices)]
+    prefix_v = [randn_bf16(g, NKV, p0, HD) for _ in range(voices)]
+    return ns, S, prefix_k, prefix_v
+
+
+def test_prefill_c4_full(a8, ref, dev):
+    """Config 4: 64 requests, n ~ U[40, 400], each after a 300-position voice prefix (4 voices x 16 slots)."""
+    say("case: prefill C4 full size")
+    g = torch.Generator().manual_seed(31)
+    ns, S, pk, pv = _c4(g)
+    p0 = 300
+    nreq = len(ns)
+    rows = nreq + 1
+    W = (NQ + 2 * NKV) * HD
+    R = sum(ns)
+    qkv, bias = randn_bf16(g, R, W), randn_bf16(g, W, std=0.02)
+    cos, sin = ref.rope_tables(10000.0, HD, 2048)
+    pos = torch.cat([p0 + torch.arange(n) for n in ns]).int()
+    slot = torch.cat([torch.full((n,), i) for i, n in enumerate(ns)]).int()
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    # host oracle: prefix copy (voice i % 4), store, prefill
+    kc = torch.zeros(rows, NKV, S, HD, dtype=BF)
+    vc = torch.zeros_like(kc)
+    for i in range(nreq):
+        kc[i, :, :p0], vc[i, :, :p0] = pk[i % 4], pv[i % 4]
+    kcd, vcd = kc.to(dev), vc.to(dev)
+    q_c = torch.empty(R, NQ, HD, dtype=BF)
+    ref.bias_rope_store(qkv, bias, cos, sin, pos, slot, q_c, kc, vc, NQ, NKV, HD)
+    out_c = torch.zeros(R, NQ, HD, dtype=BF)
+    ref.prefill_attention(q_c, kc, vc, *ref.prefill_plan(r0s, ns, list(range(nreq)), [p0] * nreq), out_c, 7)
+    # GPU
+    q_d = torch.empty(R, NQ, HD, dtype=BF, device=dev)
+    a8.bias_rope_store(qkv.to(dev), bias.to(dev), cos.to(dev), sin.to(dev), pos.to(dev), slot.to(dev), q_d, kcd, vcd,
+                       NQ, NKV, HD)
+    plan = a8.PrefillPlan(r0s, ns, list(range(nreq)), [p0] * nreq, dev)
+    out_d = torch.zeros(R, NQ, HD, dtype=BF, device=dev)
+    a8.prefill_attention(q_d, kcd, vcd, plan, out_d, 7)
+    torch.cuda.synchronize()
+    assert torch.equal(q_d.cpu(), q_c) and torch.equal(kcd.cpu(), kc) and torch.equal(vcd.cpu(), vc)
+    err = maxabs(out_d, out_c)
+    say(f"  R={R} blocks={plan.nblk} max-abs {err:.3e}")
+    assert err <= TOL
+
+
+def test_prefill_graph_mode_plan(a8, ref, dev):
+    """The graph-mode plan buffer (padding blocks point at the scratch row with n = 0) gives the same rows as
+    an exact PrefillPlan, and leaves rows past the packed tokens untouched."""
+    say("case: prefill graph-mode plan with padding")
+    g = torch.Generator().manual_seed(32)
+    NT, NR, rows, S = 512, 8, 6, 400
+    SCR = rows - 1
+    slots, ns, starts = [0, 3, 1], [130, 7, 64], [200, 0, 17]
+    nt = 256
+    q = randn_bf16(g, NT, NQ, HD)
+    kc, vc = randn_bf16(g, rows, NKV, S, HD), randn_bf16(g, rows, NKV, S, HD)
+    meta = a8.PrefillMeta(NT, NR, SCR, dev)
+    meta.load(nt, slots, ns, starts)
+    sentinel = torch.full((NT, NQ, HD), 7.0, dtype=BF, device=dev)
+    out = sentinel.clone()
+    a8.prefill_attention(q.to(dev)[:nt], kc.to(dev), vc.to(dev), meta.plan(nt), out[:nt], 7)
+    torch.cuda.synchronize()
+    r0s = [0, 130, 137]
+    want = torch.zeros(NT, NQ, HD, dtype=BF)
+    ref.prefill_attention(q, kc, vc, *ref.prefill_plan(r0s, ns, slots, starts), want, 7)
+    R = sum(ns)
+    assert maxabs(out[:R], want[:R]) <= TOL
+    assert torch.equal(out[R:].cpu(), sentinel[R:].cpu())
+
+
+def test_prefill_rows_match_decode(a8, dev):
+    """HIP prefill row j == HIP decode with lens = p0 + j + 1 on the same cache row (two independent kernels)."""
+    say("case: prefill vs decode cross-check")
+    g = torch.Generator().manual_seed(33)
+    rows, S = 3, 512
+    kc, vc = randn_bf16(g, rows, NKV, S, HD).to(dev), randn_bf16(g, rows, NKV, S, HD).to(dev)
+    ns, p0s, slots = [150, 64, 1], [300, 0, 511], [2, 0, 1]
+    r0s = [0, 150, 214]
+    R = sum(ns)
+    q = randn_bf16(g, R, NQ, HD).to(dev)
+    out = torch.zeros(R, NQ, HD, dtype=BF, device=dev)
+    a8.prefill_attention(q, kc, vc, a8.PrefillPlan(r0s, ns, slots, p0s, dev), out, 7)
+    lens = torch.tensor([p0 + j + 1 for n, p0 in zip(ns, p0s) for j in range(n)], dtype=torch.int32, device=dev)
+    rowmap = torch.tensor([s for n, s in zip(ns, slots) for _ in range(n)], dtype=torch.int32, device=dev)
+    att = a8.DecodeAttention(16 * R, NQ, NKV, HD, 16, dev)
+    dec = torch.empty_like(out)
+    att(q, kc, vc, lens, dec, nsplit=2, rowmap=rowmap)
+    torch.cuda.synchronize()
+    assert maxabs(out, dec) <= TOL
