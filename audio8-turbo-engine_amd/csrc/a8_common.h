@@ -43,6 +43,23 @@ __device__ __forceinline__ void st8(void *p, u32x2 v) { *reinterpret_cast<u32x2 
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// Raw buffer resource over [base, base + bytes): loads at byte offsets >= bytes return zeros without
+// touching memory (the descriptor's range check), which is how the kernels mask key rows past a range
+// and prefetch past its end. Word 3 = 0x00020000 is the gfx9-family raw-buffer format.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+// 4-byte vector-memory load at byte offset `off`. Unlike a scalar load of a uniform address, it is
+// counted with the tile loads (vmcnt), so waiting for it never waits for the LDS traffic or vice versa.
+__device__ __forceinline__ int bld4(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+// 16-byte load at byte offset `off` (the whole offset in the VGPR operand, so the range check sees it).
+__device__ __forceinline__ u32x4 bld16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 // D = A(16x32) * B(32x16) + C, bf16 in, fp32 accumulate. Lane l supplies A[l%16][8*(l/16)+j] and
 // B[8*(l/16)+j][l%16] (j = 0..7) and receives D[4*(l/16)+i][l%16] (i = 0..3). Only the pairing of A
 // and B slots matters for the sum over k, so callers may map any 32 reduction indices onto the

@@ -20,16 +20,17 @@
 //     from where O^T += V^T . P^T reads 128-bit MFMA operands.
 //   * Softmax statistics live per lane (column = q head); the max is reduced across the four
 //     16-lane groups with cross-lane shuffles, the row sum is kept per lane group and reduced once.
-//   * Exponentials are exp2 on pre-scaled scores (scale * log2 e folded into one multiply); m is
-//     kept in the same log2 units in the workspace, which only this file's kernels read.
-#include "a8_common.h"
+//   * The tile machinery (loads, both products, online softmax) is in decode_tile.h. The running max
+//     m is kept in raw score units (q.k) in the workspace, which only the decode kernels read; every
+//     exponential is exp2((s - m) * scale * log2 e).
+// This split + combine pair serves any nsplit the caller asks for; the default launch path is the
+// streaming kernel of decode_stream.hip.
+#include "decode_tile.h"
 
 namespace a8 {
 
-constexpr int kVRow = 72;  // LDS row of a transposed V tile: 64 keys + 8 pad (144 B, 16-B aligned)
-
 template <int NW>
-__global__ __launch_bounds__(64 * NW) void k_decode_split(
+__global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     const uint16_t *__restrict__ q, int64_t s_qb, int64_t s_qh,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
     int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
@@ -48,99 +49,45 @@ __global__ __launch_bounds__(64 * NW) void k_decode_split(
   const int lo = sp * per;
   const int hi = min(lo + per, L);
 
-  // B operand of S^T = K.Q^T: column r16 = q head kh*group + r16, reduction slot (g, j) = dim 8g+j
-  // (first MFMA) and 32+8g+j (second MFMA).
-  u32x4 qB0 = {0u, 0u, 0u, 0u}, qB1 = {0u, 0u, 0u, 0u};
-  if (r16 < group) {
-    const uint16_t *qp = q + (int64_t)row * s_qb + (int64_t)(kh * group + r16) * s_qh + 8 * g;
-    qB0 = ld16(qp);
-    qB1 = ld16(qp + 32);
-  }
-  float m = kNegInf, lsum = 0.f;
-  f32x4 o[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t row_bytes = (uint32_t)s_ks * 2u;
+  TileLane tl;
+  tl.init(lane, row_bytes);
+  // Q^T operand: column r16 = q head kh*group + r16 (zeros past the group).
+  const rsrc_t qr = make_rsrc(q + (int64_t)row * s_qb + (int64_t)kh * group * s_qh, (uint32_t)(group * s_qh * 2));
+  const u32x4 qB0 = bld16(qr, (uint32_t)(r16 * s_qh * 2) + 16u * g);
+  const u32x4 qB1 = bld16(qr, (uint32_t)(r16 * s_qh * 2) + 16u * g + 64u);
+  SoftmaxState S;
+  S.reset();
 
   const int64_t cbase = (int64_t)(crow < 0 || crow >= cache_rows ? 0 : crow) * s_kb + (int64_t)kh * s_kh;
-  const uint16_t *kb = kc + cbase, *vb = vc + cbase;
+  // K / V of this (row, kv head) as buffers ending at key hi: rows past the range read as zeros.
+  const rsrc_t kr = make_rsrc(kc + cbase, (uint32_t)hi * row_bytes);
+  const rsrc_t vr = make_rsrc(vc + cbase, (uint32_t)hi * row_bytes);
   uint16_t *vt = lds + w * 64 * kVRow;
-  const int kg = lane >> 3, dc = lane & 7;
 
-  for (int t0 = lo + 64 * w; t0 < hi; t0 += 64 * NW) {
-    const int last = hi - 1;  // keys past the range are clamped here and masked out below
-    u32x4 ka[2][2][2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int key = min(t0 + 32 * c + 8 * (r16 >> 2) + 4 * t + (r16 & 3), last);
-        const uint16_t *kp = kb + (int64_t)key * s_ks + 8 * g;
-        ka[c][t][0] = ld16(kp);
-        ka[c][t][1] = ld16(kp + 32);
-      }
-    u32x4 vr[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int key = min(t0 + 8 * kg + j, last);
-      vr[j] = ld16(vb + (int64_t)key * s_ks + 8 * dc);
+  // Software pipeline over the wave's tiles t0, t0 + 64*NW, ...: the next tile is always requested
+  // before the current one is computed. The prefetch is unconditional (past the range the buffer
+  // descriptor returns zeros without a memory access), so the compiler's wait for the current tile
+  // leaves the next tile's loads in flight. Two register buffers, unrolled so they never move.
+  constexpr int kStep = 64 * NW;
+  int t0 = lo + 64 * __builtin_amdgcn_readfirstlane(w);
+  if (t0 < hi) {
+    KVTile A, B;
+    load_tile(A, kr, vr, (uint32_t)t0, row_bytes, tl);
+    for (;;) {
+      load_tile(B, kr, vr, (uint32_t)(t0 + kStep), row_bytes, tl);
+      compute_tile(A, t0, hi, qB0, qB1, scale_log2, S, vt, tl);
+      t0 += kStep;
+      if (t0 >= hi) break;
+      load_tile(A, kr, vr, (uint32_t)(t0 + kStep), row_bytes, tl);
+      compute_tile(B, t0, hi, qB0, qB1, scale_log2, S, vt, tl);
+      t0 += kStep;
+      if (t0 >= hi) break;
     }
-
-    // S^T tile (c, t): row 4g+i <-> key t0 + 32c + 8g + 4t + i, column r16 <-> q head.
-    f32x4 s[2][2];
-    float mt = kNegInf;
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        f32x4 a = mfma16x16x32(ka[c][t][0], qB0, f32x4{0.f, 0.f, 0.f, 0.f});
-        a = mfma16x16x32(ka[c][t][1], qB1, a);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = t0 + 32 * c + 8 * g + 4 * t + i;
-          const float v = key < hi ? a[i] * scale_log2 : kNegInf;
-          a[i] = v;
-          mt = fmaxf(mt, v);
-        }
-        s[c][t] = a;
-      }
-    mt = max_over_groups(mt);
-    const float mn = fmaxf(m, mt);
-    const float alpha = (m == kNegInf) ? 0.f : fast_exp2(m - mn);
-    float ps = 0.f;
-    u32x4 pB[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        float p[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = fast_exp2(s[c][t][i] - mn);
-          ps += p[i];
-        }
-        pB[c][2 * t] = pack_bf16x2(p[0], p[1]);
-        pB[c][2 * t + 1] = pack_bf16x2(p[2], p[3]);
-      }
-    lsum = lsum * alpha + ps;
-    m = mn;
-
-    u32x4 vtr[8];
-    transpose8x8_bf16(vr, vtr);
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) st16(vt + (8 * dc + dd) * kVRow + 8 * kg, vtr[dd]);
-    wave_lds_fence();
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      o[dt] *= alpha;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const u32x4 vA = ld16(vt + (16 * dt + r16) * kVRow + 32 * c + 8 * g);
-        o[dt] = mfma16x16x32(vA, pB[c], o[dt]);
-      }
-    }
-    wave_lds_fence();
   }
-  lsum = sum_over_groups(lsum);
+  float m = S.m;
+  float lsum = sum_over_groups(S.lsum);
+  f32x4 (&o)[4] = S.o;
 
   // Lane (r16, g) holds O^T[d = 16dt + 4g + i][head r16].
   if (NW == 1) {
@@ -186,7 +133,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode_split(
 #pragma unroll
     for (int v = 0; v < NW; ++v) {
       const float mv = mb[v * 16 + head];
-      const float wt = (mv == kNegInf) ? 0.f : fast_exp2(mv - M);
+      const float wt = (mv == kNegInf) ? 0.f : fast_exp2((mv - M) * scale_log2);
       num += wt * ob[(v * 16 + head) * 64 + d];
       den += wt * lb[v * 16 + head];
     }
@@ -209,7 +156,7 @@ __global__ __launch_bounds__(64 * NW) void k_decode_split(
 __global__ __launch_bounds__(256) void k_decode_combine(const float *__restrict__ acc_ws,
                                                         const float *__restrict__ ml_ws,
                                                         uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh,
-                                                        int b, int nq, int ns) {
+                                                        int b, int nq, int ns, float scale_log2) {
   const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (pair >= b * nq) return;
   const int row = pair / nq, h = pair - row * nq, d = threadIdx.x & 63;
@@ -220,7 +167,7 @@ __global__ __launch_bounds__(256) void k_decode_combine(const float *__restrict_
   float num = 0.f, den = 0.f;
   for (int sp = 0; sp < ns; ++sp) {
     const float mv = ml[2 * sp];
-    const float wt = (mv == kNegInf) ? 0.f : fast_exp2(mv - M);
+    const float wt = (mv == kNegInf) ? 0.f : fast_exp2((mv - M) * scale_log2);
     num += wt * acc[sp * 64 + d];
     den += wt * ml[2 * sp + 1];
   }
@@ -289,29 +236,31 @@ extern "C" int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
   if ((phases & 2) && nsplit > 1) {
     const unsigned grid = (unsigned)(((int64_t)b * nq + 3) / 4);
     hipLaunchKernelGGL(k_decode_combine, dim3(grid), dim3(256), 0, st, acc_ws, ml_ws, oo, s_ob, s_oh, b, nq,
-                       nsplit);
+                       nsplit, sl2);
     return (int)hipGetLastError();
   }
   return 0;
 }
 
-// Launch-shape policy. A workgroup streams one split of one (row, kv head); the GPU wants about
-// kResidentWaves waves per CU in flight to cover HBM latency, and a wave wants at least
-// kMinTilesPerWave 64-key tiles so its prologue is amortised.
+// Launch-shape policy (measured on MI355X at 192 slots x 2048 keys: one split of 4 waves per
+// (row, kv head) streams the cache at ~42 us/layer; extra splits save ~3 us in the split kernel but
+// the combine launch costs 3-4 us). So: one split whenever the rows x kv heads already give every
+// compute unit a workgroup, and more splits only when they do not (small batches, long caches), up
+// to about two workgroups per compute unit and at least two 64-key tiles per wave.
 extern "C" int a8_decode_choose(int b, int nkv, int cache_len, int nsplit_req, int nsplit_max,
                                 int64_t cap_row_splits, int n_cu, int *nsplit_out, int *waves_out) {
   using namespace a8;
-  constexpr int kResidentWaves = 12, kMinTilesPerWave = 2;
   if (b < 1 || nkv < 1 || cache_len < 0 || n_cu < 1 || !nsplit_out || !waves_out)
     return set_error(A8_EINVAL, "decode_choose: bad arguments b=%d nkv=%d n_cu=%d", b, nkv, n_cu);
   const int tiles = cache_len > 0 ? (cache_len + 63) / 64 : 1;
+  const int nw = tiles >= 8 ? 4 : tiles >= 4 ? 2 : 1;
   const int64_t units = (int64_t)b * nkv;
-  int64_t want = ((int64_t)n_cu * kResidentWaves + units - 1) / units;
-  const int64_t max_waves = (tiles + kMinTilesPerWave - 1) / kMinTilesPerWave;
-  if (want > max_waves) want = max_waves;
-  if (want < 1) want = 1;
-  int nw = want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1;
-  int64_t ns = (want + nw - 1) / nw;
+  int64_t ns = 1;
+  if (units < n_cu) {
+    ns = (2 * (int64_t)n_cu + units - 1) / units;
+    const int64_t by_tiles = tiles / (2 * nw);  // keep >= 2 tiles per wave
+    if (ns > by_tiles) ns = by_tiles;
+  }
   if (ns < nsplit_req) ns = nsplit_req;
   if (nsplit_max >= 1 && ns > nsplit_max) ns = nsplit_max;
   if (ns > tiles) ns = tiles;

@@ -1,0 +1,372 @@
+// Streaming split-K decode (a8_decode_attn_stream, a8_decode_choose_stream): the default launch of the
+// decode attention of serve/fast_kernels.py:193-290 on MI355X.
+//
+// Same semantics as the split + combine pair (decode.hip): query row b attends keys [0, lens[b]) of
+// cache row rowmap[b] with an fp32 online softmax and bf16 softmax weights in P.V, and the partial
+// results over key ranges are merged with w = exp(m - M). What changes is the schedule, chosen for
+// HBM3E (measured on MI355X: a 201 MB read issued as a few hundred independent 256-KB streams runs
+// ~10 % slower than the same bytes swept in address order, and a separate combine launch costs
+// 3-4 us per layer):
+//   * Work unit = chunk of CH = waves * tpw * 64 keys of one (row, kv head); a unit (row, kv head)
+//     has P = ceil(cache_len / CH) chunks, numbered in cache address order. A persistent grid of G
+//     workgroups takes chunks g, g + G, g + 2G, ... so the GPU as a whole sweeps the cache in address
+//     order through a window of about G * CH * 256 bytes.
+//   * Inside a chunk the workgroup's waves take 64-key tiles round-robin (decode_tile.h); each wave
+//     keeps a two-tile register pipeline that runs across chunk boundaries, so the next chunk's
+//     loads are in flight while a chunk's partials are merged and written.
+//   * Per chunk the waves' partials are merged in LDS (double-buffered, one barrier per chunk), each
+//     wave merging a share of the outputs (one wave doing all of it costs ~5 us per layer: the next
+//     chunk's barrier waits for it). A row whose keys fit in one chunk is
+//     written straight to `out`; otherwise the merging wave stores the chunk's (acc, m, l) to the
+//     workspace and moves on, and k_decode_stream_combine (launched right after, one thread per
+//     output element) merges the row's chunks. Merging inside the streaming kernel instead would
+//     need a device-scope handshake per chunk (store completion, counter atomic, partial reads): on a
+//     saturated memory system each of those round trips waits microseconds in the same queues the
+//     KV stream fills, which costs far more than the extra launch.
+#include "decode_tile.h"
+
+namespace a8 {
+
+template <int NW>
+__global__ __launch_bounds__(64 * NW, 2) void k_decode_stream(
+    const uint16_t *__restrict__ q, int64_t s_qb, int64_t s_qh,
+    const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+    int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
+    uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
+    float *__restrict__ ml_ws, int b, int nq, int nkv, int group, int tpw, int P,
+    float sl2) {
+  __shared__ __attribute__((aligned(16))) uint16_t vts[NW * 64 * kVRow];    // per-wave V^T tiles
+  __shared__ __attribute__((aligned(16))) float mrg[2][NW * (32 + 16 * 64)];  // per-wave m, l, O (x2)
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = gridDim.x;
+  const int CH = NW * tpw * 64;
+  const int NC = b * nkv * P;
+  const int nmine = ((int)blockIdx.x < NC) ? (NC - 1 - (int)blockIdx.x) / G + 1 : 0;
+  if (nmine == 0) return;
+
+  const uint32_t row_bytes = (uint32_t)s_ks * 2u;
+  const uint32_t full_row = (uint32_t)cache_len * row_bytes;
+  TileLane tl;
+  tl.init(lane, row_bytes);
+  uint16_t *vt = vts + w * 64 * kVRow;
+
+  // Chunk i of this workgroup: unit u = c / P = row * nkv + kh, part = c % P, keys [part*CH, +CH).
+  struct Chunk {
+    int row, kh, part, lo, hi;  // hi: end of the chunk's keys (<= lo: none)
+    rsrc_t kr, vr;
+  };
+  // A row's length and cache row are read one chunk ahead with ordinary vector loads (so they arrive
+  // in order with the tile loads and never stall the pipeline); they are needed when the chunk's
+  // first tile is requested. For the first chunk only the cache row is needed up front: its tiles
+  // are requested over the whole cache row and keys past the length are masked when computed.
+  struct Meta {
+    int lraw, craw;
+  };
+  auto ids = [&](int i, Chunk &k) {
+    const int c = (int)blockIdx.x + i * G;
+    const int u = c / P;
+    k.part = c - u * P;
+    k.row = u / nkv;
+    k.kh = u - k.row * nkv;
+    k.lo = k.part * CH;
+  };
+  const rsrc_t lens_r = make_rsrc(lens, (uint32_t)b * 4u);
+  const rsrc_t map_r = make_rsrc(rowmap, rowmap ? (uint32_t)b * 4u : 0u);
+  auto meta_load = [&](int i) {
+    Meta m{0, 0};
+    if (i < nmine) {
+      Chunk k;
+      ids(i, k);
+      m.lraw = bld4(lens_r, (uint32_t)k.row * 4u);
+      m.craw = rowmap ? bld4(map_r, (uint32_t)k.row * 4u) : k.row;
+    }
+    return m;
+  };
+  auto resolve = [&](int i, const Meta &m, bool exact, Chunk &k) {
+    ids(i, k);
+    const int crow = __builtin_amdgcn_readfirstlane(m.craw);
+    const bool ok = i < nmine && crow >= 0 && crow < cache_rows;
+    const int64_t cb = (int64_t)(ok ? crow : 0) * s_kb + (int64_t)k.kh * s_kh;
+    uint32_t bound = 0;
+    k.hi = 0;
+    if (ok) {
+      if (exact) {
+        const int L = min(max(__builtin_amdgcn_readfirstlane(m.lraw), 0), cache_len);
+        k.hi = min(k.lo + CH, L);
+        bound = k.hi > 0 ? (uint32_t)k.hi * row_bytes : 0u;
+      } else {
+        k.hi = k.lo + CH;  // refined by hi_of() before the chunk is computed
+        bound = full_row;
+      }
+    }
+    k.kr = make_rsrc(kc + cb, bound);
+    k.vr = make_rsrc(vc + cb, bound);
+  };
+  auto hi_of = [&](const Chunk &k, const Meta &m, int i) {
+    const int crow = __builtin_amdgcn_readfirstlane(m.craw);
+    if (i >= nmine || crow < 0 || crow >= cache_rows) return 0;
+    const int L = min(max(__builtin_amdgcn_readfirstlane(m.lraw), 0), cache_len);
+    return min(k.lo + CH, L);
+  };
+  auto load_q = [&](const Chunk &k, int i, u32x4 &q0, u32x4 &q1) {
+    // past the last chunk the row may not exist: an empty range, nothing is read
+    const rsrc_t qr = make_rsrc(q + (int64_t)(i < nmine ? k.row : 0) * s_qb + (int64_t)k.kh * group * s_qh,
+                                i < nmine ? (uint32_t)(group * s_qh * 2) : 0u);
+    const uint32_t qo = (uint32_t)(tl.r16 * s_qh * 2) + 16u * tl.g;
+    q0 = bld16(qr, qo);
+    q1 = bld16(qr, qo + 64u);
+  };
+
+  SoftmaxState S;
+  S.reset();
+
+  // End of chunk i: every wave parks its state in LDS, then all waves merge it and write the output
+  // (a row within one chunk) or the chunk's partial. Chunks without keys are skipped by every wave
+  // alike, with no barrier, so the LDS buffer alternates with the count of merged chunks (nfin), not
+  // with i: a wave still reading one buffer is never overtaken by writes to it.
+  int nfin = 0;
+  auto finish_chunk = [&](const Chunk &k, int L) {
+    const int peff = L > 0 ? (L + CH - 1) / CH : 1;  // chunks with keys (an empty row still writes 0/0)
+    if (k.part >= peff) {  // no key of this row falls in this chunk
+      S.reset();
+      return;
+    }
+    float *mb = mrg[nfin & 1], *lb = mb + NW * 16, *ob = mb + NW * 32;
+    ++nfin;
+    const float lsum = sum_over_groups(S.lsum);
+    if (tl.g == 0) {
+      mb[w * 16 + tl.r16] = S.m;
+      lb[w * 16 + tl.r16] = lsum;
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+      *reinterpret_cast<f32x4 *>(ob + (w * 16 + tl.r16) * 64 + 16 * dt + 4 * tl.g) = S.o[dt];
+    S.reset();
+    __syncthreads();
+    // every wave merges a share of the (head, dim) outputs; no barrier after: the next chunk writes the
+    // other LDS buffer
+    for (int idx = tid; idx < group * 64; idx += 64 * NW) {
+      const int head = idx >> 6, d = idx & 63;
+      float M = kNegInf;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) M = fmaxf(M, mb[v * 16 + head]);
+      float num = 0.f, den = 0.f;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) {
+        const float mv = mb[v * 16 + head];
+        const float wt = (mv == kNegInf) ? 0.f : fast_exp2((mv - M) * sl2);
+        num += wt * ob[(v * 16 + head) * 64 + d];
+        den += wt * lb[v * 16 + head];
+      }
+      const int hq = k.kh * group + head;
+      if (peff == 1) {
+        out[(int64_t)k.row * s_ob + (int64_t)hq * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
+      } else {
+        const int64_t pi = ((int64_t)k.row * nq + hq) * P + k.part;
+        acc_ws[pi * 64 + d] = num;
+        if (d == 0) {
+          ml_ws[pi * 2] = M;
+          ml_ws[pi * 2 + 1] = den;
+        }
+      }
+    }
+  };
+
+  // The wave's tile sequence: (chunk i, tile j), i = 0..nmine-1, j = 0..tpw-1, in two register
+  // buffers with the loads always one tile ahead (past the end they read zeros, no memory traffic).
+  Meta mcur = meta_load(0);
+  Chunk cur, nxt;
+  resolve(0, mcur, /*exact=*/false, cur);
+  Meta mnxt = meta_load(1);
+  u32x4 qc0, qc1, qn0, qn1;
+  load_q(cur, 0, qc0, qc1);
+  KVTile A, B;
+  load_tile(A, cur.kr, cur.vr, (uint32_t)(cur.lo + 64 * w), row_bytes, tl);
+  int i = 0, j = 0;
+  int hi = 0;
+  bool fresh = true;  // cur's hi not refined yet
+  auto step = [&](KVTile &X, KVTile &Y) -> bool {
+    // request the tile after (i, j) into Y, then consume X
+    const bool last_tile = (j + 1 == tpw);
+    Meta mnn{0, 0};
+    if (last_tile) {
+      resolve(i + 1, mnxt, /*exact=*/true, nxt);
+      mnn = meta_load(i + 2);
+      load_q(nxt, i + 1, qn0, qn1);
+      load_tile(Y, nxt.kr, nxt.vr, (uint32_t)(nxt.lo + 64 * w), row_bytes, tl);
+    } else {
+      load_tile(Y, cur.kr, cur.vr, (uint32_t)(cur.lo + 64 * (w + NW * (j + 1))), row_bytes, tl);
+    }
+    if (fresh) {
+      hi = hi_of(cur, mcur, i);
+      fresh = false;
+    }
+    const int t0 = cur.lo + 64 * (w + NW * j);
+    if (t0 < hi) compute_tile(X, t0, hi, qc0, qc1, sl2, S, vt, tl);
+    if (last_tile) {
+      const int L = (i < nmine) ? min(max(__builtin_amdgcn_readfirstlane(mcur.lraw), 0), cache_len) : 0;
+      const int crow = __builtin_amdgcn_readfirstlane(mcur.craw);
+      finish_chunk(cur, (crow < 0 || crow >= cache_rows) ? 0 : L);
+      ++i;
+      j = 0;
+      cur = nxt;
+      mcur = mnxt;
+      mnxt = mnn;
+      qc0 = qn0;
+      qc1 = qn1;
+      fresh = true;
+      return i < nmine;
+    }
+    ++j;
+    return true;
+  };
+  for (;;) {
+    if (!step(A, B)) break;
+    if (!step(B, A)) break;
+  }
+}
+
+// Merges the chunks of rows longer than one chunk: one thread per (row, q head, dim); rows that fit one
+// chunk were written by the streaming kernel and are skipped. All of a thread's partial loads are
+// independent, so the kernel costs about one memory round trip.
+__global__ __launch_bounds__(256) void k_decode_stream_combine(
+    const float *__restrict__ acc_ws, const float *__restrict__ ml_ws, const int32_t *__restrict__ lens,
+    const int32_t *__restrict__ rowmap, uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, int b, int nq,
+    int cache_rows, int cache_len, int CH, int P, float sl2) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (int64_t)b * nq * 64) return;
+  const int d = (int)(t & 63);
+  const int pair = (int)(t >> 6);
+  const int row = pair / nq, h = pair - row * nq;
+  const int crow = rowmap ? rowmap[row] : row;
+  int L = lens[row];
+  L = (crow < 0 || crow >= cache_rows) ? 0 : min(max(L, 0), cache_len);
+  const int peff = L > 0 ? (L + CH - 1) / CH : 1;
+  if (peff == 1) return;
+  const float *ml = ml_ws + (int64_t)pair * P * 2;
+  const float *acc = acc_ws + (int64_t)pair * P * 64 + d;
+  float M = kNegInf;
+  for (int pp = 0; pp < peff; ++pp) M = fmaxf(M, ml[2 * pp]);
+  float num = 0.f, den = 0.f;
+  for (int pp = 0; pp < peff; ++pp) {
+    const float mv = ml[2 * pp];
+    const float wt = (mv == kNegInf) ? 0.f : fast_exp2((mv - M) * sl2);
+    num += wt * acc[pp * 64];
+    den += wt * ml[2 * pp + 1];
+  }
+  out[(int64_t)row * s_ob + (int64_t)h * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
+}
+
+template <int NW>
+static void launch_stream(int grid, size_t shm, hipStream_t st, const uint16_t *q, int64_t s_qb, int64_t s_qh,
+                          const uint16_t *kc, const uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                          int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap, uint16_t *out,
+                          int64_t s_ob, int64_t s_oh, float *acc_ws, float *ml_ws, int b, int nq, int nkv,
+                          int group, int tpw, int P, float sl2) {
+  hipLaunchKernelGGL(k_decode_stream<NW>, dim3(grid), dim3(64 * NW), shm, st, q, s_qb, s_qh, kc, vc, s_kb, s_kh,
+                     s_ks, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv,
+                     group, tpw, P, sl2);
+}
+
+static inline bool al16s(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace a8
+
+extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
+                                     const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                                     int cache_rows, int cache_len,
+                                     const int32_t *lens, const int32_t *rowmap,
+                                     void *out, int64_t s_ob, int64_t s_oh,
+                                     float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                                     int b, int nq, int nkv, int hd, int waves, int tiles_per_wave, int grid,
+                                     float scale, int phases, void *stream) {
+  using namespace a8;
+  if (hd != 64) return set_error(A8_EUNSUP, "decode_attn_stream: head_dim %d not supported (64 only)", hd);
+  if (b < 0 || nq <= 0 || nkv <= 0 || nq % nkv || cache_rows < 0 || cache_len < 0)
+    return set_error(A8_EINVAL, "decode_attn_stream: bad sizes b=%d nq=%d nkv=%d", b, nq, nkv);
+  const int group = nq / nkv;
+  if (group > 16) return set_error(A8_EUNSUP, "decode_attn_stream: GQA group %d > 16 not supported", group);
+  if (waves != 1 && waves != 2 && waves != 4 && waves != 8)
+    return set_error(A8_EINVAL, "decode_attn_stream: waves must be 1, 2, 4 or 8 (got %d)", waves);
+  if (tiles_per_wave < 1 || tiles_per_wave > 64 || grid < 1)
+    return set_error(A8_EINVAL, "decode_attn_stream: tiles_per_wave %d / grid %d out of range", tiles_per_wave, grid);
+  if (b == 0) return 0;
+  if (!q || !kc || !vc || !lens || !out) return set_error(A8_EINVAL, "decode_attn_stream: null pointer");
+  const int CH = waves * tiles_per_wave * 64;
+  const int P = cache_len > 0 ? (cache_len + CH - 1) / CH : 1;
+  const int64_t NC = (int64_t)b * nkv * P;
+  if (NC > (1ll << 30)) return set_error(A8_EINVAL, "decode_attn_stream: too many chunks");
+  if (P > 1 && (!acc_ws || !ml_ws || (int64_t)b * P > ws_row_splits))
+    return set_error(A8_EWSPACE, "decode_attn_stream: workspace holds %lld row-splits, need b*%d = %lld",
+                     (long long)ws_row_splits, P, (long long)b * P);
+  if (!al16s(q) || !al16s(kc) || !al16s(vc) || !al16s(out) || (P > 1 && !al16s(acc_ws)) ||
+      (s_qb | s_qh | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
+    return set_error(A8_EALIGN, "decode_attn_stream: pointers must be 16-byte aligned and strides multiples of 8");
+  if (grid > NC) grid = (int)NC;
+  const size_t shm = 0;
+  const hipStream_t st = (hipStream_t)stream;
+  const float sl2 = scale * kLog2e;
+  const auto *qq = (const uint16_t *)q;
+  const auto *kk = (const uint16_t *)kc;
+  const auto *vv = (const uint16_t *)vc;
+  auto *oo = (uint16_t *)out;
+  if (phases & 1) {
+    switch (waves) {
+      case 1: launch_stream<1>(grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
+                               rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2);
+        break;
+      case 2: launch_stream<2>(grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
+                               rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2);
+        break;
+      case 4: launch_stream<4>(grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
+                               rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2);
+        break;
+      default: launch_stream<8>(grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
+                                lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P,
+                                sl2);
+        break;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  if ((phases & 2) && P > 1) {
+    const unsigned cgrid = (unsigned)(((int64_t)b * nq * 64 + 255) / 256);
+    hipLaunchKernelGGL(k_decode_stream_combine, dim3(cgrid), dim3(256), 0, st, acc_ws, ml_ws, lens, rowmap, oo,
+                       s_ob, s_oh, b, nq, cache_rows, cache_len, CH, P, sl2);
+    return (int)hipGetLastError();
+  }
+  return 0;
+}
+
+// Launch shape of a8_decode_attn_stream: chunks of waves * tpw * 64 keys sized so that a unit has a
+// few chunks (enough workgroups to fill the GPU, a narrow address window), the workspace holds
+// b * P row-splits, and a grid of about two workgroups per compute unit.
+extern "C" int a8_decode_choose_stream(int b, int nkv, int cache_len, int64_t cap_row_splits, int n_cu,
+                                       int *waves_out, int *tpw_out, int *grid_out) {
+  using namespace a8;
+  if (b < 1 || nkv < 1 || cache_len < 0 || n_cu < 1 || !waves_out || !tpw_out || !grid_out)
+    return set_error(A8_EINVAL, "decode_choose_stream: bad arguments b=%d nkv=%d n_cu=%d", b, nkv, n_cu);
+  const int tiles = cache_len > 0 ? (cache_len + 63) / 64 : 1;
+  int nw = tiles >= 8 ? 4 : tiles >= 4 ? 2 : 1;
+  int tpw = 2;
+  if (tiles < nw * tpw) tpw = 1;
+  // chunk count per unit: at most what the workspace holds
+  const int64_t pmax = cap_row_splits >= b ? cap_row_splits / b : 1;
+  while (true) {
+    const int ch = nw * tpw * 64;
+    const int64_t P = cache_len > 0 ? (cache_len + ch - 1) / ch : 1;
+    if (P <= 1 || P <= pmax || tpw >= 64) break;
+    tpw *= 2;
+  }
+  const int ch = nw * tpw * 64;
+  const int64_t P = cache_len > 0 ? (cache_len + ch - 1) / ch : 1;
+  const int64_t NC = (int64_t)b * nkv * P;
+  int64_t grid = (int64_t)n_cu * (nw >= 4 ? 2 : 4);
+  if (grid > NC) grid = NC;
+  *waves_out = nw;
+  *tpw_out = tpw;
+  *grid_out = (int)grid;
+  return 0;
+}

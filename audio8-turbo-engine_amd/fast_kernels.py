@@ -113,10 +113,13 @@ class DecodeAttention:
     packed rows (many rows, one split) with fixed addresses for graph capture
     (fast_kernels.py:256-269).
 
-    Launch shape: the reference's `nsplit` argument is honoured as a lower bound on the number of key
-    splits; the split count and the wavefronts per split are chosen for the GPU's compute-unit count by
-    a8_decode_choose (policy "auto"). policy = "caller" uses exactly the caller's nsplit. Split
-    boundaries are not part of the contract: every choice computes the same softmax."""
+    Two launch schedules compute the same softmax (split boundaries are not part of the contract):
+      mode "split" (default): a8_decode_attn -- the reference's split kernel + combine kernel structure,
+        launch shape from a8_decode_choose for this GPU's compute-unit count; the caller's `nsplit` is a
+        lower bound on the splits (policy "auto") or exact (policy "caller").
+      mode "stream": a8_decode_attn_stream -- a persistent kernel that sweeps the cache in address order
+        in fixed-size key chunks, plus a small merge kernel for rows longer than a chunk; launch shape
+        from a8_decode_choose_stream."""
 
     def __init__(self, cap_row_splits, nq, nkv, hd, nsplit_max, device, scale=None):
         self.nq, self.nkv, self.hd = nq, nkv, hd
@@ -129,16 +132,18 @@ class DecodeAttention:
         self.ml_flat = torch.empty(self.cap * nq * 2, dtype=torch.float32, device=device)
         dev = torch.device(device)
         self.n_cu = torch.cuda.get_device_properties(dev).multi_processor_count if dev.type == "cuda" else 1
+        self.mode = "split"
         self.policy = "auto"
-        self.force_shape = None  # (nsplit, waves) pins the launch shape (tuning / tests)
+        self.force_shape = None   # split mode: (nsplit, waves) pins the launch shape (tuning / tests)
+        self.force_stream = None  # stream mode: (waves, tiles_per_wave, grid)
         self._shapes = {}
 
     def launch_shape(self, b: int, cache_len: int, nsplit: int):
-        """(key splits, wavefronts per split) for b rows over a cache of cache_len positions."""
+        """Split mode: (key splits, wavefronts per split) for b rows over a cache of cache_len positions."""
         if self.force_shape is not None:
             ns, nw = self.force_shape
             return max(1, min(int(ns), self.cap // max(b, 1))), int(nw)
-        key = (b, cache_len, nsplit, self.policy)
+        key = ("split", b, cache_len, nsplit, self.policy)
         hit = self._shapes.get(key)
         if hit is not None:
             return hit
@@ -150,11 +155,26 @@ class DecodeAttention:
         self._shapes[key] = (ns.value, nw.value)
         return self._shapes[key]
 
+    def stream_shape(self, b: int, cache_len: int):
+        """Stream mode: (wavefronts per workgroup, 64-key tiles per wave per chunk, workgroups)."""
+        if self.force_stream is not None:
+            return tuple(int(x) for x in self.force_stream)
+        key = ("stream", b, cache_len)
+        hit = self._shapes.get(key)
+        if hit is not None:
+            return hit
+        nw, tpw, grid = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+        st = _lib.load().a8_decode_choose_stream(b, self.nkv, cache_len, self.cap, self.n_cu, ctypes.byref(nw),
+                                                 ctypes.byref(tpw), ctypes.byref(grid))
+        _lib.check(st, "decode_choose_stream")
+        self._shapes[key] = (nw.value, tpw.value, grid.value)
+        return self._shapes[key]
+
     def __call__(self, q, kc, vc, lens, out, nsplit=1, bn=64, rowmap=None, phases=3):
         """q: [b, nq, hd]; kc/vc: [rows, nkv, S, hd]; query row i reads cache row rowmap[i]
         (identity when rowmap is None); lens: [b] int32 (keys [0, lens) attended); out: [b, nq, hd]
-        (fast_kernels.py:271-290). `phases` (1 = split kernel, 2 = combine kernel, 3 = both) exists
-        so a profiler can time the two kernels apart; callers leave it at 3."""
+        (fast_kernels.py:271-290). `phases` (1 = the split / streaming kernel, 2 = the combine / merge
+        kernel, 3 = both) lets a profiler time the two kernels apart; callers leave it at 3."""
         b = q.shape[0]
         nsplit = max(1, min(int(nsplit), self.nsplit_max))
         assert b * nsplit <= self.cap, (b, nsplit, self.cap)
@@ -174,14 +194,20 @@ class DecodeAttention:
         _check_device(q=q, kc=kc, vc=vc, lens=lens, rowmap=rowmap, out=out, workspace=self.acc_flat)
         if b == 0:
             return out
+        lib = _lib.load()
+        common = (q.data_ptr(), q.stride(0), q.stride(1),
+                  kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
+                  lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None,
+                  out.data_ptr(), out.stride(0), out.stride(1), self.acc_flat.data_ptr(), self.ml_flat.data_ptr())
+        if (self.mode == "stream" or self.force_stream is not None) and self.force_shape is None:
+            nw, tpw, grid = self.stream_shape(b, kc.shape[2])
+            st = lib.a8_decode_attn_stream(*common, self.cap, b, self.nq, self.nkv, self.hd, nw, tpw, grid,
+                                           float(self.scale), int(phases), _lib.stream_of(q))
+            _lib.check(st, "decode_attention")
+            return out
         ns, nw = self.launch_shape(b, kc.shape[2], nsplit)
-        st = _lib.load().a8_decode_attn(
-            q.data_ptr(), q.stride(0), q.stride(1),
-            kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
-            lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None,
-            out.data_ptr(), out.stride(0), out.stride(1),
-            self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap,
-            b, self.nq, self.nkv, self.hd, ns, nw, float(self.scale), int(phases), _lib.stream_of(q))
+        st = lib.a8_decode_attn(*common, self.cap, b, self.nq, self.nkv, self.hd, ns, nw, float(self.scale),
+                                int(phases), _lib.stream_of(q))
         _lib.check(st, "decode_attention")
         return out
 

@@ -37,7 +37,8 @@ def parse():
     p.add_argument("--config", default="C3", choices=["C2", "C3"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
-    p.add_argument("--shape", default=None, help="force the decode launch shape as NSPLIT,WAVES")
+    p.add_argument("--shape", default=None, help="use the split + combine kernels at NSPLIT,WAVES")
+    p.add_argument("--stream-shape", default=None, help="force the streaming kernel's WAVES,TILES_PER_WAVE,GRID")
     return p.parse_args()
 
 
@@ -109,7 +110,7 @@ def cpu_baseline(w, budget_s):
     cos, sin = ref.rope_tables(10000.0, HD, S)
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 200):
         q = torch.empty(b, NQ, HD, dtype=torch.bfloat16)
         t0 = time.perf_counter()
         ref.bias_rope_store(qkv, bias, cos, sin, pos, slot, q, kc, vc, NQ, NKV, HD)
@@ -141,8 +142,17 @@ def main():
     st, b = w["st"], w["b"]
     if args.shape:
         st.attn.force_shape = tuple(int(x) for x in args.shape.split(","))
+    if args.stream_shape:
+        st.attn.force_stream = tuple(int(x) for x in args.stream_shape.split(","))
     nsplit_req = a8.ref_nsplit(b, NKV)
-    ns, nw = st.attn.launch_shape(b, w["S"], nsplit_req)
+    if st.attn.mode == "stream" and st.attn.force_shape is None:
+        nw, tpw, grid = st.attn.stream_shape(b, w["S"])
+        chunks = -(-w["S"] // (nw * tpw * 64))
+        launch = {"kernel": "k_decode_stream" + (" + k_decode_stream_combine" if chunks > 1 else ""), "waves": nw,
+                  "tiles_per_wave": tpw, "grid": grid, "chunk_keys": nw * tpw * 64, "chunks_per_row": chunks}
+    else:
+        ns, nw = st.attn.launch_shape(b, w["S"], nsplit_req)
+        launch = {"kernel": "k_decode_split" + ("" if ns == 1 else " + k_decode_combine"), "nsplit": ns, "waves": nw}
 
     def tick():
         st.forward(w["qkv"], w["bias"], w["pos"], w["slot"], w["lens"], nsplit=nsplit_req, rowmap=False, q=w["q"],
@@ -178,12 +188,12 @@ def main():
         "config": {"workload": f"{args.config}: {b} slots x KV {max(lens)}" + (" (U[128,2048])" if args.config == "C2"
                    else "") + f", GQA {NQ}/{NKV} hd {HD}, {LAYERS} layers x (bias_rope_store + split-K decode) "
                    "as one HIP graph tick", "slots": b, "kv_len": max(lens), "cache_len": w["S"], "layers": LAYERS,
-                   "decode_launch": {"nsplit": ns, "waves": nw}},
+                   "decode_launch": launch},
         "us_per_layer": round(us_layer, 3),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "decode_us_per_layer": round(dec_us, 3),
         "store_us_per_layer": round(ms_sto * 1e3 / LAYERS, 3),
-        "roofline": {"bound": "hbm", "kernel": "k_decode_split" + ("" if ns == 1 else " + k_decode_combine"),
+        "roofline": {"bound": "hbm", "kernel": launch["kernel"],
                      "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": dec_bytes, "us_per_launch": round(dec_us, 3)},

@@ -112,6 +112,34 @@ int a8_decode_choose(int b, int nkv, int cache_len, int nsplit_req, int nsplit_m
                      int64_t cap_row_splits, int n_cu, int *nsplit_out, int *waves_out);
 
 /*
+ * Split-K flash-decoding, streaming schedule: the default decode launch. Same inputs, outputs and
+ * semantics as a8_decode_attn (serve/fast_kernels.py:271-290 with the kernels 193-253). Each
+ * (row, kv head) is cut into chunks of waves * tiles_per_wave * 64 keys, P = ceil(cache_len / chunk)
+ * per row; `grid` persistent workgroups sweep the chunks in cache address order. Rows whose keys fit
+ * in one chunk are written by that kernel; longer rows leave per-chunk partials in acc_ws / ml_ws
+ * (b * P row-splits <= ws_row_splits) that a second, small kernel merges.
+ * waves   1, 2, 4 or 8; tiles_per_wave >= 1; grid >= 1 (clamped to the chunk count).
+ * phases  bit 0: streaming kernel, bit 1: merge kernel (3 = both; the normal value).
+ * Use a8_decode_choose_stream for the launch shape.
+ */
+int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
+                          const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                          int cache_rows, int cache_len,
+                          const int32_t *lens, const int32_t *rowmap,
+                          void *out, int64_t s_ob, int64_t s_oh,
+                          float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                          int b, int nq, int nkv, int hd, int waves, int tiles_per_wave, int grid,
+                          float scale, int phases, void *stream);
+
+/*
+ * Launch shape of a8_decode_attn_stream for b rows over a cache of cache_len positions on a GPU of
+ * n_cu compute units, within a workspace of cap_row_splits row-splits. Replaces the per-bucket split
+ * heuristic of serve/fast_engine.py:776 (tuned there for an 84-SM GPU).
+ */
+int a8_decode_choose_stream(int b, int nkv, int cache_len, int64_t cap_row_splits, int n_cu,
+                            int *waves_out, int *tiles_per_wave_out, int *grid_out);
+
+/*
  * Packed causal prefill attention over keys already stored in cache rows.
  * Replaces serve/fast_kernels.py:350-358 (prefill_attention) and its kernel
  * _prefill_attn_kernel (296-332); the block plan is the reference's PrefillPlan

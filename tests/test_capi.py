@@ -21,7 +21,8 @@ def declared_functions():
 
 def test_header_declares_the_entry_points():
     assert set(declared_functions()) == {"a8_version", "a8_last_error", "a8_hip_runtime_path", "a8_bias_rope_store",
-                                         "a8_decode_attn", "a8_decode_choose", "a8_prefill_attn"}
+                                         "a8_decode_attn", "a8_decode_choose", "a8_decode_attn_stream",
+                                         "a8_decode_choose_stream", "a8_prefill_attn"}
 
 
 def test_library_exports_every_declared_symbol(a8):
@@ -110,11 +111,60 @@ def test_decode_choose_contract(a8):
                         assert ns <= max(1, -(-S // 64))            # no more splits than 64-key tiles
                         if ns < req:                                 # only the caps may cut the request
                             assert ns in (nmax, cap // b, max(1, -(-S // 64)))
-    # the peak-load config fills the GPU with >= 8 waves per CU
-    ns, nw = _choose(lib, 192)
-    assert 192 * 2 * ns * nw >= 8 * 256
+    # the peak-load config: one split (no combine launch), 4 waves per split
+    assert _choose(lib, 192) == (1, 4)
+    # a single row over a long cache is split to occupy the GPU
+    ns, nw = _choose(lib, 1, S=2048)
+    assert ns >= 4 and ns * nw * 2 <= 2 * 256 * 4
     # tiny caches: one wave, one split
     assert _choose(lib, 384, S=10, nmax=1) == (1, 1)
     with pytest.raises(ctypes.ArgumentError):
         lib.a8_decode_choose(1, 2, 8, 1, 1, 8, 256, None, "x")
     assert lib.a8_decode_choose(0, 2, 8, 1, 1, 8, 256, ctypes.byref(ctypes.c_int()), ctypes.byref(ctypes.c_int())) == -1
+
+
+def _stream_args(**kw):
+    a = dict(q=16, s_qb=896, s_qh=64, kc=16, vc=16, s_kb=1024, s_kh=512, s_ks=64, rows=1, S=8, lens=16,
+             rowmap=None, out=16, s_ob=896, s_oh=64, acc=16, ml=16, ws=4, b=1, nq=14, nkv=2, hd=64,
+             waves=4, tpw=2, grid=4, scale=0.125, phases=3, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_decode_stream_rejects_before_launch(a8):
+    lib = a8.load_library()
+    f = lib.a8_decode_attn_stream
+    assert f(*_stream_args(hd=32)) == -3
+    assert f(*_stream_args(nq=34)) == -3
+    assert f(*_stream_args(waves=5)) == -1
+    assert f(*_stream_args(tpw=0)) == -1
+    assert f(*_stream_args(grid=0)) == -1
+    # 3 rows over a 2048-key cache in 512-key chunks need 3 * 4 row-splits of workspace
+    assert f(*_stream_args(b=3, S=2048, ws=11)) == -4
+    assert f(*_stream_args(b=3, S=2048, ws=12, ml=None)) == -4
+    assert f(*_stream_args(q=8)) == -2
+    assert f(*_stream_args(b=0)) == 0
+
+
+def _choose_stream(lib, b, nkv=2, S=2048, cap=8192, n_cu=256):
+    nw, tpw, grid = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    assert lib.a8_decode_choose_stream(b, nkv, S, cap, n_cu, ctypes.byref(nw), ctypes.byref(tpw),
+                                       ctypes.byref(grid)) == 0
+    return nw.value, tpw.value, grid.value
+
+
+def test_decode_choose_stream_contract(a8):
+    lib = a8.load_library()
+    for b in (1, 2, 16, 64, 192, 384, 2000):
+        for S in (1, 10, 64, 385, 2048, 4096):
+            for cap in (b, 4 * b, 16 * b, 8192):
+                nw, tpw, grid = _choose_stream(lib, b, S=S, cap=cap)
+                assert nw in (1, 2, 4, 8) and tpw >= 1 and grid >= 1
+                ch = nw * tpw * 64
+                P = -(-S // ch)
+                assert P == 1 or b * P <= cap or tpw >= 64     # fits the workspace
+                assert grid <= b * 2 * P                          # no idle workgroups
+    # the peak-load config gets several chunks per row (address-order sweep) on a ~2-per-CU grid
+    nw, tpw, grid = _choose_stream(lib, 192)
+    assert -(-2048 // (nw * tpw * 64)) >= 2 and grid <= 2 * 256
+    assert _choose_stream(lib, 384, S=10, cap=384) == (1, 1, 768)

@@ -132,7 +132,8 @@ def test_decode_rowmap_and_strided_cache(a8, ref, dev):
 
 
 def test_decode_phases_split_then_combine(a8, ref, dev):
-    """The split and combine kernels launched one at a time give the same bits as one call."""
+    """The split and combine kernels (and the streaming and merge kernels) launched one at a time give the
+    same bits as one call."""
     say("case: decode phases 1 then 2")
     g = torch.Generator().manual_seed(25)
     b, S = 16, 700
@@ -140,13 +141,14 @@ def test_decode_phases_split_then_combine(a8, ref, dev):
     kc, vc = randn_bf16(g, b, NKV, S, HD).to(dev), randn_bf16(g, b, NKV, S, HD).to(dev)
     lens = torch.randint(1, S + 1, (b,), generator=g).int().to(dev)
     att = a8.DecodeAttention(16 * b, NQ, NKV, HD, 16, dev)
-    att.force_shape = (5, 2)
-    o1, o2 = torch.empty(b, NQ, HD, dtype=BF, device=dev), torch.empty(b, NQ, HD, dtype=BF, device=dev)
-    att(q, kc, vc, lens, o1)
-    att(q, kc, vc, lens, o2, phases=1)
-    att(q, kc, vc, lens, o2, phases=2)
-    torch.cuda.synchronize()
-    assert torch.equal(o1.cpu(), o2.cpu())
+    for split, stream in (((5, 2), None), (None, (2, 1, 9))):
+        att.force_shape, att.force_stream = split, stream
+        o1, o2 = torch.empty(b, NQ, HD, dtype=BF, device=dev), torch.empty(b, NQ, HD, dtype=BF, device=dev)
+        att(q, kc, vc, lens, o1)
+        att(q, kc, vc, lens, o2, phases=1)
+        att(q, kc, vc, lens, o2, phases=2)
+        torch.cuda.synchronize()
+        assert torch.equal(o1.cpu(), o2.cpu())
 
 
 def test_decode_after_store_c1(a8, ref, dev):
@@ -166,3 +168,46 @@ def test_decode_after_store_c1(a8, ref, dev):
                        NQ, NKV, HD)
     out, _ = run_gpu(a8, dev, qd.cpu(), kcd.cpu(), vcd.cpu(), pos + 1)
     assert maxabs(out, want) <= TOL
+
+
+@pytest.mark.parametrize("nw,tpw,grid", [(4, 2, 512), (4, 2, 1), (4, 2, 3), (1, 1, 7), (2, 1, 64), (8, 2, 256),
+                                         (4, 4, 100), (1, 3, 1000), (8, 1, 2)])
+def test_decode_stream_shapes(a8, ref, dev, nw, tpw, grid):
+    """The streaming kernel at forced launch shapes: chunks of nw * tpw * 64 keys swept by `grid`
+    workgroups (grid 1: one workgroup takes every chunk; 64-key chunks: many partials per row, merged by
+    the merge kernel). Ragged lengths, a row map, empty rows; two calls in a row give the same bits."""
+    say(f"case: decode stream waves={nw} tpw={tpw} grid={grid}")
+    g = torch.Generator().manual_seed(27)
+    b, rows, S = 20, 9, 1500
+    q = randn_bf16(g, b, NQ, HD)
+    kc, vc = randn_bf16(g, rows, NKV, S, HD), randn_bf16(g, rows, NKV, S, HD)
+    lens = torch.randint(1, S + 1, (b,), generator=g).int()
+    lens[:6] = torch.tensor([0, 1, 64, 65, 1500, 0], dtype=torch.int32)
+    rowmap = torch.randint(0, rows, (b,), generator=g).int()
+    want = ref.decode_attention(q, kc, vc, lens, rowmap=rowmap)
+    att = a8.DecodeAttention(b * 32, NQ, NKV, HD, 16, dev)
+    att.force_stream = (nw, tpw, grid)
+    outs = []
+    for _ in range(2):
+        out = torch.empty(b, NQ, HD, dtype=BF, device=dev)
+        att(q.to(dev), kc.to(dev), vc.to(dev), lens.to(dev), out, rowmap=rowmap.to(dev))
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    o = outs[0]
+    assert torch.isnan(o[0].float()).all() and torch.isnan(o[5].float()).all()
+    assert maxabs(o[1:5], want[1:5]) <= TOL and maxabs(o[6:], want[6:]) <= TOL
+
+
+def test_decode_stream_default_shapes_all_configs(a8, ref, dev):
+    """The chooser's shape for each config's row count / cache length runs and matches the oracle."""
+    g = torch.Generator().manual_seed(28)
+    for b, S in ((1, 512), (64, 4096), (192, 2048), (384, 10), (7, 100), (300, 3000)):
+        say(f"case: decode stream default shape b={b} S={S}")
+        q = randn_bf16(g, b, NQ, HD)
+        kc, vc = randn_bf16(g, b, NKV, S, HD), randn_bf16(g, b, NKV, S, HD)
+        lens = torch.randint(1, S + 1, (b,), generator=g).int()
+        want = ref.decode_attention(q, kc, vc, lens)
+        out, att = run_gpu(a8, dev, q, kc, vc, lens, cap=max(16 * b, 8192))
+        say(f"  shape {att.stream_shape(b, S)}")
+        assert maxabs(out, want) <= TOL
