@@ -30,11 +30,13 @@ __device__ __forceinline__ uint32_t f2bf_rne(float f) {
   return u >> 16;
 }
 
-// Two fp32 -> one dword of two bf16 (lo in bits 0..15) through the hardware's RNE conversion
-// (v_cvt_pk_bf16_f32). Used where values are finite by construction (softmax weights, outputs).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> one dword of two bf16 (lo in bits 0..15) with one v_cvt_pk_bf16_f32 (round to nearest
+// even). Used where values are finite by construction (softmax weights, outputs).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
@@ -50,6 +52,15 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
+// The same descriptor from a base and size the compiler cannot prove wave-uniform (values derived from
+// vector-loaded metadata): reading them from the first lane makes the descriptor scalar, where a
+// divergent descriptor would wrap every load in a loop over lanes.
+__device__ __forceinline__ rsrc_t make_rsrc_wave(const void *base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  return make_rsrc(reinterpret_cast<const void *>(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
+}
 // 4-byte vector-memory load at byte offset `off`. Unlike a scalar load of a uniform address, it is
 // counted with the tile loads (vmcnt), so waiting for it never waits for the LDS traffic or vice versa.
 __device__ __forceinline__ int bld4(rsrc_t r, uint32_t off) {
@@ -58,6 +69,26 @@ __device__ __forceinline__ int bld4(rsrc_t r, uint32_t off) {
 // 16-byte load at byte offset `off` (the whole offset in the VGPR operand, so the range check sees it).
 __device__ __forceinline__ u32x4 bld16(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// 16-byte-per-lane DMA from a raw buffer straight into LDS (buffer_load_dwordx4 ... lds): lane l's
+// 16 bytes from buffer offset voff + soff + IMM land at LDS address lds + IMM + 16 l (the immediate
+// moves both sides, soff only the buffer side). The range check covers voff + soff + IMM; lanes past
+// the range write zeros. lds must be wave-uniform (it goes to M0). Completion is counted in vmcnt.
+typedef __attribute__((address_space(3))) void lds_void_t;
+template <int IMM>
+__device__ __forceinline__ void bld16_lds(rsrc_t r, void *lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, voff, soff, IMM, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i supplies the address of 4 consecutive bf16 and
+// lane j receives, in slot k, element j%4 of lane 4k + j/4's data. With lane i pointing at row
+// (r0 + i/4), columns c0 + 4(i%4).. of a row-major bf16 matrix, lane j receives column c0 + j of rows
+// r0..r0+3: a 4 x 16 block read transposed.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 lds_tr16(const void *p) {
+  return __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4 *)const_cast<void *>(p)));
 }
 
 // D = A(16x32) * B(32x16) + C, bf16 in, fp32 accumulate. Lane l supplies A[l%16][8*(l/16)+j] and

@@ -49,9 +49,9 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   const int lo = sp * per;
   const int hi = min(lo + per, L);
 
-  const uint32_t row_bytes = (uint32_t)s_ks * 2u;
+  constexpr uint32_t row_bytes = kRow;  // s_ks == 64, checked by the entry point
   TileLane tl;
-  tl.init(lane, row_bytes);
+  tl.init(lane);
   // Q^T operand: column r16 = q head kh*group + r16 (zeros past the group).
   const rsrc_t qr = make_rsrc(q + (int64_t)row * s_qb + (int64_t)kh * group * s_qh, (uint32_t)(group * s_qh * 2));
   const u32x4 qB0 = bld16(qr, (uint32_t)(r16 * s_qh * 2) + 16u * g);
@@ -65,24 +65,24 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   const rsrc_t vr = make_rsrc(vc + cbase, (uint32_t)hi * row_bytes);
   uint16_t *vt = lds + w * 64 * kVRow;
 
-  // Software pipeline over the wave's tiles t0, t0 + 64*NW, ...: the next tile is always requested
-  // before the current one is computed. The prefetch is unconditional (past the range the buffer
-  // descriptor returns zeros without a memory access), so the compiler's wait for the current tile
-  // leaves the next tile's loads in flight. Two register buffers, unrolled so they never move.
+  // Software pipeline over the wave's tiles first + k * 64*NW, k = 0..n-1, two register buffers:
+  // each iteration requests tile k, consumes tile k-1 (loaded one step earlier), requests tile k+1 and
+  // consumes tile k. Nothing is in flight when the loop is entered, so the loop header sees the same
+  // pending loads on both edges and the compiler's waits stay partial (vmcnt(16+)); a prologue load
+  // in front of the loop lands in other registers and costs a full drain (vmcnt(0)) per iteration.
+  // Requests past the range read zeros without memory traffic.
   constexpr int kStep = 64 * NW;
-  int t0 = lo + 64 * __builtin_amdgcn_readfirstlane(w);
-  if (t0 < hi) {
+  const int first = lo + 64 * __builtin_amdgcn_readfirstlane(w);
+  const int n = first < hi ? (hi - first + kStep - 1) / kStep : 0;
+  if (n > 0) {
     KVTile A, B;
-    load_tile(A, kr, vr, (uint32_t)t0, row_bytes, tl);
-    for (;;) {
-      load_tile(B, kr, vr, (uint32_t)(t0 + kStep), row_bytes, tl);
-      compute_tile(A, t0, hi, qB0, qB1, scale_log2, S, vt, tl);
-      t0 += kStep;
-      if (t0 >= hi) break;
-      load_tile(A, kr, vr, (uint32_t)(t0 + kStep), row_bytes, tl);
-      compute_tile(B, t0, hi, qB0, qB1, scale_log2, S, vt, tl);
-      t0 += kStep;
-      if (t0 >= hi) break;
+    for (int k = 0;; k += 2) {
+      load_tile(A, kr, vr, (uint32_t)(first + k * kStep), tl);
+      if (k > 0) compute_tile(B, first + (k - 1) * kStep, hi, qB0, qB1, scale_log2, S, vt, tl);
+      if (k >= n) break;
+      load_tile(B, kr, vr, (uint32_t)(first + (k + 1) * kStep), tl);
+      compute_tile(A, first + k * kStep, hi, qB0, qB1, scale_log2, S, vt, tl);
+      if (k + 1 >= n) break;
     }
   }
   float m = S.m;
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     lb[w * 16 + r16] = lsum;
   }
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4 *>(ob + (w * 16 + r16) * 64 + 16 * dt + 4 * g) = o[dt];
+  for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4 *>(ob + (w * 16 + r16) * kOb + 16 * dt + 4 * g) = o[dt];
   __syncthreads();
   for (int idx = threadIdx.x; idx < group * 64; idx += 64 * NW) {
     const int head = idx >> 6, d = idx & 63;
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     for (int v = 0; v < NW; ++v) {
       const float mv = mb[v * 16 + head];
       const float wt = (mv == kNegInf) ? 0.f : fast_exp2((mv - M) * scale_log2);
-      num += wt * ob[(v * 16 + head) * 64 + d];
+      num += wt * ob[(v * 16 + head) * kOb + d];
       den += wt * lb[v * 16 + head];
     }
     const int hq = kh * group + head;
@@ -210,6 +210,8 @@ extern "C" int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
   if (nsplit > 1 && (!acc_ws || !ml_ws || (int64_t)b * nsplit > ws_row_splits))
     return set_error(A8_EWSPACE, "decode_attn: workspace holds %lld row-splits, need b*nsplit = %lld",
                      (long long)ws_row_splits, (long long)b * nsplit);
+  if (s_ks != hd) return set_error(A8_EUNSUP, "decode_attn: cache positions must be contiguous rows (s_ks %lld)",
+                                   (long long)s_ks);
   if (!al16(q) || !al16(kc) || !al16(vc) || !al16(out) || (nsplit > 1 && !al16(acc_ws)) ||
       (s_qb | s_qh | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
     return set_error(A8_EALIGN, "decode_attn: pointers must be 16-byte aligned and strides multiples of 8");

@@ -27,16 +27,18 @@
 
 namespace a8 {
 
-template <int NW>
-__global__ __launch_bounds__(64 * NW, 2) void k_decode_stream(
+// NT = 64-key tiles per pipeline step (decode_tile.h compute_step); tpw is a multiple of NT. With
+// NT = 2 a wave holds two 128-key steps in registers (one wave per SIMD, up to 512 VGPRs).
+template <int NW, int NT>
+__global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
     const uint16_t *__restrict__ q, int64_t s_qb, int64_t s_qh,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
     int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
     uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
     float *__restrict__ ml_ws, int b, int nq, int nkv, int group, int tpw, int P,
     float sl2) {
-  __shared__ __attribute__((aligned(16))) uint16_t vts[NW * 64 * kVRow];    // per-wave V^T tiles
-  __shared__ __attribute__((aligned(16))) float mrg[2][NW * (32 + 16 * 64)];  // per-wave m, l, O (x2)
+  __shared__ __attribute__((aligned(16))) uint16_t vts[NW * NT * 64 * kVRow];  // per-wave V^T tiles
+  __shared__ __attribute__((aligned(16))) float mrg[2][NW * (32 + 16 * kOb)];  // per-wave m, l, O (x2)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -46,11 +48,13 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_stream(
   const int nmine = ((int)blockIdx.x < NC) ? (NC - 1 - (int)blockIdx.x) / G + 1 : 0;
   if (nmine == 0) return;
 
-  const uint32_t row_bytes = (uint32_t)s_ks * 2u;
+  constexpr uint32_t row_bytes = kRow;  // s_ks == 64, checked by the entry point
   const uint32_t full_row = (uint32_t)cache_len * row_bytes;
   TileLane tl;
-  tl.init(lane, row_bytes);
-  uint16_t *vt = vts + w * 64 * kVRow;
+  tl.init(lane);
+  uint16_t *vt = vts + w * NT * 64 * kVRow;
+  constexpr int KS = 64 * NT;  // keys per step
+  const int spw = tpw / NT;     // steps per wave and chunk
 
   // Chunk i of this workgroup: unit u = c / P = row * nkv + kh, part = c % P, keys [part*CH, +CH).
   struct Chunk {
@@ -101,8 +105,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_stream(
         bound = full_row;
       }
     }
-    k.kr = make_rsrc(kc + cb, bound);
-    k.vr = make_rsrc(vc + cb, bound);
+    k.kr = make_rsrc_wave(kc + cb, bound);
+    k.vr = make_rsrc_wave(vc + cb, bound);
   };
   auto hi_of = [&](const Chunk &k, const Meta &m, int i) {
     const int crow = __builtin_amdgcn_readfirstlane(m.craw);
@@ -142,7 +146,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_stream(
     }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
-      *reinterpret_cast<f32x4 *>(ob + (w * 16 + tl.r16) * 64 + 16 * dt + 4 * tl.g) = S.o[dt];
+      *reinterpret_cast<f32x4 *>(ob + (w * 16 + tl.r16) * kOb + 16 * dt + 4 * tl.g) = S.o[dt];
     S.reset();
     __syncthreads();
     // every wave merges a share of the (head, dim) outputs; no barrier after: the next chunk writes the
@@ -157,7 +161,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_stream(
       for (int v = 0; v < NW; ++v) {
         const float mv = mb[v * 16 + head];
         const float wt = (mv == kNegInf) ? 0.f : fast_exp2((mv - M) * sl2);
-        num += wt * ob[(v * 16 + head) * 64 + d];
+        num += wt * ob[(v * 16 + head) * kOb + d];
         den += wt * lb[v * 16 + head];
       }
       const int hq = k.kh * group + head;
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_stream(
     }
   };
 
-  // The wave's tile sequence: (chunk i, tile j), i = 0..nmine-1, j = 0..tpw-1, in two register
+  // The wave's step sequence: (chunk i, step j), i = 0..nmine-1, j = 0..spw-1, in two register
   // buffers with the loads always one tile ahead (past the end they read zeros, no memory traffic).
   Meta mcur = meta_load(0);
   Chunk cur, nxt;
@@ -182,29 +186,29 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_stream(
   Meta mnxt = meta_load(1);
   u32x4 qc0, qc1, qn0, qn1;
   load_q(cur, 0, qc0, qc1);
-  KVTile A, B;
-  load_tile(A, cur.kr, cur.vr, (uint32_t)(cur.lo + 64 * w), row_bytes, tl);
+  KVTile A[NT], B[NT];
+  load_step<NT>(A, cur.kr, cur.vr, (uint32_t)(cur.lo + KS * w), tl);
   int i = 0, j = 0;
   int hi = 0;
   bool fresh = true;  // cur's hi not refined yet
-  auto step = [&](KVTile &X, KVTile &Y) -> bool {
+  auto step = [&](KVTile (&X)[NT], KVTile (&Y)[NT]) -> bool {
     // request the tile after (i, j) into Y, then consume X
-    const bool last_tile = (j + 1 == tpw);
+    const bool last_tile = (j + 1 == spw);
     Meta mnn{0, 0};
     if (last_tile) {
       resolve(i + 1, mnxt, /*exact=*/true, nxt);
       mnn = meta_load(i + 2);
       load_q(nxt, i + 1, qn0, qn1);
-      load_tile(Y, nxt.kr, nxt.vr, (uint32_t)(nxt.lo + 64 * w), row_bytes, tl);
+      load_step<NT>(Y, nxt.kr, nxt.vr, (uint32_t)(nxt.lo + KS * w), tl);
     } else {
-      load_tile(Y, cur.kr, cur.vr, (uint32_t)(cur.lo + 64 * (w + NW * (j + 1))), row_bytes, tl);
+      load_step<NT>(Y, cur.kr, cur.vr, (uint32_t)(cur.lo + KS * (w + NW * (j + 1))), tl);
     }
     if (fresh) {
       hi = hi_of(cur, mcur, i);
       fresh = false;
     }
-    const int t0 = cur.lo + 64 * (w + NW * j);
-    if (t0 < hi) compute_tile(X, t0, hi, qc0, qc1, sl2, S, vt, tl);
+    const int t0 = cur.lo + KS * (w + NW * j);
+    if (t0 < hi) compute_step<NT>(X, t0, hi, qc0, qc1, sl2, S, vt, tl);
     if (last_tile) {
       const int L = (i < nmine) ? min(max(__builtin_amdgcn_readfirstlane(mcur.lraw), 0), cache_len) : 0;
       const int crow = __builtin_amdgcn_readfirstlane(mcur.craw);
@@ -259,13 +263,14 @@ __global__ __launch_bounds__(256) void k_decode_stream_combine(
   out[(int64_t)row * s_ob + (int64_t)h * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
 }
 
-template <int NW>
+template <int NW, int NT>
 static void launch_stream(int grid, size_t shm, hipStream_t st, const uint16_t *q, int64_t s_qb, int64_t s_qh,
                           const uint16_t *kc, const uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
                           int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap, uint16_t *out,
                           int64_t s_ob, int64_t s_oh, float *acc_ws, float *ml_ws, int b, int nq, int nkv,
                           int group, int tpw, int P, float sl2) {
-  hipLaunchKernelGGL(k_decode_stream<NW>, dim3(grid), dim3(64 * NW), shm, st, q, s_qb, s_qh, kc, vc, s_kb, s_kh,
+  auto kern = k_decode_stream<NW, NT>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), shm, st, q, s_qb, s_qh, kc, vc, s_kb, s_kh,
                      s_ks, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv,
                      group, tpw, P, sl2);
 }
@@ -301,6 +306,9 @@ extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
   if (P > 1 && (!acc_ws || !ml_ws || (int64_t)b * P > ws_row_splits))
     return set_error(A8_EWSPACE, "decode_attn_stream: workspace holds %lld row-splits, need b*%d = %lld",
                      (long long)ws_row_splits, P, (long long)b * P);
+  if (s_ks != hd)
+    return set_error(A8_EUNSUP, "decode_attn_stream: cache positions must be contiguous rows (s_ks %lld)",
+                     (long long)s_ks);
   if (!al16s(q) || !al16s(kc) || !al16s(vc) || !al16s(out) || (P > 1 && !al16s(acc_ws)) ||
       (s_qb | s_qh | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
     return set_error(A8_EALIGN, "decode_attn_stream: pointers must be 16-byte aligned and strides multiples of 8");
@@ -313,21 +321,20 @@ extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
   const auto *vv = (const uint16_t *)vc;
   auto *oo = (uint16_t *)out;
   if (phases & 1) {
-    switch (waves) {
-      case 1: launch_stream<1>(grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
-                               rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2);
-        break;
-      case 2: launch_stream<2>(grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
-                               rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2);
-        break;
-      case 4: launch_stream<4>(grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
-                               rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2);
-        break;
-      default: launch_stream<8>(grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
-                                lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P,
-                                sl2);
-        break;
+#define A8_STREAM_ARGS grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens, rowmap, \
+                       oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2
+    // two-tile steps where the tile count allows and the LDS holds them (8 waves x 2 V^T tiles do not fit)
+    const bool nt2 = (tiles_per_wave % 2 == 0) && waves <= 4;
+    switch (waves * 2 + (nt2 ? 1 : 0)) {
+      case 2: launch_stream<1, 1>(A8_STREAM_ARGS); break;
+      case 3: launch_stream<1, 2>(A8_STREAM_ARGS); break;
+      case 4: launch_stream<2, 1>(A8_STREAM_ARGS); break;
+      case 5: launch_stream<2, 2>(A8_STREAM_ARGS); break;
+      case 8: launch_stream<4, 1>(A8_STREAM_ARGS); break;
+      case 9: launch_stream<4, 2>(A8_STREAM_ARGS); break;
+      default: launch_stream<8, 1>(A8_STREAM_ARGS); break;
     }
+#undef A8_STREAM_ARGS
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }

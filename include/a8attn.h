@@ -91,6 +91,8 @@ int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bias,
  * phases  bit 0: run the split kernel, bit 1: run the combine kernel (3 = both; the normal value).
  *         Running them separately lets a caller time each kernel.
  * Rows with lens == 0 produce NaN (0/0), exactly as the reference's combine does.
+ * The cache positions must be contiguous rows (s_ks == hd == 64, true of every reference cache view);
+ * otherwise A8_EUNSUP.
  */
 int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
                    const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
