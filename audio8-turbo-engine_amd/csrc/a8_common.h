@@ -120,6 +120,34 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Workgroup barrier for data exchanged through LDS with ordinary LDS stores: compiler-only fences,
+// this wave's LDS operations completed (s_waitcnt lgkmcnt(0)), then s_barrier. Vector-memory loads
+// and LDS DMA stay in flight: __syncthreads() would wait for all of them (on gfx9 one counter tracks
+// loads and stores, and its fence covers LDS DMA), draining the loads prefetched for the next tiles.
+// Not for LDS written by DMA.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Four 16-byte LDS stores at byte offsets 0, 64, 128, 192 from p. Written as one asm block because
+// the compiler's wait bookkeeping may take plain stores next to in-flight LDS DMA as overlapping it
+// and drain every outstanding load first. Completion is not tracked: wait with lds_barrier (or an
+// explicit lgkmcnt(0)) before the data is read.
+__device__ __forceinline__ void lds_store_4x16(void *p, f32x4 a, f32x4 b, f32x4 c, f32x4 d) {
+  const uint32_t addr = (uint32_t)reinterpret_cast<uintptr_t>(p);
+  asm volatile(
+      "ds_write_b128 %0, %1\n\t"
+      "ds_write_b128 %0, %2 offset:64\n\t"
+      "ds_write_b128 %0, %3 offset:128\n\t"
+      "ds_write_b128 %0, %4 offset:192"
+      :
+      : "v"(addr), "v"(a), "v"(b), "v"(c), "v"(d)
+      : "memory");
+}
+
 // 8x8 transpose of bf16 words held as 8 rows x 16 bytes: out[c] collects element c of every row
 // (row j in slot j). Each output dword pairs rows (2e, 2e+1).
 __device__ __forceinline__ void transpose8x8_bf16(const u32x4 (&in)[8], u32x4 (&out)[8]) {

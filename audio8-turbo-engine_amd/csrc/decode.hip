@@ -36,7 +36,10 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
     uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
     float *__restrict__ ml_ws, int nq, int group, int ns, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[NW * 64 * kVRow];
+  // V tiles of the two pipeline buffers (one per wave each); separate arrays, so the compiler tells
+  // their DMA completions apart and waits only for the buffer it reads.
+  __shared__ __attribute__((aligned(16))) uint16_t vbA[NW * kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t vbB[NW * kVTile];
   const int sp = blockIdx.x, kh = blockIdx.y, row = blockIdx.z;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int r16 = lane & 15, g = lane >> 4;
@@ -63,7 +66,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   // K / V of this (row, kv head) as buffers ending at key hi: rows past the range read as zeros.
   const rsrc_t kr = make_rsrc(kc + cbase, (uint32_t)hi * row_bytes);
   const rsrc_t vr = make_rsrc(vc + cbase, (uint32_t)hi * row_bytes);
-  uint16_t *vt = lds + w * 64 * kVRow;
+  uint16_t *va = vbA + w * kVTile, *vb = vbB + w * kVTile;
 
   // Software pipeline over the wave's tiles first + k * 64*NW, k = 0..n-1, two register buffers:
   // each iteration requests tile k, consumes tile k-1 (loaded one step earlier), requests tile k+1 and
@@ -75,16 +78,19 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   const int first = lo + 64 * __builtin_amdgcn_readfirstlane(w);
   const int n = first < hi ? (hi - first + kStep - 1) / kStep : 0;
   if (n > 0) {
-    KVTile A, B;
+    KTile A[1], B[1];
     for (int k = 0;; k += 2) {
-      load_tile(A, kr, vr, (uint32_t)(first + k * kStep), tl);
-      if (k > 0) compute_tile(B, first + (k - 1) * kStep, hi, qB0, qB1, scale_log2, S, vt, tl);
+      load_step<1>(A, va, kr, vr, (uint32_t)(first + k * kStep), tl);
+      if (k > 0) compute_step<1>(B, vb, first + (k - 1) * kStep, hi, qB0, qB1, scale_log2, S, tl, lane);
       if (k >= n) break;
-      load_tile(B, kr, vr, (uint32_t)(first + (k + 1) * kStep), tl);
-      compute_tile(A, first + k * kStep, hi, qB0, qB1, scale_log2, S, vt, tl);
+      load_step<1>(B, vb, kr, vr, (uint32_t)(first + (k + 1) * kStep), tl);
+      compute_step<1>(A, va, first + k * kStep, hi, qB0, qB1, scale_log2, S, tl, lane);
       if (k + 1 >= n) break;
     }
   }
+  // The last request past the range still writes (zeros) into LDS when it returns: let it land
+  // before the LDS is reused or the wave ends. s_waitcnt vmcnt(0).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   float m = S.m;
   float lsum = sum_over_groups(S.lsum);
   f32x4 (&o)[4] = S.o;
@@ -112,9 +118,10 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     return;
   }
 
-  // Merge the waves' partials through LDS (the V tiles are dead now).
+  // Merge the waves' partials through LDS (the V tiles are dead now: every wave's DMA has landed).
   __syncthreads();
-  float *mb = reinterpret_cast<float *>(lds);  // [NW][16]
+  static_assert((32 + 16 * kOb) * 4 <= kVTile * 2, "merge buffer exceeds the V tiles");
+  float *mb = reinterpret_cast<float *>(vbA);  // [NW][16]
   float *lb = mb + NW * 16;                     // [NW][16]
   float *ob = lb + NW * 16;                     // [NW][16 heads][64 dims]
   if (g == 0) {

@@ -37,7 +37,10 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
     uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
     float *__restrict__ ml_ws, int b, int nq, int nkv, int group, int tpw, int P,
     float sl2) {
-  __shared__ __attribute__((aligned(16))) uint16_t vts[NW * NT * 64 * kVRow];  // per-wave V^T tiles
+  // V tiles of the two pipeline buffers (NT per wave each); separate arrays, so the compiler tells
+  // their DMA completions apart and waits only for the buffer it reads.
+  __shared__ __attribute__((aligned(16))) uint16_t vbA[NW * NT * kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t vbB[NW * NT * kVTile];
   __shared__ __attribute__((aligned(16))) float mrg[2][NW * (32 + 16 * kOb)];  // per-wave m, l, O (x2)
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -52,7 +55,7 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
   const uint32_t full_row = (uint32_t)cache_len * row_bytes;
   TileLane tl;
   tl.init(lane);
-  uint16_t *vt = vts + w * NT * 64 * kVRow;
+  uint16_t *va = vbA + w * NT * kVTile, *vb = vbB + w * NT * kVTile;
   constexpr int KS = 64 * NT;  // keys per step
   const int spw = tpw / NT;     // steps per wave and chunk
 
@@ -144,11 +147,9 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
       mb[w * 16 + tl.r16] = S.m;
       lb[w * 16 + tl.r16] = lsum;
     }
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-      *reinterpret_cast<f32x4 *>(ob + (w * 16 + tl.r16) * kOb + 16 * dt + 4 * tl.g) = S.o[dt];
+    lds_store_4x16(ob + (w * 16 + tl.r16) * kOb + 4 * tl.g, S.o[0], S.o[1], S.o[2], S.o[3]);
     S.reset();
-    __syncthreads();
+    lds_barrier();  // the next chunk's loads stay in flight
     // every wave merges a share of the (head, dim) outputs; no barrier after: the next chunk writes the
     // other LDS buffer
     for (int idx = tid; idx < group * 64; idx += 64 * NW) {
@@ -186,12 +187,14 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
   Meta mnxt = meta_load(1);
   u32x4 qc0, qc1, qn0, qn1;
   load_q(cur, 0, qc0, qc1);
-  KVTile A[NT], B[NT];
-  load_step<NT>(A, cur.kr, cur.vr, (uint32_t)(cur.lo + KS * w), tl);
+  KTile A[NT], B[NT];
+  load_step<NT>(A, va, cur.kr, cur.vr, (uint32_t)(cur.lo + KS * w), tl);
   int i = 0, j = 0;
   int hi = 0;
   bool fresh = true;  // cur's hi not refined yet
-  auto step = [&](KVTile (&X)[NT], KVTile (&Y)[NT]) -> bool {
+  // always inlined: each call site then sees which V buffer (vbA or vbB) it reads and writes, so the
+  // compiler waits only for that buffer's DMA
+  auto step = [&](KTile (&X)[NT], uint16_t *xv, KTile (&Y)[NT], uint16_t *yv) __attribute__((always_inline)) -> bool {
     // request the tile after (i, j) into Y, then consume X
     const bool last_tile = (j + 1 == spw);
     Meta mnn{0, 0};
@@ -199,16 +202,21 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
       resolve(i + 1, mnxt, /*exact=*/true, nxt);
       mnn = meta_load(i + 2);
       load_q(nxt, i + 1, qn0, qn1);
-      load_step<NT>(Y, nxt.kr, nxt.vr, (uint32_t)(nxt.lo + KS * w), tl);
-    } else {
-      load_step<NT>(Y, cur.kr, cur.vr, (uint32_t)(cur.lo + KS * (w + NW * (j + 1))), tl);
+    }
+    {
+      // one load sequence for both cases (operands selected): with two, the compiler's wait
+      // bookkeeping merges their states conservatively and drains every load in flight
+      const rsrc_t kr = last_tile ? nxt.kr : cur.kr;
+      const rsrc_t vr = last_tile ? nxt.vr : cur.vr;
+      const int tn = last_tile ? nxt.lo + KS * w : cur.lo + KS * (w + NW * (j + 1));
+      load_step<NT>(Y, yv, kr, vr, (uint32_t)tn, tl);
     }
     if (fresh) {
       hi = hi_of(cur, mcur, i);
       fresh = false;
     }
     const int t0 = cur.lo + KS * (w + NW * j);
-    if (t0 < hi) compute_step<NT>(X, t0, hi, qc0, qc1, sl2, S, vt, tl);
+    if (t0 < hi) compute_step<NT>(X, xv, t0, hi, qc0, qc1, sl2, S, tl, lane);
     if (last_tile) {
       const int L = (i < nmine) ? min(max(__builtin_amdgcn_readfirstlane(mcur.lraw), 0), cache_len) : 0;
       const int crow = __builtin_amdgcn_readfirstlane(mcur.craw);
@@ -227,9 +235,12 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
     return true;
   };
   for (;;) {
-    if (!step(A, B)) break;
-    if (!step(B, A)) break;
+    if (!step(A, va, B, vb)) break;
+    if (!step(B, vb, A, va)) break;
   }
+  // the request past the last chunk still writes (zeros) into LDS: let it land before the wave ends.
+  // s_waitcnt vmcnt(0).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
 // Merges the chunks of rows longer than one chunk: one thread per (row, q head, dim); rows that fit one
@@ -295,6 +306,8 @@ extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
   if (group > 16) return set_error(A8_EUNSUP, "decode_attn_stream: GQA group %d > 16 not supported", group);
   if (waves != 1 && waves != 2 && waves != 4 && waves != 8)
     return set_error(A8_EINVAL, "decode_attn_stream: waves must be 1, 2, 4 or 8 (got %d)", waves);
+  if (waves == 8)  // 8 waves' double-buffered V tiles and merge buffers exceed the 160 KB of LDS
+    return set_error(A8_EUNSUP, "decode_attn_stream: 8 waves per workgroup not supported (1, 2 or 4)");
   if (tiles_per_wave < 1 || tiles_per_wave > 64 || grid < 1)
     return set_error(A8_EINVAL, "decode_attn_stream: tiles_per_wave %d / grid %d out of range", tiles_per_wave, grid);
   if (b == 0) return 0;
@@ -323,16 +336,15 @@ extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
   if (phases & 1) {
 #define A8_STREAM_ARGS grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens, rowmap, \
                        oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2
-    // two-tile steps where the tile count allows and the LDS holds them (8 waves x 2 V^T tiles do not fit)
-    const bool nt2 = (tiles_per_wave % 2 == 0) && waves <= 4;
+    // two-tile steps where the tile count allows and the LDS holds them (4 waves x 2 x 2 V tiles and
+    // the merge buffers do not fit in 160 KB)
+    const bool nt2 = (tiles_per_wave % 2 == 0) && waves <= 2;
     switch (waves * 2 + (nt2 ? 1 : 0)) {
       case 2: launch_stream<1, 1>(A8_STREAM_ARGS); break;
       case 3: launch_stream<1, 2>(A8_STREAM_ARGS); break;
       case 4: launch_stream<2, 1>(A8_STREAM_ARGS); break;
       case 5: launch_stream<2, 2>(A8_STREAM_ARGS); break;
-      case 8: launch_stream<4, 1>(A8_STREAM_ARGS); break;
-      case 9: launch_stream<4, 2>(A8_STREAM_ARGS); break;
-      default: launch_stream<8, 1>(A8_STREAM_ARGS); break;
+      default: launch_stream<4, 1>(A8_STREAM_ARGS); break;
     }
 #undef A8_STREAM_ARGS
     const hipError_t e = hipGetLastError();

@@ -137,6 +137,7 @@ def test_decode_stream_rejects_before_launch(a8):
     assert f(*_stream_args(hd=32)) == -3
     assert f(*_stream_args(nq=34)) == -3
     assert f(*_stream_args(waves=5)) == -1
+    assert f(*_stream_args(waves=8)) == -3                          # LDS: 1, 2 or 4 waves
     assert f(*_stream_args(tpw=0)) == -1
     assert f(*_stream_args(grid=0)) == -1
     # 3 rows over a 2048-key cache in 512-key chunks need 3 * 4 row-splits of workspace
