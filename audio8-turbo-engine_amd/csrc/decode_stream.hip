@@ -359,33 +359,39 @@ extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
   return 0;
 }
 
-// Launch shape of a8_decode_attn_stream: chunks of waves * tpw * 64 keys sized so that a unit has a
-// few chunks (enough workgroups to fill the GPU, a narrow address window), the workspace holds
-// b * P row-splits, and a grid of about two workgroups per compute unit.
+// Launch shape of a8_decode_attn_stream. Measured on MI355X (C3, 384 units of 2048 keys): whole-unit
+// chunks swept by 192 workgroups of 4 waves (2 units each, 37.6 us/layer) beat 256 workgroups (40.7,
+// uneven: some take 1 unit, some 2), 384 (one unit each: twice the concurrent streams) and short
+// chunks in address order (more merges). So: a workgroup target of 3/4 of the compute units, chunks
+// per unit only as many as needed to reach it (long rows of few units), and a grid that divides the
+// chunk count evenly. The workspace caps the chunk count per unit.
 extern "C" int a8_decode_choose_stream(int b, int nkv, int cache_len, int64_t cap_row_splits, int n_cu,
                                        int *waves_out, int *tpw_out, int *grid_out) {
   using namespace a8;
   if (b < 1 || nkv < 1 || cache_len < 0 || n_cu < 1 || !waves_out || !tpw_out || !grid_out)
     return set_error(A8_EINVAL, "decode_choose_stream: bad arguments b=%d nkv=%d n_cu=%d", b, nkv, n_cu);
-  const int tiles = cache_len > 0 ? (cache_len + 63) / 64 : 1;
-  int nw = tiles >= 8 ? 4 : tiles >= 4 ? 2 : 1;
-  int tpw = 2;
-  if (tiles < nw * tpw) tpw = 1;
+  const int64_t tiles = cache_len > 0 ? (cache_len + 63) / 64 : 1;
+  const int nw = tiles >= 8 ? 4 : tiles >= 4 ? 2 : 1;
+  const int64_t units = (int64_t)b * nkv;
+  const int64_t g0 = n_cu * 3 / 4 > 0 ? n_cu * 3 / 4 : 1;
+  const int64_t p_want = (g0 + units - 1) / units;
+  int64_t tpw = (tiles + nw * p_want - 1) / (nw * p_want);
+  if (tpw < 1) tpw = 1;
+  if (tpw > 64) tpw = 64;
   // chunk count per unit: at most what the workspace holds
   const int64_t pmax = cap_row_splits >= b ? cap_row_splits / b : 1;
-  while (true) {
-    const int ch = nw * tpw * 64;
-    const int64_t P = cache_len > 0 ? (cache_len + ch - 1) / ch : 1;
-    if (P <= 1 || P <= pmax || tpw >= 64) break;
+  while (tpw < 64) {
+    const int64_t P = (tiles + nw * tpw - 1) / (nw * tpw);
+    if (P <= 1 || P <= pmax) break;
     tpw *= 2;
   }
-  const int ch = nw * tpw * 64;
-  const int64_t P = cache_len > 0 ? (cache_len + ch - 1) / ch : 1;
-  const int64_t NC = (int64_t)b * nkv * P;
-  int64_t grid = (int64_t)n_cu * (nw >= 4 ? 2 : 4);
-  if (grid > NC) grid = NC;
+  if (tpw > 64) tpw = 64;
+  const int64_t P = (tiles + nw * tpw - 1) / (nw * tpw);
+  const int64_t NC = units * P;
+  const int64_t per = (NC + g0 - 1) / g0;  // chunks per workgroup
+  const int64_t grid = (NC + per - 1) / per;
   *waves_out = nw;
-  *tpw_out = tpw;
+  *tpw_out = (int)tpw;
   *grid_out = (int)grid;
   return 0;
 }

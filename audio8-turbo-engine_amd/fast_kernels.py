@@ -114,12 +114,15 @@ class DecodeAttention:
     (fast_kernels.py:256-269).
 
     Two launch schedules compute the same softmax (split boundaries are not part of the contract):
-      mode "split" (default): a8_decode_attn -- the reference's split kernel + combine kernel structure,
-        launch shape from a8_decode_choose for this GPU's compute-unit count; the caller's `nsplit` is a
-        lower bound on the splits (policy "auto") or exact (policy "caller").
-      mode "stream": a8_decode_attn_stream -- a persistent kernel that sweeps the cache in address order
-        in fixed-size key chunks, plus a small merge kernel for rows longer than a chunk; launch shape
-        from a8_decode_choose_stream."""
+      mode "split": a8_decode_attn -- the reference's split kernel + combine kernel structure, launch
+        shape from a8_decode_choose for this GPU's compute-unit count; the caller's `nsplit` is a lower
+        bound on the splits (policy "auto") or exact (policy "caller").
+      mode "stream": a8_decode_attn_stream -- a persistent kernel that takes fixed-size key chunks in
+        turn (whole rows when there are enough of them), plus a small merge kernel for rows longer than
+        a chunk; launch shape from a8_decode_choose_stream.
+      mode "auto" (default): "stream" when every workgroup of its grid gets at least two whole units
+        (row, kv head) of 1024+ keys -- the peak-load shape, where it is measured faster -- else
+        "split" (short, few or ragged rows, where its per-row split sizes win)."""
 
     def __init__(self, cap_row_splits, nq, nkv, hd, nsplit_max, device, scale=None):
         self.nq, self.nkv, self.hd = nq, nkv, hd
@@ -132,7 +135,7 @@ class DecodeAttention:
         self.ml_flat = torch.empty(self.cap * nq * 2, dtype=torch.float32, device=device)
         dev = torch.device(device)
         self.n_cu = torch.cuda.get_device_properties(dev).multi_processor_count if dev.type == "cuda" else 1
-        self.mode = "split"
+        self.mode = "auto"
         self.policy = "auto"
         self.force_shape = None   # split mode: (nsplit, waves) pins the launch shape (tuning / tests)
         self.force_stream = None  # stream mode: (waves, tiles_per_wave, grid)
@@ -170,6 +173,23 @@ class DecodeAttention:
         self._shapes[key] = (nw.value, tpw.value, grid.value)
         return self._shapes[key]
 
+    def schedule(self, b: int, cache_len: int, nsplit: int = 1):
+        """The schedule a call with b rows over a cache of cache_len positions uses:
+        ("stream", (waves, tiles_per_wave, grid)) or ("split", (nsplit, waves))."""
+        if self.force_shape is None and (self.force_stream is not None or self.mode == "stream" or
+                                         (self.mode == "auto" and self._stream_pays(b, cache_len))):
+            return "stream", self.stream_shape(b, cache_len)
+        nsplit = max(1, min(int(nsplit), self.nsplit_max))
+        return "split", self.launch_shape(b, cache_len, nsplit)
+
+    def _stream_pays(self, b: int, cache_len: int) -> bool:
+        """Mode "auto": the streaming schedule for many long rows (see the class docstring)."""
+        if cache_len < 1024:
+            return False
+        nw, tpw, grid = self.stream_shape(b, cache_len)
+        whole = nw * tpw * 64 >= cache_len
+        return whole and b * self.nkv >= 2 * grid
+
     def __call__(self, q, kc, vc, lens, out, nsplit=1, bn=64, rowmap=None, phases=3):
         """q: [b, nq, hd]; kc/vc: [rows, nkv, S, hd]; query row i reads cache row rowmap[i]
         (identity when rowmap is None); lens: [b] int32 (keys [0, lens) attended); out: [b, nq, hd]
@@ -199,13 +219,14 @@ class DecodeAttention:
                   kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
                   lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None,
                   out.data_ptr(), out.stride(0), out.stride(1), self.acc_flat.data_ptr(), self.ml_flat.data_ptr())
-        if (self.mode == "stream" or self.force_stream is not None) and self.force_shape is None:
-            nw, tpw, grid = self.stream_shape(b, kc.shape[2])
+        kind, shape = self.schedule(b, kc.shape[2], nsplit)
+        if kind == "stream":
+            nw, tpw, grid = shape
             st = lib.a8_decode_attn_stream(*common, self.cap, b, self.nq, self.nkv, self.hd, nw, tpw, grid,
                                            float(self.scale), int(phases), _lib.stream_of(q))
             _lib.check(st, "decode_attention")
             return out
-        ns, nw = self.launch_shape(b, kc.shape[2], nsplit)
+        ns, nw = shape
         st = lib.a8_decode_attn(*common, self.cap, b, self.nq, self.nkv, self.hd, ns, nw, float(self.scale),
                                 int(phases), _lib.stream_of(q))
         _lib.check(st, "decode_attention")

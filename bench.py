@@ -16,6 +16,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -39,6 +40,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
     p.add_argument("--shape", default=None, help="use the split + combine kernels at NSPLIT,WAVES")
     p.add_argument("--stream-shape", default=None, help="force the streaming kernel's WAVES,TILES_PER_WAVE,GRID")
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="only launch one layer's decode 4x and a 256 MiB copy (target of rocprofv3 --pmc passes)")
     return p.parse_args()
 
 
@@ -123,6 +126,37 @@ def cpu_baseline(w, budget_s):
             "sample": f"1 of {LAYERS} layers (store + decode, {b} slots, same inputs), {len(times)} reps, median"}
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c3_traffic.md")
+
+
+def measured_traffic(cfg, launch):
+    """HBM bytes per launch of the decode kernel, from the rocprofv3 FETCH_SIZE / WRITE_SIZE passes over
+    `bench.py --traffic-probe` summarised in profiles/decode_c3_traffic.md (counters cannot be read from
+    inside a timed run); None when that summary is absent or was taken at another config or launch shape."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    fields = dict(m.groups() for m in re.finditer(r"^- (\w+): `?([^`\n]+)`?$", text, re.M))
+    if fields.get("config") != cfg or fields.get("launch") != json.dumps(launch, sort_keys=True):
+        return None
+    return int(fields["traffic_bytes_per_launch"])
+
+
+def traffic_probe(torch, st, w, nsplit_req):
+    """Counter target for the traffic measurement: 4 launches of one layer's decode (the bench's launch
+    shape) and a plain 256 MiB elementwise copy (read 256 MiB, write 256 MiB) that calibrates
+    FETCH_SIZE / WRITE_SIZE to bytes. Run under rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE."""
+    for _ in range(4):
+        st.attn(w["q"], st.kc[0], st.vc[0], w["lens"], w["outs"][0], nsplit=nsplit_req)
+    x = torch.ones(64 << 20, dtype=torch.float32, device=w["q"].device)
+    y = torch.empty_like(x)
+    for _ in range(2):
+        torch.add(x, 0.0, out=y)
+    torch.cuda.synchronize()
+    print("traffic probe: 4 decode launches, 2 copies of 268435456 bytes", flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -145,14 +179,18 @@ def main():
     if args.stream_shape:
         st.attn.force_stream = tuple(int(x) for x in args.stream_shape.split(","))
     nsplit_req = a8.ref_nsplit(b, NKV)
-    if st.attn.mode == "stream" and st.attn.force_shape is None:
-        nw, tpw, grid = st.attn.stream_shape(b, w["S"])
+    kind, shape = st.attn.schedule(b, w["S"], nsplit_req)
+    if kind == "stream":
+        nw, tpw, grid = shape
         chunks = -(-w["S"] // (nw * tpw * 64))
         launch = {"kernel": "k_decode_stream" + (" + k_decode_stream_combine" if chunks > 1 else ""), "waves": nw,
                   "tiles_per_wave": tpw, "grid": grid, "chunk_keys": nw * tpw * 64, "chunks_per_row": chunks}
     else:
-        ns, nw = st.attn.launch_shape(b, w["S"], nsplit_req)
+        ns, nw = shape
         launch = {"kernel": "k_decode_split" + ("" if ns == 1 else " + k_decode_combine"), "nsplit": ns, "waves": nw}
+    if args.traffic_probe:
+        traffic_probe(torch, st, w, nsplit_req)
+        return
 
     def tick():
         st.forward(w["qkv"], w["bias"], w["pos"], w["slot"], w["lens"], nsplit=nsplit_req, rowmap=False, q=w["q"],
@@ -174,6 +212,7 @@ def main():
     g_sto = capture(torch, store_only)
     ms_sto = time_graph(torch, g_sto, args.steps, args.warmup)
 
+    traffic = measured_traffic(args.config, launch)
     lens = w["lens_h"].tolist()
     layer_bytes = ref_counts.decode_bytes(lens, NQ, NKV, HD)                  # store + decode, algorithmic
     dec_bytes = ref_counts.decode_bytes(lens, NQ, NKV, HD, with_store=False)  # K+V read + q in + out
@@ -195,7 +234,7 @@ def main():
         "store_us_per_layer": round(ms_sto * 1e3 / LAYERS, 3),
         "roofline": {"bound": "hbm", "kernel": launch["kernel"],
                      "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_per_launch": dec_bytes, "us_per_launch": round(dec_us, 3)},
         "device": {"name": props.name, "arch": getattr(props, "gcnArchName", ""), "cus": props.multi_processor_count},
     }

@@ -165,7 +165,10 @@ def test_decode_choose_stream_contract(a8):
                 P = -(-S // ch)
                 assert P == 1 or b * P <= cap or tpw >= 64     # fits the workspace
                 assert grid <= b * 2 * P                          # no idle workgroups
-    # the peak-load config gets several chunks per row (address-order sweep) on a ~2-per-CU grid
-    nw, tpw, grid = _choose_stream(lib, 192)
-    assert -(-2048 // (nw * tpw * 64)) >= 2 and grid <= 2 * 256
-    assert _choose_stream(lib, 384, S=10, cap=384) == (1, 1, 768)
+    # the peak-load config: whole-unit chunks, two per workgroup of 4 waves on 192 workgroups
+    assert _choose_stream(lib, 192) == (4, 8, 192)
+    # tiny caches: one wave, one tile, four units per workgroup
+    assert _choose_stream(lib, 384, S=10, cap=384) == (1, 1, 192)
+    # a single long row is cut into chunks to occupy the GPU
+    nw, tpw, grid = _choose_stream(lib, 1, S=2048)
+    assert -(-2048 // (nw * tpw * 64)) >= 8 and grid >= 8
