@@ -67,9 +67,15 @@ class AttnStack:
         self.kc = list(self.kc_all.unbind(0))
         self.vc = list(self.vc_all.unbind(0))
         self.attn = DecodeAttention(max_rows, nq, nkv, hd, nsplit_max, dev)
+        # decode with rowmap = slot: store and attend in one launch where the schedule allows
+        # (DecodeAttention.store_and_attend); False keeps the two calls
+        self.fuse = True
 
     def layer(self, i, qkv, bias, pos, slot, lens, q, o, nsplit=1, rowmap=True, plan=None):
         """Layer i's attention (fast_engine.py:127-132): store, then attend. q / o: [R, nq, hd] buffers."""
+        if plan is None and rowmap and self.fuse:
+            return self.attn.store_and_attend(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
+                                              lens, o, nsplit=nsplit, ring=self.ring)
         bias_rope_store(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
                         self.nq, self.nkv, self.hd, ring=self.ring)
         if plan is not None:

@@ -24,19 +24,39 @@
 //     saturated memory system each of those round trips waits microseconds in the same queues the
 //     KV stream fills, which costs far more than the extra launch.
 #include "decode_tile.h"
+#include "rope.h"
 
 namespace a8 {
 
+// Inputs of the fused store (a8_store_decode_stream): the bias_rope_store arguments the decode does not
+// already take. The query row r's cache row is slot[r] (the decode's row map).
+struct StoreIn {
+  const uint16_t *qkv;
+  int64_t s_qkv;
+  const uint16_t *bias;  // nullptr: no bias
+  const uint16_t *cos_tab, *sin_tab;
+  int64_t s_cs;
+  int n_tab;
+  const int32_t *pos;
+  uint16_t *qo;  // nullptr: q is not written out
+  int64_t s_qo_r, s_qo_h;
+  int ring;
+};
+
 // NT = 64-key tiles per pipeline step (decode_tile.h compute_step); tpw is a multiple of NT. With
-// NT = 2 a wave holds two 128-key steps in registers (one wave per SIMD, up to 512 VGPRs).
-template <int NW, int NT>
-__global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
+// NT = 2, or FUSED (the next chunk's qkv / bias / table chunks are held in registers), a wave may use
+// up to 512 registers (one wave per SIMD).
+// FUSED: q and the new k / v come from qkv + bias + RoPE (rope.h, the store kernel's arithmetic) at each
+// chunk's first step instead of from q; the unit's first chunk stores k / v (and q) like
+// k_bias_rope_store, and the tile holding the new key column takes it from registers.
+template <int NW, int NT, bool FUSED>
+__global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode_stream(
     const uint16_t *__restrict__ q, int64_t s_qb, int64_t s_qh,
-    const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+    uint16_t *kc, uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,  // written when FUSED
     int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
     uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
     float *__restrict__ ml_ws, int b, int nq, int nkv, int group, int tpw, int P,
-    float sl2) {
+    float sl2, StoreIn si) {
   // V tiles of the two pipeline buffers (NT per wave each); separate arrays, so the compiler tells
   // their DMA completions apart and waits only for the buffer it reads.
   __shared__ __attribute__((aligned(16))) uint16_t vbA[NW * NT * kVTile];
@@ -69,7 +89,7 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
   // first tile is requested. For the first chunk only the cache row is needed up front: its tiles
   // are requested over the whole cache row and keys past the length are masked when computed.
   struct Meta {
-    int lraw, craw;
+    int lraw, craw, praw;
   };
   auto ids = [&](int i, Chunk &k) {
     const int c = (int)blockIdx.x + i * G;
@@ -81,13 +101,15 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
   };
   const rsrc_t lens_r = make_rsrc(lens, (uint32_t)b * 4u);
   const rsrc_t map_r = make_rsrc(rowmap, rowmap ? (uint32_t)b * 4u : 0u);
+  const rsrc_t pos_r = make_rsrc(si.pos, FUSED ? (uint32_t)b * 4u : 0u);
   auto meta_load = [&](int i) {
-    Meta m{0, 0};
+    Meta m{0, 0, 0};
     if (i < nmine) {
       Chunk k;
       ids(i, k);
       m.lraw = bld4(lens_r, (uint32_t)k.row * 4u);
       m.craw = rowmap ? bld4(map_r, (uint32_t)k.row * 4u) : k.row;
+      if (FUSED) m.praw = bld4(pos_r, (uint32_t)k.row * 4u);
     }
     return m;
   };
@@ -124,6 +146,75 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
     const uint32_t qo = (uint32_t)(tl.r16 * s_qh * 2) + 16u * tl.g;
     q0 = bld16(qr, qo);
     q1 = bld16(qr, qo + 64u);
+  };
+  // FUSED: one head per lane -- lanes r16 < group the q heads kh*group + r16, lane kLaneK the k head,
+  // lane kLaneV the v head of the chunk's row -- and its partner chunks (dims 8g.., 32+8g..) of qkv and
+  // bias, plus the position's cos / sin chunks, requested one chunk ahead like q; rows / positions that
+  // do not exist read zeros.
+  struct QkvRaw {
+    u32x4 w[2], bb[2], cs[2], sn[2];
+  };
+  const int H = nq + 2 * nkv;
+  auto lane_head = [&](const Chunk &k) {
+    return tl.r16 < group ? k.kh * group + tl.r16
+                          : tl.r16 == kLaneK ? nq + k.kh : tl.r16 == kLaneV ? nq + nkv + k.kh : 0;
+  };
+  auto load_qkv = [&](const Chunk &k, int i, const Meta &m, QkvRaw &r) {
+    const bool live = i < nmine;
+    const int p = __builtin_amdgcn_readfirstlane(m.praw);
+    const bool pv = live && p >= 0 && p < si.n_tab;
+    const rsrc_t xr = make_rsrc_wave(si.qkv + (int64_t)(live ? k.row : 0) * si.s_qkv, live ? (uint32_t)H * 128u : 0u);
+    const rsrc_t br = make_rsrc(si.bias, si.bias ? (uint32_t)H * 128u : 0u);
+    const rsrc_t cr = make_rsrc_wave(si.cos_tab + (int64_t)(pv ? p : 0) * si.s_cs, pv ? 128u : 0u);
+    const rsrc_t sr = make_rsrc_wave(si.sin_tab + (int64_t)(pv ? p : 0) * si.s_cs, pv ? 128u : 0u);
+    const uint32_t og = 16u * tl.g, ho = (uint32_t)lane_head(k) * 128u + og;
+    r.w[0] = bld16(xr, ho);
+    r.w[1] = bld16(xr, ho + 64u);
+    r.bb[0] = bld16(br, ho);
+    r.bb[1] = bld16(br, ho + 64u);
+    r.cs[0] = bld16(cr, og);
+    r.cs[1] = bld16(cr, og + 64u);
+    r.sn[0] = bld16(sr, og);
+    r.sn[1] = bld16(sr, og + 64u);
+  };
+  // FUSED, at a chunk's first step: one RoPE pass per lane gives q (lanes r16 < group: the Q^T operand),
+  // the new k (lane kLaneK) and v (lane kLaneV: x narrowed, not rotated); the key column they replace;
+  // the unit's first chunk (wave 0) writes k / v to the cache and q to qo, as k_bias_rope_store would.
+  KVPatch pt;
+  pt.col = -1;
+  auto apply_qkv = [&](const Chunk &k, int i, const Meta &m, const QkvRaw &r, u32x4 &q0, u32x4 &q1) {
+    const bool live = i < nmine;
+    const int p = __builtin_amdgcn_readfirstlane(m.praw);
+    const bool pv = live && p >= 0 && p < si.n_tab;
+    const int crow = __builtin_amdgcn_readfirstlane(m.craw);
+    const int sidx = pv ? p % si.ring : 0;
+    const bool store_ok = pv && crow >= 0 && crow < cache_rows && sidx < cache_len;
+    float xl[8], xh[8], ol[8], oh[8];
+    rope_x(r.w[0], r.w[1], r.bb[0], r.bb[1], si.bias != nullptr, xl, xh);
+    rope_rotate_f(xl, xh, r.cs[0], r.cs[1], r.sn[0], r.sn[1], ol, oh);
+    const bool vlane = tl.r16 == kLaneV;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ol[j] = vlane ? xl[j] : ol[j];
+      oh[j] = vlane ? xh[j] : oh[j];
+    }
+    rope_narrow(ol, oh, pt.lo, pt.hi);
+    const bool qlive = pv && tl.r16 < group;
+    const u32x4 z{0u, 0u, 0u, 0u};
+    q0 = qlive ? pt.lo : z;  // unknown position: the reference reads no table row; q is zero here
+    q1 = qlive ? pt.hi : z;
+    pt.col = store_ok ? sidx : -1;
+    if (k.part == 0 && w == 0) {
+      uint16_t *dst = nullptr;
+      if (store_ok && (tl.r16 == kLaneK || vlane))
+        dst = (vlane ? vc : kc) + (int64_t)crow * s_kb + (int64_t)k.kh * s_kh + (int64_t)sidx * s_ks;
+      else if (si.qo && qlive)
+        dst = si.qo + (int64_t)k.row * si.s_qo_r + (int64_t)(k.kh * group + tl.r16) * si.s_qo_h;
+      if (dst) {
+        st16(dst + 8 * tl.g, pt.lo);
+        st16(dst + 32 + 8 * tl.g, pt.hi);
+      }
+    }
   };
 
   SoftmaxState S;
@@ -186,7 +277,11 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
   resolve(0, mcur, /*exact=*/false, cur);
   Meta mnxt = meta_load(1);
   u32x4 qc0, qc1, qn0, qn1;
-  load_q(cur, 0, qc0, qc1);
+  QkvRaw rc, rn;
+  if (FUSED)
+    load_qkv(cur, 0, mcur, rc);
+  else
+    load_q(cur, 0, qc0, qc1);
   KTile A[NT], B[NT];
   load_step<NT>(A, va, cur.kr, cur.vr, (uint32_t)(cur.lo + KS * w), tl);
   int i = 0, j = 0;
@@ -201,7 +296,10 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
     if (last_tile) {
       resolve(i + 1, mnxt, /*exact=*/true, nxt);
       mnn = meta_load(i + 2);
-      load_q(nxt, i + 1, qn0, qn1);
+      if (FUSED)
+        load_qkv(nxt, i + 1, mnxt, rn);
+      else
+        load_q(nxt, i + 1, qn0, qn1);
     }
     {
       // one load sequence for both cases (operands selected): with two, the compiler's wait
@@ -213,10 +311,11 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
     }
     if (fresh) {
       hi = hi_of(cur, mcur, i);
+      if (FUSED) apply_qkv(cur, i, mcur, rc, qc0, qc1);
       fresh = false;
     }
     const int t0 = cur.lo + KS * (w + NW * j);
-    if (t0 < hi) compute_step<NT>(X, xv, t0, hi, qc0, qc1, sl2, S, tl, lane);
+    if (t0 < hi) compute_step<NT, FUSED>(X, xv, t0, hi, qc0, qc1, sl2, S, tl, lane, &pt);
     if (last_tile) {
       const int L = (i < nmine) ? min(max(__builtin_amdgcn_readfirstlane(mcur.lraw), 0), cache_len) : 0;
       const int crow = __builtin_amdgcn_readfirstlane(mcur.craw);
@@ -226,8 +325,12 @@ __global__ __launch_bounds__(64 * NW, NT == 1 ? 2 : 1) void k_decode_stream(
       cur = nxt;
       mcur = mnxt;
       mnxt = mnn;
-      qc0 = qn0;
-      qc1 = qn1;
+      if (FUSED) {
+        rc = rn;
+      } else {
+        qc0 = qn0;
+        qc1 = qn1;
+      }
       fresh = true;
       return i < nmine;
     }
@@ -274,77 +377,78 @@ __global__ __launch_bounds__(256) void k_decode_stream_combine(
   out[(int64_t)row * s_ob + (int64_t)h * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
 }
 
-template <int NW, int NT>
-static void launch_stream(int grid, size_t shm, hipStream_t st, const uint16_t *q, int64_t s_qb, int64_t s_qh,
-                          const uint16_t *kc, const uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
-                          int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap, uint16_t *out,
-                          int64_t s_ob, int64_t s_oh, float *acc_ws, float *ml_ws, int b, int nq, int nkv,
-                          int group, int tpw, int P, float sl2) {
-  auto kern = k_decode_stream<NW, NT>;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), shm, st, q, s_qb, s_qh, kc, vc, s_kb, s_kh,
-                     s_ks, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv,
-                     group, tpw, P, sl2);
+template <int NW, int NT, bool FUSED>
+static void launch_stream(int grid, hipStream_t st, const uint16_t *q, int64_t s_qb, int64_t s_qh, uint16_t *kc,
+                          uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks, int cache_rows, int cache_len,
+                          const int32_t *lens, const int32_t *rowmap, uint16_t *out, int64_t s_ob, int64_t s_oh,
+                          float *acc_ws, float *ml_ws, int b, int nq, int nkv, int group, int tpw, int P, float sl2,
+                          const StoreIn &si) {
+  auto kern = k_decode_stream<NW, NT, FUSED>;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), 0, st, q, s_qb, s_qh, kc, vc, s_kb, s_kh, s_ks, cache_rows,
+                     cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tpw, P, sl2, si);
 }
 
 static inline bool al16s(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-}  // namespace a8
-
-extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
-                                     const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
-                                     int cache_rows, int cache_len,
-                                     const int32_t *lens, const int32_t *rowmap,
-                                     void *out, int64_t s_ob, int64_t s_oh,
-                                     float *acc_ws, float *ml_ws, int64_t ws_row_splits,
-                                     int b, int nq, int nkv, int hd, int waves, int tiles_per_wave, int grid,
-                                     float scale, int phases, void *stream) {
-  using namespace a8;
-  if (hd != 64) return set_error(A8_EUNSUP, "decode_attn_stream: head_dim %d not supported (64 only)", hd);
+// Body of a8_decode_attn_stream and a8_store_decode_stream (fused = si.qkv != nullptr: q is unused and
+// rowmap is the store's slot array). Checks the decode arguments, launches the streaming kernel and,
+// for rows longer than a chunk, the merge kernel.
+static int stream_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh, void *kc, void *vc,
+                        int64_t s_kb, int64_t s_kh, int64_t s_ks, int cache_rows, int cache_len,
+                        const int32_t *lens, const int32_t *rowmap, void *out, int64_t s_ob, int64_t s_oh,
+                        float *acc_ws, float *ml_ws, int64_t ws_row_splits, int b, int nq, int nkv, int hd,
+                        int waves, int tiles_per_wave, int grid, float scale, int phases, const StoreIn &si,
+                        void *stream) {
+  const bool fused = si.qkv != nullptr;
+  if (hd != 64) return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64 only)", fn, hd);
   if (b < 0 || nq <= 0 || nkv <= 0 || nq % nkv || cache_rows < 0 || cache_len < 0)
-    return set_error(A8_EINVAL, "decode_attn_stream: bad sizes b=%d nq=%d nkv=%d", b, nq, nkv);
+    return set_error(A8_EINVAL, "%s: bad sizes b=%d nq=%d nkv=%d", fn, b, nq, nkv);
   const int group = nq / nkv;
-  if (group > 16) return set_error(A8_EUNSUP, "decode_attn_stream: GQA group %d > 16 not supported", group);
+  if (group > 16) return set_error(A8_EUNSUP, "%s: GQA group %d > 16 not supported", fn, group);
   if (waves != 1 && waves != 2 && waves != 4 && waves != 8)
-    return set_error(A8_EINVAL, "decode_attn_stream: waves must be 1, 2, 4 or 8 (got %d)", waves);
+    return set_error(A8_EINVAL, "%s: waves must be 1, 2, 4 or 8 (got %d)", fn, waves);
   if (waves == 8)  // 8 waves' double-buffered V tiles and merge buffers exceed the 160 KB of LDS
-    return set_error(A8_EUNSUP, "decode_attn_stream: 8 waves per workgroup not supported (1, 2 or 4)");
+    return set_error(A8_EUNSUP, "%s: 8 waves per workgroup not supported (1, 2 or 4)", fn);
   if (tiles_per_wave < 1 || tiles_per_wave > 64 || grid < 1)
-    return set_error(A8_EINVAL, "decode_attn_stream: tiles_per_wave %d / grid %d out of range", tiles_per_wave, grid);
+    return set_error(A8_EINVAL, "%s: tiles_per_wave %d / grid %d out of range", fn, tiles_per_wave, grid);
   if (b == 0) return 0;
-  if (!q || !kc || !vc || !lens || !out) return set_error(A8_EINVAL, "decode_attn_stream: null pointer");
+  if ((!fused && !q) || !kc || !vc || !lens || !out) return set_error(A8_EINVAL, "%s: null pointer", fn);
   const int CH = waves * tiles_per_wave * 64;
   const int P = cache_len > 0 ? (cache_len + CH - 1) / CH : 1;
   const int64_t NC = (int64_t)b * nkv * P;
-  if (NC > (1ll << 30)) return set_error(A8_EINVAL, "decode_attn_stream: too many chunks");
+  if (NC > (1ll << 30)) return set_error(A8_EINVAL, "%s: too many chunks", fn);
   if (P > 1 && (!acc_ws || !ml_ws || (int64_t)b * P > ws_row_splits))
-    return set_error(A8_EWSPACE, "decode_attn_stream: workspace holds %lld row-splits, need b*%d = %lld",
+    return set_error(A8_EWSPACE, "%s: workspace holds %lld row-splits, need b*%d = %lld", fn,
                      (long long)ws_row_splits, P, (long long)b * P);
   if (s_ks != hd)
-    return set_error(A8_EUNSUP, "decode_attn_stream: cache positions must be contiguous rows (s_ks %lld)",
-                     (long long)s_ks);
-  if (!al16s(q) || !al16s(kc) || !al16s(vc) || !al16s(out) || (P > 1 && !al16s(acc_ws)) ||
-      (s_qb | s_qh | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
-    return set_error(A8_EALIGN, "decode_attn_stream: pointers must be 16-byte aligned and strides multiples of 8");
+    return set_error(A8_EUNSUP, "%s: cache positions must be contiguous rows (s_ks %lld)", fn, (long long)s_ks);
+  if ((!fused && !al16s(q)) || !al16s(kc) || !al16s(vc) || !al16s(out) || (P > 1 && !al16s(acc_ws)) ||
+      ((fused ? 0 : (s_qb | s_qh)) | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
+    return set_error(A8_EALIGN, "%s: pointers must be 16-byte aligned and strides multiples of 8", fn);
   if (grid > NC) grid = (int)NC;
-  const size_t shm = 0;
   const hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;
   const auto *qq = (const uint16_t *)q;
-  const auto *kk = (const uint16_t *)kc;
-  const auto *vv = (const uint16_t *)vc;
+  auto *kk = (uint16_t *)kc;
+  auto *vv = (uint16_t *)vc;
   auto *oo = (uint16_t *)out;
   if (phases & 1) {
-#define A8_STREAM_ARGS grid, shm, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens, rowmap, \
-                       oo, s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2
+#define A8_STREAM_ARGS grid, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens, rowmap, oo, \
+                       s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2, si
     // two-tile steps where the tile count allows and the LDS holds them (4 waves x 2 x 2 V tiles and
     // the merge buffers do not fit in 160 KB)
     const bool nt2 = (tiles_per_wave % 2 == 0) && waves <= 2;
-    switch (waves * 2 + (nt2 ? 1 : 0)) {
-      case 2: launch_stream<1, 1>(A8_STREAM_ARGS); break;
-      case 3: launch_stream<1, 2>(A8_STREAM_ARGS); break;
-      case 4: launch_stream<2, 1>(A8_STREAM_ARGS); break;
-      case 5: launch_stream<2, 2>(A8_STREAM_ARGS); break;
-      default: launch_stream<4, 1>(A8_STREAM_ARGS); break;
+    switch ((waves * 2 + (nt2 ? 1 : 0)) * 2 + (fused ? 1 : 0)) {
+      case 4: launch_stream<1, 1, false>(A8_STREAM_ARGS); break;
+      case 5: launch_stream<1, 1, true>(A8_STREAM_ARGS); break;
+      case 6: launch_stream<1, 2, false>(A8_STREAM_ARGS); break;
+      case 7: launch_stream<1, 2, true>(A8_STREAM_ARGS); break;
+      case 8: launch_stream<2, 1, false>(A8_STREAM_ARGS); break;
+      case 9: launch_stream<2, 1, true>(A8_STREAM_ARGS); break;
+      case 10: launch_stream<2, 2, false>(A8_STREAM_ARGS); break;
+      case 11: launch_stream<2, 2, true>(A8_STREAM_ARGS); break;
+      case 17: launch_stream<4, 1, true>(A8_STREAM_ARGS); break;
+      default: launch_stream<4, 1, false>(A8_STREAM_ARGS); break;
     }
 #undef A8_STREAM_ARGS
     const hipError_t e = hipGetLastError();
@@ -357,6 +461,63 @@ extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
     return (int)hipGetLastError();
   }
   return 0;
+}
+
+}  // namespace a8
+
+extern "C" int a8_decode_attn_stream(const void *q, int64_t s_qb, int64_t s_qh,
+                                     const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                                     int cache_rows, int cache_len,
+                                     const int32_t *lens, const int32_t *rowmap,
+                                     void *out, int64_t s_ob, int64_t s_oh,
+                                     float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                                     int b, int nq, int nkv, int hd, int waves, int tiles_per_wave, int grid,
+                                     float scale, int phases, void *stream) {
+  using namespace a8;
+  const StoreIn none{};
+  return stream_entry("decode_attn_stream", q, s_qb, s_qh, const_cast<void *>(kc), const_cast<void *>(vc), s_kb,
+                      s_kh, s_ks, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws,
+                      ws_row_splits, b, nq, nkv, hd, waves, tiles_per_wave, grid, scale, phases, none, stream);
+}
+
+extern "C" int a8_store_decode_stream(const void *qkv, int64_t s_qkv, const void *bias,
+                                      const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab,
+                                      const int32_t *pos, const int32_t *slot,
+                                      void *qo, int64_t s_qo_r, int64_t s_qo_h,
+                                      void *kc, void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                                      int cache_rows, int cache_len, const int32_t *lens,
+                                      void *out, int64_t s_ob, int64_t s_oh,
+                                      float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                                      int b, int nq, int nkv, int hd, int ring, int waves, int tiles_per_wave,
+                                      int grid, float scale, int phases, void *stream) {
+  using namespace a8;
+  if (ring <= 0 || n_tab < 0) return set_error(A8_EINVAL, "store_decode_stream: bad ring %d / n_tab %d", ring, n_tab);
+  if (b > 0 && (!qkv || !cos_tab || !sin_tab || !pos || !slot))
+    return set_error(A8_EINVAL, "store_decode_stream: null pointer");
+  if (b > 0 && (!al16s(qkv) || !al16s(cos_tab) || !al16s(sin_tab) || (bias && !al16s(bias)) || (qo && !al16s(qo)) ||
+                (s_qkv | s_cs | (qo ? (s_qo_r | s_qo_h) : 0)) & 7))
+    return set_error(A8_EALIGN, "store_decode_stream: pointers must be 16-byte aligned and strides multiples of 8");
+  if (nkv > 0 && nq / nkv > kLaneK)  // lanes kLaneK / kLaneV compute k / v next to the q heads
+    return set_error(A8_EUNSUP, "store_decode_stream: GQA group %d > %d not supported", nq / nkv, kLaneK);
+  if (b > 0 && (phases & 1) == 0)  // the store is part of the streaming kernel
+    return set_error(A8_EINVAL, "store_decode_stream: phases must include the streaming kernel (bit 0)");
+  StoreIn si{};
+  si.qkv = (const uint16_t *)qkv;
+  si.s_qkv = s_qkv;
+  si.bias = (const uint16_t *)bias;
+  si.cos_tab = (const uint16_t *)cos_tab;
+  si.sin_tab = (const uint16_t *)sin_tab;
+  si.s_cs = s_cs;
+  si.n_tab = n_tab;
+  si.pos = pos;
+  si.qo = (uint16_t *)qo;
+  si.s_qo_r = s_qo_r;
+  si.s_qo_h = s_qo_h;
+  si.ring = ring;
+  if (b == 0) return 0;
+  return stream_entry("store_decode_stream", nullptr, 0, 0, kc, vc, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
+                      slot, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, b, nq, nkv, hd, waves, tiles_per_wave,
+                      grid, scale, phases, si, stream);
 }
 
 // Launch shape of a8_decode_attn_stream. Measured on MI355X (C3, 384 units of 2048 keys): whole-unit

@@ -139,14 +139,62 @@ __device__ __forceinline__ void zero_rows(uint16_t *vtile, int from, int lane) {
   }
 }
 
+// One key column whose K / V in the cache are being replaced in this launch (the fused store + decode):
+// the tile holding it takes the new row from registers, whatever its loads returned. lo / hi are dims
+// 8g.. and 32+8g.. of a lane's RoPE result: lane (r16 = kLaneK, g) holds the new k, lane (kLaneV, g) the
+// new v. col < 0: no column.
+constexpr int kLaneK = 14, kLaneV = 15;
+struct KVPatch {
+  int col;
+  u32x4 lo, hi;
+};
+
+// Replaces key column pt.col (when it lies in [t0, t0 + 64 NT)) in the tiles: its K row in the four
+// lanes that hold it (ka[c][t][*] of lanes r16 = 4 (r / 8) + r % 4, r = column % 32; the k comes from
+// lane kLaneK of the same group by a shuffle), its V row in the LDS tile (chunks permuted as the DMA
+// placed them, written by the kLaneV lanes). The LDS write follows the tile's DMA.
+template <int NT>
+__device__ __forceinline__ void patch_column(KTile (&T)[NT], uint16_t *vbuf, int t0, const KVPatch &pt,
+                                             const TileLane &L) {
+  const int kk = pt.col - t0;
+  if (kk < 0 || kk >= 64 * NT) return;
+  const int h = kk >> 6, r64 = kk & 63, cc = r64 >> 5, rr = r64 & 31;
+  const int r16s = 4 * (rr >> 3) + (rr & 3), ts = (rr >> 2) & 1;
+  const int src = 16 * L.g + kLaneK;
+  u32x4 klo, khi;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    klo[e] = (uint32_t)__shfl((int)pt.lo[e], src);
+    khi[e] = (uint32_t)__shfl((int)pt.hi[e], src);
+  }
+  const bool mine = L.r16 == r16s;
+#pragma unroll
+  for (int hh = 0; hh < NT; ++hh)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bool sel = mine && hh == h && c == cc && t == ts;
+        T[hh].ka[c][t][0] = sel ? klo : T[hh].ka[c][t][0];
+        T[hh].ka[c][t][1] = sel ? khi : T[hh].ka[c][t][1];
+      }
+  if (L.r16 == kLaneV) {
+    const int s = (r64 & 3) ^ ((r64 >> 3) & 1);
+    uint16_t *row = vbuf + h * kVTile + r64 * 64;
+    st16(row + 8 * (L.g ^ (2 * s)), pt.lo);
+    st16(row + 8 * ((4 + L.g) ^ (2 * s)), pt.hi);
+  }
+}
+
 // Consumes keys [t0, min(t0 + 64 NT, hi)) of the NT tiles (K in T, V in vbuf; t0 < hi). Rows past hi
 // may hold anything: their scores are masked and their LDS value rows zeroed (0 * NaN would not be
 // 0). One softmax update covers all NT tiles. qB0 / qB1: Q^T operands (dims 8g.. and 32+8g..).
-// sl2 = scale * log2(e).
-template <int NT>
-__device__ __forceinline__ void compute_step(const KTile (&T)[NT], uint16_t *vbuf, int t0, int hi, u32x4 qB0,
+// sl2 = scale * log2(e). With PATCH, key column pt.col takes the new K / V row first.
+template <int NT, bool PATCH = false>
+__device__ __forceinline__ void compute_step(KTile (&T)[NT], uint16_t *vbuf, int t0, int hi, u32x4 qB0,
                                              u32x4 qB1, float sl2, SoftmaxState &S, const TileLane &L,
-                                             int lane) {
+                                             int lane, const KVPatch *pt = nullptr) {
+  if (PATCH) patch_column<NT>(T, vbuf, t0, *pt, L);
   f32x4 s[NT][2][2];
   const bool full = t0 + 64 * NT <= hi;
   float mt = kNegInf;

@@ -11,7 +11,7 @@
 // of one head, so rotate_half needs no cross-lane traffic and every global access is a 128-bit
 // load/store; 4 consecutive lanes cover one 128-byte head row. The work is ~1 MB per layer at 192
 // slots: the kernel is launch-latency bound and sized as a single flat grid.
-#include "a8_common.h"
+#include "rope.h"
 
 namespace a8 {
 
@@ -22,7 +22,6 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     uint16_t *__restrict__ qo, int64_t s_qo_r, int64_t s_qo_h,
     uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
     int cache_rows, int cache_len, int nq, int nkv, int ring) {
-#pragma clang fp contract(off)
   const int H = nq + 2 * nkv;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (int64_t)R * H * 4) return;
@@ -38,29 +37,18 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
 
   const uint16_t *src = qkv + (int64_t)r * s_qkv + h * 64;
   const u32x4 wlo = ld16(src + 8 * c), whi = ld16(src + 32 + 8 * c);
-  float xl[8], xh[8];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    xl[2 * e] = bf_lo(wlo[e]); xl[2 * e + 1] = bf_hi(wlo[e]);
-    xh[2 * e] = bf_lo(whi[e]); xh[2 * e + 1] = bf_hi(whi[e]);
-  }
+  u32x4 blo{0u, 0u, 0u, 0u}, bhi{0u, 0u, 0u, 0u};
   if (bias) {
-    const u32x4 blo = ld16(bias + h * 64 + 8 * c), bhi = ld16(bias + h * 64 + 32 + 8 * c);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xl[2 * e] += bf_lo(blo[e]); xl[2 * e + 1] += bf_hi(blo[e]);
-      xh[2 * e] += bf_lo(bhi[e]); xh[2 * e + 1] += bf_hi(bhi[e]);
-    }
+    blo = ld16(bias + h * 64 + 8 * c);
+    bhi = ld16(bias + h * 64 + 32 + 8 * c);
   }
+  float xl[8], xh[8];
+  rope_x(wlo, whi, blo, bhi, bias != nullptr, xl, xh);
 
   u32x4 olo, ohi;
   if (h >= nq + nkv) {  // v head: bias only
     if (!store_ok) return;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      olo[e] = f2bf_rne(xl[2 * e]) | (f2bf_rne(xl[2 * e + 1]) << 16);
-      ohi[e] = f2bf_rne(xh[2 * e]) | (f2bf_rne(xh[2 * e + 1]) << 16);
-    }
+    rope_narrow(xl, xh, olo, ohi);
     uint16_t *dst = vc + sl * s_kb + (int64_t)(h - nq - nkv) * s_kh + (int64_t)sidx * s_ks;
     st16(dst + 8 * c, olo);
     st16(dst + 32 + 8 * c, ohi);
@@ -68,27 +56,8 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
   }
 
   const uint16_t *crow = cos_tab + (int64_t)p * s_cs, *srow = sin_tab + (int64_t)p * s_cs;
-  const u32x4 clo = ld16(crow + 8 * c), chi = ld16(crow + 32 + 8 * c);
-  const u32x4 slo = ld16(srow + 8 * c), shi = ld16(srow + 32 + 8 * c);
-  float ol[8], oh[8];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int j = 2 * e + k;
-      const float cl = k ? bf_hi(clo[e]) : bf_lo(clo[e]), ch = k ? bf_hi(chi[e]) : bf_lo(chi[e]);
-      const float sn_l = k ? bf_hi(slo[e]) : bf_lo(slo[e]), sn_h = k ? bf_hi(shi[e]) : bf_lo(shi[e]);
-      // d < 32: partner x[d+32] with sign -1; d >= 32: partner x[d-32] with sign +1.
-      // Two roundings for the products, one for the sum (contraction is off in this function).
-      ol[j] = xl[j] * cl + (-xh[j]) * sn_l;
-      oh[j] = xh[j] * ch + xl[j] * sn_h;
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    olo[e] = f2bf_rne(ol[2 * e]) | (f2bf_rne(ol[2 * e + 1]) << 16);
-    ohi[e] = f2bf_rne(oh[2 * e]) | (f2bf_rne(oh[2 * e + 1]) << 16);
-  }
+  rope_rotate(xl, xh, ld16(crow + 8 * c), ld16(crow + 32 + 8 * c), ld16(srow + 8 * c), ld16(srow + 32 + 8 * c),
+              olo, ohi);
   uint16_t *dst;
   if (h < nq) {
     dst = qo + (int64_t)r * s_qo_r + (int64_t)h * s_qo_h;

@@ -4,6 +4,7 @@ signatures, argument meaning, tensor layouts and error behaviour.
 
     bias_rope_store(...)                    fast_kernels.py:179-187   (kernel 139-176)
     DecodeAttention(...) / __call__(...)    fast_kernels.py:256-290   (kernels 193-253)
+    DecodeAttention.store_and_attend(...)   bias_rope_store then __call__ (fast_engine.py:127-132), one launch
     PrefillPlan(...)                        fast_kernels.py:335-347
     prefill_attention(...)                  fast_kernels.py:350-358   (kernel 296-332)
 
@@ -62,13 +63,8 @@ def _check_cache(kc: torch.Tensor, vc: torch.Tensor, nkv: int, hd: int):
           f"cache shape {tuple(kc.shape)} does not match [rows, {nkv}, S, {hd}]")
 
 
-def bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv, hd, ring=1 << 30):
-    """qkv: [R, (nq+2nkv)*hd]; bias: [(nq+2nkv)*hd] or None. Writes rotated q to qo [R, nq, hd] and k / v
-    into kc / vc [Bslots, nkv, S, hd] at [slot, :, pos % ring] (fast_kernels.py:179-187).
-
-    Per row r, head h: x = f32(qkv) + f32(bias); q / k get rotate_half RoPE from the bf16 cos / sin tables
-    in fp32 and are rounded once to bf16; v is rounded from x. Rows whose position is outside the tables, or
-    whose slot / position is outside the cache, store nothing (the reference leaves that undefined)."""
+def _check_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv, hd, ring):
+    """The store arguments' dtypes, shapes, strides and devices; returns the row count."""
     R = qkv.shape[0]
     width = (nq + 2 * nkv) * hd
     _check_bf16("qkv", qkv, 2)
@@ -89,6 +85,17 @@ def bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv,
     _check_cache(kc, vc, nkv, hd)
     _need(isinstance(ring, int) and 1 <= ring < 2 ** 31, f"ring must be an int in [1, 2^31) (got {ring})")
     _check_device(qkv=qkv, bias=bias, cos_tab=cos_tab, sin_tab=sin_tab, pos=pos, slot=slot, qo=qo, kc=kc, vc=vc)
+    return R
+
+
+def bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv, hd, ring=1 << 30):
+    """qkv: [R, (nq+2nkv)*hd]; bias: [(nq+2nkv)*hd] or None. Writes rotated q to qo [R, nq, hd] and k / v
+    into kc / vc [Bslots, nkv, S, hd] at [slot, :, pos % ring] (fast_kernels.py:179-187).
+
+    Per row r, head h: x = f32(qkv) + f32(bias); q / k get rotate_half RoPE from the bf16 cos / sin tables
+    in fp32 and are rounded once to bf16; v is rounded from x. Rows whose position is outside the tables, or
+    whose slot / position is outside the cache, store nothing (the reference leaves that undefined)."""
+    R = _check_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv, hd, ring)
     if R == 0:
         return qo
     lib = _lib.load()
@@ -189,6 +196,40 @@ class DecodeAttention:
         nw, tpw, grid = self.stream_shape(b, cache_len)
         whole = nw * tpw * 64 >= cache_len
         return whole and b * self.nkv >= 2 * grid
+
+    def store_and_attend(self, qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, lens, out, nsplit=1,
+                         ring=1 << 30, phases=3):
+        """bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, ...) then
+        self(q, kc, vc, lens, out, nsplit, rowmap=slot): the per-layer pair of fast_engine.py:127-132, in
+        one launch (a8_store_decode_stream) when the streaming schedule applies, else as the two calls.
+        Same results bit for bit, given that rows have distinct slots (one slot per request, as in the
+        engine's decode tick; rows sharing a slot, like the fast stack's 2-token first pass, need the two
+        calls). One difference where the reference is undefined: a row whose position lies outside the
+        RoPE tables attends with q = 0 here (the two calls leave its q row unwritten)."""
+        R = _check_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd, ring)
+        kind, shape = self.schedule(R, kc.shape[2], nsplit)
+        if kind != "stream":
+            bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd,
+                            ring=ring)
+            return self(q, kc, vc, lens, out, nsplit=nsplit, rowmap=slot, phases=phases)
+        _check_i32("lens", lens, R)
+        _check_bf16("out", out, 3)
+        _need(out.shape[0] >= R and out.shape[1] == self.nq and out.shape[2] == self.hd,
+              f"out shape {tuple(out.shape)} does not match [{R}, {self.nq}, {self.hd}]")
+        _check_device(qkv=qkv, kc=kc, lens=lens, out=out, workspace=self.acc_flat)
+        if R == 0:
+            return out
+        nw, tpw, grid = shape
+        st = _lib.load().a8_store_decode_stream(
+            qkv.data_ptr(), qkv.stride(0), bias.data_ptr() if bias is not None else None,
+            cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.stride(0), cos_tab.shape[0],
+            pos.data_ptr(), slot.data_ptr(), q.data_ptr(), q.stride(0), q.stride(1),
+            kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
+            lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+            self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap,
+            R, self.nq, self.nkv, self.hd, ring, nw, tpw, grid, float(self.scale), int(phases), _lib.stream_of(qkv))
+        _lib.check(st, "store_and_attend")
+        return out
 
     def __call__(self, q, kc, vc, lens, out, nsplit=1, bn=64, rowmap=None, phases=3):
         """q: [b, nq, hd]; kc/vc: [rows, nkv, S, hd]; query row i reads cache row rowmap[i]

@@ -193,7 +193,8 @@ def main():
         return
 
     def tick():
-        st.forward(w["qkv"], w["bias"], w["pos"], w["slot"], w["lens"], nsplit=nsplit_req, rowmap=False, q=w["q"],
+        # the engine's slow-stack call (fast_engine.py:132: rowmap = slot), which takes the fused store + decode
+        st.forward(w["qkv"], w["bias"], w["pos"], w["slot"], w["lens"], nsplit=nsplit_req, rowmap=True, q=w["q"],
                    outs=w["outs"])
 
     def decode_only():
@@ -226,7 +227,7 @@ def main():
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"{args.config}: {b} slots x KV {max(lens)}" + (" (U[128,2048])" if args.config == "C2"
                    else "") + f", GQA {NQ}/{NKV} hd {HD}, {LAYERS} layers x (bias_rope_store + split-K decode) "
-                   "as one HIP graph tick", "slots": b, "kv_len": max(lens), "cache_len": w["S"], "layers": LAYERS,
+                   "as one HIP graph tick" + (", store fused into the decode launch" if kind == "stream" else ""), "slots": b, "kv_len": max(lens), "cache_len": w["S"], "layers": LAYERS,
                    "decode_launch": launch},
         "us_per_layer": round(us_layer, 3),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),

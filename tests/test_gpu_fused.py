@@ -1,0 +1,136 @@
+"""The fused store + decode launch (a8_store_decode_stream, DecodeAttention.store_and_attend) against the two
+calls it replaces (bias_rope_store, then DecodeAttention with rowmap = slot, fast_engine.py:127-132) at the
+same streaming launch shape: outputs, q and both caches bit for bit."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+NQ, NKV, HD = 14, 2, 64
+W = (NQ + 2 * NKV) * HD
+BF = torch.bfloat16
+
+
+def _inputs(seed, b, rows, S, lens, pos, slot, bias=True, max_pos=4096):
+    g = torch.Generator().manual_seed(seed)
+    qkv = randn_bf16(g, b, W)
+    bb = (torch.randn(W, generator=g) * 0.02).to(BF) if bias else None
+    kc, vc = randn_bf16(g, rows, NKV, S, HD), randn_bf16(g, rows, NKV, S, HD)
+    return dict(qkv=qkv, bias=bb, kc=kc, vc=vc, lens=torch.tensor(lens, dtype=torch.int32),
+                pos=torch.tensor(pos, dtype=torch.int32), slot=torch.tensor(slot, dtype=torch.int32),
+                max_pos=max_pos)
+
+
+def _run_both(a8, dev, x, shape, ring=1 << 30):
+    cos, sin = a8.rope_tables(10000.0, HD, x["max_pos"], dev)
+    b = x["qkv"].shape[0]
+    d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in x.items()}
+    att = a8.DecodeAttention(max(16 * b, 8192), NQ, NKV, HD, 16, dev)
+    att.force_stream = shape
+    res = []
+    for fused in (False, True):
+        kc, vc = d["kc"].clone(), d["vc"].clone()
+        q = torch.zeros(b, NQ, HD, dtype=BF, device=dev)
+        out = torch.empty(b, NQ, HD, dtype=BF, device=dev)
+        if fused:
+            att.store_and_attend(d["qkv"], d["bias"], cos, sin, d["pos"], d["slot"], q, kc, vc, d["lens"], out,
+                                 ring=ring)
+        else:
+            a8.bias_rope_store(d["qkv"], d["bias"], cos, sin, d["pos"], d["slot"], q, kc, vc, NQ, NKV, HD, ring=ring)
+            att(q, kc, vc, d["lens"], out, rowmap=d["slot"])
+        torch.cuda.synchronize()
+        res.append((out.cpu(), q.cpu(), kc.cpu(), vc.cpu()))
+    return res
+
+
+def _bits_equal(a, b):
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_store_and_attend_peak_shape(a8, dev):
+    """The C3 launch shape (whole 2048-key rows, 4 waves, 2 units per workgroup), rows at pos = lens - 1
+    in a shuffled slot order."""
+    say("case: fused store+decode, 96 rows x 2048, shape (4, 8, 48)")
+    b, S = 96, 2048
+    g = torch.Generator().manual_seed(41)
+    slot = torch.randperm(b + 4, generator=g)[:b].tolist()
+    lens = [S] * (b - 8) + [1, 2, 63, 64, 65, 1000, 2047, 129]
+    pos = [L - 1 for L in lens]
+    x = _inputs(41, b, b + 4, S, lens, pos, slot)
+    (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, (4, 8, 48))
+    assert _bits_equal(q0, q1)
+    assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
+    assert _bits_equal(o0, o1)
+    assert not torch.isnan(o1.float()).any()
+
+
+@pytest.mark.parametrize("shape", [(4, 8, 64), (4, 2, 100), (2, 2, 37), (1, 2, 9), (1, 1, 200), (2, 16, 5),
+                                   (4, 4, 1)])
+def test_store_and_attend_edge_rows(a8, dev, shape):
+    """Ragged lengths; the new key at the end, in the middle of the attended range (lens > pos + 1) or past
+    it (pos >= lens); ring wrap (pos >= ring); a slot outside the cache (NaN row, nothing stored); no
+    bias; chunks shorter than a row (merge kernel) and 128-key steps."""
+    say(f"case: fused store+decode edge rows, shape {shape}")
+    S, rows, ring = 1024, 40, 1000
+    lens = [1, 2, 64, 65, 1000, 700, 512, 1000, 300, 5, 900, 1000, 640, 1, 128, 999]
+    pos = [0, 1, 63, 64, 999, 100, 900, 1500, 299, 4, 2, 1999, 639, 0, 127, 998]
+    slot = [3, 7, 0, 39, 12, 5, 21, 9, 33, 2, 17, 28, 40, 11, 30, 1]   # slot 40: outside the cache
+    b = len(lens)
+    for bias in (True, False):
+        x = _inputs(43 + bias, b, rows, S, lens, pos, slot, bias=bias)
+        (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, shape, ring=ring)
+        assert _bits_equal(q0, q1)
+        assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
+        assert _bits_equal(o0, o1)
+        assert torch.isnan(o1[12].float()).all()                       # slot 40 does not exist
+
+
+def test_store_and_attend_positions_outside_tables(a8, dev):
+    """A row whose position is outside the RoPE tables stores nothing (like the store kernel); the other
+    rows are unaffected and identical to the two calls."""
+    say("case: fused store+decode, positions outside the tables")
+    S, rows = 512, 8
+    lens, pos, slot = [100, 200, 300, 512], [99, 5000, -3, 511], [0, 1, 2, 3]
+    x = _inputs(47, 4, rows, S, lens, pos, slot, max_pos=1024)
+    (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, (4, 2, 8))
+    assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
+    for r in (0, 3):
+        assert _bits_equal(o0[r], o1[r]) and _bits_equal(q0[r], q1[r])
+    assert torch.isfinite(o1[1:3].float()).all()                       # q = 0: the mean of the values
+
+
+def test_attn_stack_tick_fused_matches_unfused(a8, dev):
+    """AttnStack.forward (the engine's per-layer order) with the fused launch equals the two-call path for
+    a 3-layer stack, caches included, at the peak-load schedule."""
+    say("case: 3-layer stack, fused vs unfused tick")
+    b, S, L = 64, 2048, 3
+    st = [a8.AttnStack(L, NQ, NKV, HD, 10000.0, max_rows=8192, cache_rows=b, cache_len=S, max_pos=S, dev=dev)
+          for _ in range(2)]
+    g = torch.Generator(device=dev).manual_seed(5)
+    for i in range(L):
+        st[0].kc[i].normal_(generator=g)
+        st[0].vc[i].normal_(generator=g)
+        st[1].kc[i].copy_(st[0].kc[i])
+        st[1].vc[i].copy_(st[0].vc[i])
+    lens = torch.full((b,), S, dtype=torch.int32, device=dev)
+    lens[:5] = torch.tensor([1, 700, 1500, 2000, 64], dtype=torch.int32)
+    pos, slot = lens - 1, torch.arange(b, dtype=torch.int32, device=dev)
+    qkv = [torch.randn(b, W, generator=g, device=dev).to(BF) for _ in range(L)]
+    bias = [(torch.randn(W, generator=g, device=dev) * 0.02).to(BF) for _ in range(L)]
+    outs = []
+    for k, fuse in enumerate((False, True)):
+        st[k].fuse = fuse
+        st[k].attn.force_stream = (4, 8, 32)
+        outs.append(st[k].forward(qkv, bias, pos, slot, lens))
+    torch.cuda.synchronize()
+    for i in range(L):
+        assert _bits_equal(outs[0][i], outs[1][i])
+        assert _bits_equal(st[0].kc[i], st[1].kc[i]) and _bits_equal(st[0].vc[i], st[1].vc[i])
