@@ -75,7 +75,7 @@ class AttnStack:
         """Layer i's attention (fast_engine.py:127-132): store, then attend. q / o: [R, nq, hd] buffers."""
         if plan is None and rowmap and self.fuse:
             return self.attn.store_and_attend(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
-                                              lens, o, nsplit=nsplit, ring=self.ring)
+                                              lens, o, nsplit=nsplit, ring=self.ring, write_q=False)
         bias_rope_store(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
                         self.nq, self.nkv, self.hd, ring=self.ring)
         if plan is not None:

@@ -101,16 +101,22 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Cross-lane reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48).
+// Cross-lane reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48), with the
+// gfx950 lane swaps (VALU, no LDS round trip): v_permlane16_swap(v, v) yields the values of the even and
+// the odd 16-lane row of each row pair, v_permlane32_swap(v, v) those of the lower and the upper 32
+// lanes, so one swap plus one operation reduces over l, l^16 and a second over l, l^32. Every lane of a
+// set gets the same bits.
 __device__ __forceinline__ float max_over_groups(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float sum_over_groups(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Orders LDS traffic between the lanes of one wave: the hardware serves one wave's LDS

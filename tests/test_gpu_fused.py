@@ -29,7 +29,7 @@ def _inputs(seed, b, rows, S, lens, pos, slot, bias=True, max_pos=4096):
                 max_pos=max_pos)
 
 
-def _run_both(a8, dev, x, shape, ring=1 << 30):
+def _run_both(a8, dev, x, shape, ring=1 << 30, write_q=True):
     cos, sin = a8.rope_tables(10000.0, HD, x["max_pos"], dev)
     b = x["qkv"].shape[0]
     d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in x.items()}
@@ -42,7 +42,7 @@ def _run_both(a8, dev, x, shape, ring=1 << 30):
         out = torch.empty(b, NQ, HD, dtype=BF, device=dev)
         if fused:
             att.store_and_attend(d["qkv"], d["bias"], cos, sin, d["pos"], d["slot"], q, kc, vc, d["lens"], out,
-                                 ring=ring)
+                                 ring=ring, write_q=write_q)
         else:
             a8.bias_rope_store(d["qkv"], d["bias"], cos, sin, d["pos"], d["slot"], q, kc, vc, NQ, NKV, HD, ring=ring)
             att(q, kc, vc, d["lens"], out, rowmap=d["slot"])
@@ -65,11 +65,12 @@ def test_store_and_attend_peak_shape(a8, dev):
     lens = [S] * (b - 8) + [1, 2, 63, 64, 65, 1000, 2047, 129]
     pos = [L - 1 for L in lens]
     x = _inputs(41, b, b + 4, S, lens, pos, slot)
-    (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, (4, 8, 48))
-    assert _bits_equal(q0, q1)
-    assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
-    assert _bits_equal(o0, o1)
-    assert not torch.isnan(o1.float()).any()
+    for write_q in (True, False):
+        (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, (4, 8, 48), write_q=write_q)
+        assert _bits_equal(q0, q1) if write_q else not q1.any()           # q untouched when not asked for
+        assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
+        assert _bits_equal(o0, o1)
+        assert not torch.isnan(o1.float()).any()
 
 
 @pytest.mark.parametrize("shape", [(4, 8, 64), (4, 2, 100), (2, 2, 37), (1, 2, 9), (1, 1, 200), (2, 16, 5),
