@@ -7,32 +7,67 @@
 // softmax weights in P.V, out = bf16(acc / l).
 //
 // MI355X design (compute-heavy: ~325 FLOP per compulsory byte, so both products run on MFMA):
-//   * One workgroup = one query block x one kv head; its waves are the kv head's q heads (GQA
-//     group, up to 8 per workgroup), so each K/V tile is staged in LDS once and read by every head.
-//   * K tile [64 keys][64 d] is staged row-major; the V tile is staged transposed (V^T[d][key]) by
-//     8-key x 16-byte register transposes, so both products read 128-bit MFMA operands from LDS.
-//   * Per wave: S^T = K . Q^T (v_mfma_f32_16x16x32_bf16, 64 keys x 64 query rows per tile), online
-//     softmax per query column, O^T += V^T . P^T with the S^T C-layout reused as the P^T B operand
-//     (key rows permuted within 32-key chunks, as in the decode kernel).
-#include "a8_common.h"
+//   * One workgroup = one query block x one kv head (x a share of its q heads when the group has more
+//     than 8); its waves are the q heads (7 for the engine's GQA 7), two per SIMD, so one wave's softmax
+//     VALU work overlaps the other's MFMAs. A wave reads each tile's K / V operands from LDS once and
+//     runs its four 16-row query groups through them one after another (register pressure stays
+//     within the 256 of two waves per SIMD).
+//   * K and V tiles (64 keys x 128 B each) go from HBM / L2 straight into LDS by DMA
+//     (buffer_load ... lds), double-buffered: the next tile's 16 DMA instructions (spread over the
+//     waves) are in flight while the current tile is computed; one barrier per tile (each wave's own DMA
+//     complete, then s_barrier) hands a tile to all waves.
+//   * K is row-major with the 16-byte chunks of row r permuted by chunk ^ ((r & 3) | ((r >> 3) & 1) << 2),
+//     so the permuted S^T rows (below) read 8 distinct banks per 8 lanes; V uses the decode tile's
+//     layout and is read transposed by ds_read_b64_tr_b16 (decode_tile.h).
+//   * Per unit: S^T = K . Q^T (v_mfma_f32_16x16x32_bf16, 64 keys x 16 query rows per tile), online
+//     softmax per query column in raw score units (exp2 with the scale folded into one FMA; tiles
+//     wholly below the causal diagonal skip the mask; the accumulator rescale is skipped when no max
+//     moved), O^T += V^T . P^T with the S^T C-layout reused as the P^T B operand (key rows permuted
+//     within 32-key chunks, as in the decode kernel).
+#include "decode_tile.h"
 
 namespace a8 {
 
-constexpr int kPfRow = 72;    // LDS row: 64 bf16 + 8 pad (144 B)
 constexpr int kPfMaxHW = 8;   // q heads (waves) per workgroup
 
-__global__ __launch_bounds__(64 * kPfMaxHW) void k_prefill(
+// K chunk permutation of tile row r (see above).
+__device__ __forceinline__ int pf_kswz(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
+
+// Requests DMA instruction i (0..15) of tile rows [t0, t0 + 64): i < 8 K rows 8i..8i+7, else V rows
+// 8(i-8).. . k0 / k1, v0 / v1: this lane's source offsets inside a tile for even / odd instructions
+// (plain values: i depends on the wave, and an array indexed by it would live in scratch memory).
+__device__ __forceinline__ void pf_dma(int i, uint32_t t0, rsrc_t kr, rsrc_t vr, uint16_t *kt, uint16_t *vt,
+                                       uint32_t k0, uint32_t k1, uint32_t v0, uint32_t v1) {
+  const int j = i & 7;
+  const uint32_t off = t0 * kRow + (uint32_t)j * 1024u;
+  const bool odd = j & 1;
+  if (i < 8)
+    bld16_lds<0>(kr, reinterpret_cast<char *>(kt) + j * 1024, off + (odd ? k1 : k0), 0u);
+  else
+    bld16_lds<0>(vr, reinterpret_cast<char *>(vt) + j * 1024, off + (odd ? v1 : v0), 0u);
+}
+
+// UPW = 16-row query groups per wave (the block's 64 rows).
+constexpr int UPW = 4;
+__global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     const uint16_t *__restrict__ q, int64_t s_qr, int64_t s_qh, int R,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
     int cache_rows, int cache_len, uint16_t *__restrict__ out, int64_t s_or, int64_t s_oh,
     const int32_t *__restrict__ bq0, const int32_t *__restrict__ bn, const int32_t *__restrict__ bslot,
-    const int32_t *__restrict__ bpos0, int group, int hsplit, int hpw, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[64 * kPfRow];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[64 * kPfRow];
+    const int32_t *__restrict__ bpos0, int group, int hsplit, int hpw, float sl2) {
+  // two K and two V tile buffers, separate arrays so the compiler tells their DMA apart
+  __shared__ __attribute__((aligned(16))) uint16_t kA[kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t kB[kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t vA[kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t vB[kVTile];
+  // Q^T operands of every wave's query groups, parked in LDS (8 KB per wave) to keep registers for the
+  // accumulators: [wave][group][dim half][lane] x 16 bytes
+  __shared__ __attribute__((aligned(16))) uint16_t qs[kPfMaxHW * 4 * 2 * 64 * 8];
   const int blk = blockIdx.x;
   const int kh = blockIdx.y / hsplit, hs = blockIdx.y - kh * hsplit;
-  const int tid = threadIdx.x, nthr = blockDim.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw = __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6));
   const int r16 = lane & 15, g = lane >> 4;
 
   // Block metadata is uniform over the workgroup, so early exits happen before any barrier.
@@ -44,140 +79,179 @@ __global__ __launch_bounds__(64 * kPfMaxHW) void k_prefill(
   const int nv = min(min(n, 64), R - q0);  // valid query rows
   const int hi = min(p0 + n, cache_len);   // keys [0, hi)
   if (hi <= 0) return;
+  const int ntile = (hi + 63) / 64;
 
-  const int gi = hs * hpw + w;  // head index within the group
+  // K / V of this (cache row, kv head) as buffers ending at key hi: rows past it read as zeros.
+  const int64_t cb = sl * s_kb + (int64_t)kh * s_kh;
+  const rsrc_t kr = make_rsrc(kc + cb, (uint32_t)hi * kRow);
+  const rsrc_t vr = make_rsrc(vc + cb, (uint32_t)hi * kRow);
+  TileLane tl;
+  tl.init(lane);
+  const int row8 = lane >> 3, ch8 = lane & 7;
+  const uint32_t kd0 = (uint32_t)row8 * kRow + 16u * (uint32_t)(ch8 ^ (row8 & 3));
+  const uint32_t kd1 = (uint32_t)row8 * kRow + 16u * (uint32_t)(ch8 ^ ((row8 & 3) | 4));
+  const uint32_t vd0 = tl.vd[0], vd1 = tl.vd[1];
+  uint32_t vt[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) vt[dt] = tl.vt[dt];
+  // K A-operand reads: row 32c + 8(r16/4) + 4t + r16%4, chunk g (+4 for dims 32..63)
+  const int krow = 8 * (r16 >> 2) + (r16 & 3), kz = pf_kswz(krow);
+  const uint32_t ko0 = (uint32_t)krow * kRow + 16u * (uint32_t)(g ^ kz);
+  const uint32_t ko1 = (uint32_t)krow * kRow + 16u * (uint32_t)((4 + g) ^ kz);
+
+  // This wave's units k = query group qt (rows 16k..16k+15 of the block) of q head hs*hpw + w.
+  const int gi = hs * hpw + w;
   const bool active = gi < group;
-  const int h = kh * group + gi;
-
-  // Q^T operands (B of S^T = K.Q^T): column r16 <-> query row 16qt + r16, slot (g, j) <-> dim
-  // 8g+j (hh = 0) and 32+8g+j (hh = 1).
-  u32x4 qB[4][2];
+  bool live[UPW];
+  int head[UPW], qt_of[UPW];
+  // Q^T operands: column r16 <-> query row 16qt + r16, slot (g, j) <-> dim 8g+j / 32+8g+j
+  uint16_t *qw = qs + w * (4 * 2 * 64 * 8) + lane * 8;
+  f32x4 o[UPW][4];   // O^T rows d = 16dt + 4g + i, column = query row 16qt + r16
+  float mrun[UPW], lrun[UPW];
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    const int mrow = 16 * qt + r16;
-    if (active && mrow < nv) {
-      const uint16_t *qp = q + (int64_t)(q0 + mrow) * s_qr + (int64_t)h * s_qh + 8 * g;
-      qB[qt][0] = ld16(qp);
-      qB[qt][1] = ld16(qp + 32);
-    } else {
-      qB[qt][0] = u32x4{0u, 0u, 0u, 0u};
-      qB[qt][1] = u32x4{0u, 0u, 0u, 0u};
+  for (int k = 0; k < UPW; ++k) {
+    live[k] = active;
+    head[k] = kh * group + gi;
+    qt_of[k] = k;
+    const int mrow = 16 * qt_of[k] + r16;
+    u32x4 q0v{0u, 0u, 0u, 0u}, q1v{0u, 0u, 0u, 0u};
+    if (live[k] && mrow < nv) {
+      const uint16_t *qp = q + (int64_t)(q0 + mrow) * s_qr + (int64_t)head[k] * s_qh + 8 * g;
+      q0v = ld16(qp);
+      q1v = ld16(qp + 32);
     }
+    st16(qw + (2 * k) * 64 * 8, q0v);
+    st16(qw + (2 * k + 1) * 64 * 8, q1v);
+    mrun[k] = kNegInf;
+    lrun[k] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[k][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  float mrun[4], lrun[4];
-  f32x4 o[4][4];  // [dt][qt]: O^T rows d = 16dt + 4g + i, column = query row 16qt + r16
-#pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    mrun[qt] = kNegInf;
-    lrun[qt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
 
-  const uint16_t *kb = kc + sl * s_kb + (int64_t)kh * s_kh;
-  const uint16_t *vb = vc + sl * s_kb + (int64_t)kh * s_kh;
-
-  for (int kt0 = 0; kt0 < hi; kt0 += 64) {
-    const int last = hi - 1;
-    // ---- stage K[key][d] and V^T[d][key] for keys kt0..kt0+63 (clamped to the range) ----
-    for (int i = tid; i < 512; i += nthr) {
-      const int kr = i >> 3, ch = i & 7;
-      const int key = min(kt0 + kr, last);
-      st16(ks + kr * kPfRow + 8 * ch, ld16(kb + (int64_t)key * s_ks + 8 * ch));
-    }
-    for (int u = tid; u < 64; u += nthr) {
-      const int kg = u >> 3, dc = u & 7;
-      u32x4 vr[8], vtr[8];
+  // this wave's share of a tile's 16 DMA instructions
+  auto issue = [&](int t, uint16_t *kt, uint16_t *vt) __attribute__((always_inline)) {
+    for (int i = w; i < 16; i += nw) pf_dma(i, (uint32_t)(64 * t), kr, vr, kt, vt, kd0, kd1, vd0, vd1);
+  };
+  // tile t (in kt / vt) requested by every wave: own DMA complete, then meet (which also retires the
+  // previous tile's LDS reads before its buffers are refilled). s_waitcnt vmcnt(0).
+  auto ready = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    lds_barrier();
+  };
+  auto compute = [&](int t, const uint16_t *kt, const uint16_t *vtile) __attribute__((always_inline)) {
+    if (!active) return;
+    const int kt0 = 64 * t;
+    // operands of the tile, read once: K rows (A of S^T; tile (c, tt) row 4g+i <-> key
+    // kt0 + 32c + 8g + 4tt + i) and V^T (A of O^T)
+    u32x4 ka[2][2][2], va[4][2];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vr[j] = ld16(vb + (int64_t)min(kt0 + 8 * kg + j, last) * s_ks + 8 * dc);
-      transpose8x8_bf16(vr, vtr);
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int dd = 0; dd < 8; ++dd) st16(vt + (8 * dc + dd) * kPfRow + 8 * kg, vtr[dd]);
-    }
-    __syncthreads();
-
-    if (active) {
-      // ---- S^T = K.Q^T; tile (c, t) row 4g+i <-> key kt0 + 32c + 8g + 4t + i ----
-      f32x4 s[2][2][4];
+      for (int tt = 0; tt < 2; ++tt) {
+        const char *kp = reinterpret_cast<const char *>(kt) + (32 * c + 4 * tt) * kRow;
+        ka[c][tt][0] = ld16(kp + ko0);
+        ka[c][tt][1] = ld16(kp + ko1);
+      }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const char *vp = reinterpret_cast<const char *>(vtile) + vt[dt] + 32 * c * kRow;
+        const u32x2 lo = lds_tr16(vp), hi2 = lds_tr16(vp + 4 * kRow);
+        va[dt][c] = u32x4{lo[0], lo[1], hi2[0], hi2[1]};
+      }
+    // tiles wholly below the causal diagonal and inside the range skip the mask
+    const bool full = kt0 + 63 <= p0 && kt0 + 64 <= hi;
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) {
+      // one query group at a time: no interleaving of the groups' score / weight registers
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4 qb0 = ld16(qw + (2 * k) * 64 * 8), qb1 = ld16(qw + (2 * k + 1) * 64 * 8);
+      f32x4 s[2][2];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const uint16_t *kr = ks + (32 * c + 8 * (r16 >> 2) + 4 * t + (r16 & 3)) * kPfRow + 8 * g;
-          const u32x4 ka0 = ld16(kr), ka1 = ld16(kr + 32);
-#pragma unroll
-          for (int qt = 0; qt < 4; ++qt) {
-            f32x4 a = mfma16x16x32(ka0, qB[qt][0], f32x4{0.f, 0.f, 0.f, 0.f});
-            s[c][t][qt] = mfma16x16x32(ka1, qB[qt][1], a);
-          }
-        }
-      // ---- causal mask + online softmax per query column ----
-      u32x4 pB[2][4];
-      float alpha[4];
-#pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
-        const int lim = min(p0 + 16 * qt + r16, last);  // keys <= query position (and < hi)
-        float mt = kNegInf;
+        for (int tt = 0; tt < 2; ++tt)
+          s[c][tt] = mfma16x16x32(ka[c][tt][1], qb1, mfma16x16x32(ka[c][tt][0], qb0, f32x4{0.f, 0.f, 0.f, 0.f}));
+      float mt = kNegInf;
+      if (full) {
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
+          for (int tt = 0; tt < 2; ++tt)
+            mt = fmaxf(mt, fmaxf(fmaxf(s[c][tt][0], s[c][tt][1]), fmaxf(s[c][tt][2], s[c][tt][3])));
+      } else {
+        const int lim = min(p0 + 16 * qt_of[k] + r16, hi - 1);  // keys <= query position (and < hi)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int key = kt0 + 32 * c + 8 * g + 4 * t + i;
-              const float v = key <= lim ? s[c][t][qt][i] * scale_log2 : kNegInf;
-              s[c][t][qt][i] = v;
+              const int key = kt0 + 32 * c + 8 * g + 4 * tt + i;
+              const float v = key <= lim ? s[c][tt][i] : kNegInf;
+              s[c][tt][i] = v;
               mt = fmaxf(mt, v);
             }
-        mt = max_over_groups(mt);
-        const float mn = fmaxf(mrun[qt], mt);
-        // mn stays -inf only for a column with no key yet (a padding row): keep it inert.
-        const float mref = mn == kNegInf ? 0.f : mn;
-        alpha[qt] = (mrun[qt] == kNegInf) ? 0.f : fast_exp2(mrun[qt] - mref);
-        float ps = 0.f;
+      }
+      mt = max_over_groups(mt);
+      const float mn = fmaxf(mrun[k], mt);
+      // mn stays -inf only for a column with no key yet (a padding row): keep it inert.
+      const float mc = mn == kNegInf ? 0.f : mn * sl2;
+      const float alpha = (mrun[k] == kNegInf) ? 0.f : fast_exp2(__builtin_fmaf(mrun[k], sl2, -mc));
+      float ps = 0.f;
+      u32x4 pB[2];
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            float p[4];
+        for (int tt = 0; tt < 2; ++tt) {
+          float pv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              p[i] = fast_exp2(s[c][t][qt][i] - mref);
-              ps += p[i];
-            }
-            pB[c][qt][2 * t] = pack_bf16x2(p[0], p[1]);
-            pB[c][qt][2 * t + 1] = pack_bf16x2(p[2], p[3]);
+          for (int i = 0; i < 4; ++i) {
+            pv[i] = fast_exp2(__builtin_fmaf(s[c][tt][i], sl2, -mc));
+            ps += pv[i];
           }
-        lrun[qt] = lrun[qt] * alpha[qt] + ps;
-        mrun[qt] = mn;
-      }
-      // ---- O^T += V^T . P^T ----
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-        for (int qt = 0; qt < 4; ++qt) o[dt][qt] *= alpha[qt];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const u32x4 vA = ld16(vt + (16 * dt + r16) * kPfRow + 32 * c + 8 * g);
-#pragma unroll
-          for (int qt = 0; qt < 4; ++qt) o[dt][qt] = mfma16x16x32(vA, pB[c][qt], o[dt][qt]);
+          pB[c][2 * tt] = pack_bf16x2(pv[0], pv[1]);
+          pB[c][2 * tt + 1] = pack_bf16x2(pv[2], pv[3]);
         }
-      }
-    }
-    __syncthreads();
-  }
-
-  if (!active) return;
+      lrun[k] = lrun[k] * alpha + ps;
+      mrun[k] = mn;
+      if (__ballot(alpha != 1.f)) {
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    const float l = sum_over_groups(lrun[qt]);
-    const int mrow = 16 * qt + r16;
+        for (int dt = 0; dt < 4; ++dt) o[k][dt] *= alpha;
+      }
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) o[k][dt] = mfma16x16x32(va[dt][c], pB[c], o[k][dt]);
+    }
+  };
+
+  issue(0, kA, vA);
+  for (int t = 0;; t += 2) {
+    ready();
+    if (t + 1 < ntile) issue(t + 1, kB, vB);
+    compute(t, kA, vA);
+    if (t + 1 >= ntile) break;
+    ready();
+    if (t + 2 < ntile) issue(t + 2, kA, vA);
+    compute(t + 1, kB, vB);
+    if (t + 2 >= ntile) break;
+  }
+  // the last request may still write (zeros, past the range) into LDS: let it land before the end
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+
+#pragma unroll
+  for (int k = 0; k < UPW; ++k) {
+    if (!live[k]) continue;
+    const float l = sum_over_groups(lrun[k]);
+    const int mrow = 16 * qt_of[k] + r16;
     if (mrow >= nv) continue;
-    uint16_t *op = out + (int64_t)(q0 + mrow) * s_or + (int64_t)h * s_oh + 4 * g;
+    uint16_t *op = out + (int64_t)(q0 + mrow) * s_or + (int64_t)head[k] * s_oh + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
-      st8(op + 16 * dt, u32x2{pack_bf16x2(o[dt][qt][0] / l, o[dt][qt][1] / l),
-                              pack_bf16x2(o[dt][qt][2] / l, o[dt][qt][3] / l)});
+      st8(op + 16 * dt, u32x2{pack_bf16x2(o[k][dt][0] / l, o[k][dt][1] / l),
+                              pack_bf16x2(o[k][dt][2] / l, o[k][dt][3] / l)});
   }
 }
 
@@ -202,13 +276,15 @@ extern "C" int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
     return set_error(A8_EINVAL, "prefill_attn: null pointer");
   if (!al16(q) || !al16(kc) || !al16(vc) || !al16(out) || (s_qr | s_qh | s_kb | s_kh | s_ks | s_or | s_oh) & 7)
     return set_error(A8_EALIGN, "prefill_attn: pointers must be 16-byte aligned and strides multiples of 8");
+  if (s_ks != hd)
+    return set_error(A8_EUNSUP, "prefill_attn: cache positions must be contiguous rows (s_ks %lld)", (long long)s_ks);
   const int nkv = nq / group;
-  const int hpw = group < kPfMaxHW ? group : kPfMaxHW;
+  const int hpw = group < kPfMaxHW ? group : kPfMaxHW;  // q heads (waves) per workgroup
   const int hsplit = (group + hpw - 1) / hpw;
   if ((int64_t)nkv * hsplit > 65535) return set_error(A8_EUNSUP, "prefill_attn: too many heads");
   hipLaunchKernelGGL(k_prefill, dim3(nblk, nkv * hsplit), dim3(64 * hpw), 0, (hipStream_t)stream,
-                     (const uint16_t *)q, s_qr, s_qh, R, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh,
-                     s_ks, cache_rows, cache_len, (uint16_t *)out, s_or, s_oh, bq0, bn, bslot, bpos0, group, hsplit,
-                     hpw, scale * kLog2e);
+                     (const uint16_t *)q, s_qr, s_qh, R, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, s_ks,
+                     cache_rows, cache_len, (uint16_t *)out, s_or, s_oh, bq0, bn, bslot, bpos0, group, hsplit, hpw,
+                     scale * kLog2e);
   return (int)hipGetLastError();
 }
