@@ -67,13 +67,16 @@ class AttnStack:
         self.kc = list(self.kc_all.unbind(0))
         self.vc = list(self.vc_all.unbind(0))
         self.attn = DecodeAttention(max_rows, nq, nkv, hd, nsplit_max, dev)
-        # decode with rowmap = slot: store and attend in one launch where the schedule allows
-        # (DecodeAttention.store_and_attend); False keeps the two calls
-        self.fuse = True
 
-    def layer(self, i, qkv, bias, pos, slot, lens, q, o, nsplit=1, rowmap=True, plan=None):
-        """Layer i's attention (fast_engine.py:127-132): store, then attend. q / o: [R, nq, hd] buffers."""
-        if plan is None and rowmap and self.fuse:
+    def layer(self, i, qkv, bias, pos, slot, lens, q, o, nsplit=1, rowmap=True, plan=None, fuse=False):
+        """Layer i's attention (fast_engine.py:127-132): store, then attend. q / o: [R, nq, hd] buffers.
+
+        fuse=True declares that every row has a slot of its own and attends that slot's cache row (rowmap,
+        or rowmap off with slot[r] = r, as in the slow stack's decode tick, fast_engine.py:752-753); the
+        decode then stores and attends in one launch where the schedule allows
+        (DecodeAttention.store_and_attend), with the same results. Rows sharing a slot (the fast stack's
+        2-token pass) must keep fuse=False."""
+        if plan is None and fuse:
             return self.attn.store_and_attend(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
                                               lens, o, nsplit=nsplit, ring=self.ring, write_q=False)
         bias_rope_store(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
@@ -84,7 +87,7 @@ class AttnStack:
             self.attn(q, self.kc[i], self.vc[i], lens, o, nsplit=nsplit, rowmap=slot if rowmap else None)
         return o
 
-    def forward(self, qkv, bias, pos, slot, lens, nsplit=1, rowmap=True, plan=None, q=None, outs=None):
+    def forward(self, qkv, bias, pos, slot, lens, nsplit=1, rowmap=True, plan=None, q=None, outs=None, fuse=False):
         """All layers in order. qkv / bias: per-layer lists ([R, (nq+2nkv)*hd] rows, [(nq+2nkv)*hd] or None).
         outs: per-layer [R, nq, hd] outputs (allocated when None; pass buffers under graph capture)."""
         R = qkv[0].shape[0]
@@ -95,7 +98,7 @@ class AttnStack:
             outs = [torch.empty(R, self.nq, self.hd, dtype=torch.bfloat16, device=dev) for _ in range(self.n_layers)]
         for i in range(self.n_layers):
             self.layer(i, qkv[i], bias[i] if bias is not None else None, pos, slot, lens, q, outs[i],
-                       nsplit=nsplit, rowmap=rowmap, plan=plan)
+                       nsplit=nsplit, rowmap=rowmap, plan=plan, fuse=fuse)
         return outs
 
 

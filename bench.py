@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode-attn µs/layer + achieved HBM GB/s (% peak) at 192 slots, KV 2048"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_TFLOPS = 2500.0
 NQ, NKV, HD, LAYERS = 14, 2, 64, 24
 W = (NQ + 2 * NKV) * HD
 
@@ -40,6 +41,7 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU-baseline sample")
     p.add_argument("--shape", default=None, help="use the split + combine kernels at NSPLIT,WAVES")
     p.add_argument("--stream-shape", default=None, help="force the streaming kernel's WAVES,TILES_PER_WAVE,GRID")
+    p.add_argument("--no-configs", action="store_true", help="skip the other configs' figures (C1, C2, C4, C5)")
     p.add_argument("--traffic-probe", action="store_true",
                    help="only launch one layer's decode 4x and a 256 MiB copy (target of rocprofv3 --pmc passes)")
     return p.parse_args()
@@ -84,6 +86,11 @@ def capture(torch, fn):
     return g
 
 
+def time_median(torch, g, steps, warmup, runs=5):
+    """Median over `runs` of time_graph (ms per replay)."""
+    return statistics.median(time_graph(torch, g, steps, warmup if i == 0 else 2) for i in range(runs))
+
+
 def time_graph(torch, g, steps, warmup):
     """ms per replay: warmup replays, then `steps` replays between two events on the launching stream."""
     for _ in range(warmup):
@@ -126,6 +133,117 @@ def cpu_baseline(w, budget_s):
             "sample": f"1 of {LAYERS} layers (store + decode, {b} slots, same inputs), {len(times)} reps, median"}
 
 
+def per_config(a8, torch, dev, steps):
+    """µs per layer (per pass at C5), achieved GB/s or TFLOP/s and the roofline fraction of the other BASELINE
+    configs, each timed as a captured graph (median of 5 runs). Decode configs: store + decode per layer, the
+    engine's calls (fused where the schedule allows). C4: store + packed prefill per layer, and the prefill
+    launch alone against the bf16 MFMA peak."""
+    from oracle import attn_ref as ref_counts  # byte / FLOP counts only
+    import numpy as np
+
+    res = {}
+    gen = torch.Generator(device=dev).manual_seed(7)
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=gen, device=dev) * std).to(torch.bfloat16)
+
+    # C1: one row, KV 385 after storing position 384; C2: 64 slots, lengths U[128, 2048], cache 4096
+    for cfg in ("C1", "C2"):
+        if cfg == "C1":
+            b, S, layers = 1, 512, LAYERS
+            lens = torch.full((b,), 385, dtype=torch.int32)
+        else:
+            b, S, layers = 64, 4096, LAYERS
+            lens = torch.randint(128, 2049, (b,), generator=torch.Generator().manual_seed(0), dtype=torch.int32)
+        st = a8.AttnStack(layers, NQ, NKV, HD, 10000.0, max_rows=max(16 * b, 8192), cache_rows=b + 1, cache_len=S,
+                          max_pos=S, dev=dev)
+        for i in range(layers):
+            st.kc[i].normal_(generator=gen)
+            st.vc[i].normal_(generator=gen)
+        lens_d, pos, slot = lens.to(dev), (lens - 1).to(dev), torch.arange(b, dtype=torch.int32, device=dev)
+        qkv = [randn(b, W) for _ in range(layers)]
+        bias = [randn(W, std=0.02) for _ in range(layers)]
+        q = torch.empty(b, NQ, HD, dtype=torch.bfloat16, device=dev)
+        outs = [torch.empty(b, NQ, HD, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+        nsplit = a8.ref_nsplit(b, NKV)
+        g = capture(torch, lambda: st.forward(qkv, bias, pos, slot, lens_d, nsplit=nsplit, rowmap=False, q=q,
+                                              outs=outs, fuse=True))
+        us = time_median(torch, g, steps, 10) * 1e3 / layers
+        nbytes = ref_counts.decode_bytes(lens.tolist(), NQ, NKV, HD)
+        kind, shape = st.attn.schedule(b, S, nsplit)
+        res[cfg] = {"us_per_layer": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                    "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
+                    "schedule": [kind, list(shape)], "rows": b, "kv_len": int(max(lens)),
+                    "note": "latency bound" if cfg == "C1" else "store + decode per layer"}
+        del g, st, qkv, outs
+        torch.cuda.empty_cache()
+
+    # C5: fast-AR shape, 192 slots x 4 layers, cache [192, 2, 10, 64]: a 2-token pass (384 rows at positions
+    # 0 / 1 sharing their slot, rowmap = slot) then 8 passes of 192 rows at positions 2..9
+    b, S, layers = 192, 10, 4
+    st = a8.AttnStack(layers, NQ, NKV, HD, 10000.0, max_rows=max(2 * 2 * b, 16), cache_rows=b, cache_len=S,
+                      max_pos=16, dev=dev, nsplit_max=1)
+    passes = []
+    r = torch.arange(2 * b, dtype=torch.int32)
+    passes.append(((r % 2).to(dev), (r // 2).to(dev), (r % 2 + 1).to(dev), True, 2 * b))
+    for p in range(2, 10):
+        rows = torch.arange(b, dtype=torch.int32)
+        passes.append((torch.full((b,), p, dtype=torch.int32, device=dev), rows.to(dev),
+                       torch.full((b,), p + 1, dtype=torch.int32, device=dev), False, b))
+    qkvs = [[randn(nr, W) for _ in range(layers)] for (_, _, _, _, nr) in passes]
+    bias = [randn(W, std=0.02) for _ in range(layers)]
+    q = torch.empty(2 * b, NQ, HD, dtype=torch.bfloat16, device=dev)
+    outs = [torch.empty(2 * b, NQ, HD, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+
+    def c5():
+        for (pos, slot, lens_d, rmap, nr), qkv in zip(passes, qkvs):
+            st.forward(qkv, bias, pos, slot, lens_d, nsplit=1, rowmap=rmap, q=q[:nr], outs=[o[:nr] for o in outs])
+
+    g = capture(torch, c5)
+    us = time_median(torch, g, steps, 10) * 1e3 / (len(passes) * layers)
+    res["C5"] = {"us_per_pass_layer": round(us, 3), "passes": len(passes), "layers": layers, "rows": b,
+                 "note": "latency bound (<= 1 MB of KV per pass)"}
+    del g, st, qkvs, outs
+    torch.cuda.empty_cache()
+
+    # C4: 64 requests, n ~ U[40, 400], after a 300-position voice prefix; store + packed prefill per layer
+    ns = torch.randint(40, 401, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+    p0, nreq, layers = 300, 64, LAYERS
+    R, S = sum(ns), 704
+    st = a8.AttnStack(layers, NQ, NKV, HD, 10000.0, max_rows=8192, cache_rows=nreq + 1, cache_len=S, max_pos=S,
+                      dev=dev)
+    for i in range(layers):
+        st.kc[i].normal_(generator=gen)
+        st.vc[i].normal_(generator=gen)
+    pos = torch.cat([p0 + torch.arange(n) for n in ns]).int().to(dev)
+    slot = torch.cat([torch.full((n,), i) for i, n in enumerate(ns)]).int().to(dev)
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    plan = a8.PrefillPlan(r0s, ns, list(range(nreq)), [p0] * nreq, dev)
+    qkv = [randn(R, W) for _ in range(layers)]
+    bias = [randn(W, std=0.02) for _ in range(layers)]
+    q = torch.empty(R, NQ, HD, dtype=torch.bfloat16, device=dev)
+    outs = [torch.empty(R, NQ, HD, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+    g = capture(torch, lambda: st.forward(qkv, bias, pos, slot, None, plan=plan, q=q, outs=outs))
+    us = time_median(torch, g, steps, 10) * 1e3 / layers
+    del g
+
+    def pf_only():
+        for i in range(layers):
+            a8.prefill_attention(q, st.kc[i], st.vc[i], plan, outs[i], NQ // NKV)
+
+    g = capture(torch, pf_only)
+    us_pf = time_median(torch, g, steps, 10) * 1e3 / layers
+    flops = ref_counts.prefill_flops(ns, [p0] * nreq, NQ, HD)
+    res["C4"] = {"us_per_layer": round(us, 3), "prefill_us_per_layer": round(us_pf, 3),
+                 "prefill_TFLOP/s": round(flops / us_pf / 1e6, 1),
+                 "frac_mfma_bf16": round(flops / us_pf / 1e6 / MFMA_BF16_TFLOPS, 4), "flops_per_layer": flops,
+                 "rows": R, "blocks": plan.nblk,
+                 "note": "store + prefill per layer; the prefill's fp32 softmax VALU work bounds it before MFMA does"}
+    del g, st, qkv, outs
+    torch.cuda.empty_cache()
+    return res
+
+
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c3_traffic.md")
 
 
@@ -144,17 +262,18 @@ def measured_traffic(cfg, launch):
 
 
 def traffic_probe(torch, st, w, nsplit_req):
-    """Counter target for the traffic measurement: 4 launches of one layer's decode (the bench's launch
-    shape) and a plain 256 MiB elementwise copy (read 256 MiB, write 256 MiB) that calibrates
+    """Counter target for the traffic measurement: 4 launches of one layer of the tick (the bench's launch:
+    store + decode) and a plain 256 MiB elementwise copy (read 256 MiB, write 256 MiB) that calibrates
     FETCH_SIZE / WRITE_SIZE to bytes. Run under rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE."""
     for _ in range(4):
-        st.attn(w["q"], st.kc[0], st.vc[0], w["lens"], w["outs"][0], nsplit=nsplit_req)
+        st.layer(0, w["qkv"][0], w["bias"][0], w["pos"], w["slot"], w["lens"], w["q"], w["outs"][0],
+                 nsplit=nsplit_req, rowmap=False, fuse=True)
     x = torch.ones(64 << 20, dtype=torch.float32, device=w["q"].device)
     y = torch.empty_like(x)
     for _ in range(2):
         torch.add(x, 0.0, out=y)
     torch.cuda.synchronize()
-    print("traffic probe: 4 decode launches, 2 copies of 268435456 bytes", flush=True)
+    print("traffic probe: 4 tick-layer launches, 2 copies of 268435456 bytes", flush=True)
 
 
 def main():
@@ -180,22 +299,26 @@ def main():
         st.attn.force_stream = tuple(int(x) for x in args.stream_shape.split(","))
     nsplit_req = a8.ref_nsplit(b, NKV)
     kind, shape = st.attn.schedule(b, w["S"], nsplit_req)
+    fused = kind == "stream"
     if kind == "stream":
         nw, tpw, grid = shape
         chunks = -(-w["S"] // (nw * tpw * 64))
-        launch = {"kernel": "k_decode_stream" + (" + k_decode_stream_combine" if chunks > 1 else ""), "waves": nw,
+        launch = {"kernel": "k_decode_stream" + (" (store fused)" if fused else "") +
+                  (" + k_decode_stream_combine" if chunks > 1 else ""), "waves": nw,
                   "tiles_per_wave": tpw, "grid": grid, "chunk_keys": nw * tpw * 64, "chunks_per_row": chunks}
     else:
         ns, nw = shape
-        launch = {"kernel": "k_decode_split" + ("" if ns == 1 else " + k_decode_combine"), "nsplit": ns, "waves": nw}
+        launch = {"kernel": "k_bias_rope_store + k_decode_split" + ("" if ns == 1 else " + k_decode_combine"),
+                  "nsplit": ns, "waves": nw}
     if args.traffic_probe:
         traffic_probe(torch, st, w, nsplit_req)
         return
 
     def tick():
-        # the engine's slow-stack call (fast_engine.py:132: rowmap = slot), which takes the fused store + decode
-        st.forward(w["qkv"], w["bias"], w["pos"], w["slot"], w["lens"], nsplit=nsplit_req, rowmap=True, q=w["q"],
-                   outs=w["outs"])
+        # the engine's slow tick (fast_engine.py:752-753: slot = arange, rowmap off); one slot per row, so the
+        # store and the decode run as one launch where the schedule allows
+        st.forward(w["qkv"], w["bias"], w["pos"], w["slot"], w["lens"], nsplit=nsplit_req, rowmap=False, q=w["q"],
+                   outs=w["outs"], fuse=True)
 
     def decode_only():
         for i in range(LAYERS):
@@ -207,11 +330,12 @@ def main():
                                st.vc[i], NQ, NKV, HD)
 
     g_tick = capture(torch, tick)
-    ms = time_graph(torch, g_tick, args.steps, args.warmup)
+    ms = time_median(torch, g_tick, args.steps, args.warmup)
     g_dec = capture(torch, decode_only)
-    ms_dec = time_graph(torch, g_dec, args.steps, args.warmup)
+    ms_dec = time_median(torch, g_dec, args.steps, args.warmup)
     g_sto = capture(torch, store_only)
-    ms_sto = time_graph(torch, g_sto, args.steps, args.warmup)
+    ms_sto = time_median(torch, g_sto, args.steps, args.warmup)
+    del g_tick, g_dec, g_sto
 
     traffic = measured_traffic(args.config, launch)
     lens = w["lens_h"].tolist()
@@ -231,16 +355,25 @@ def main():
                    "decode_launch": launch},
         "us_per_layer": round(us_layer, 3),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "decode_us_per_layer": round(dec_us, 3),
-        "store_us_per_layer": round(ms_sto * 1e3 / LAYERS, 3),
+        # the tick's one launch per layer (the fused store + decode at C3): algorithmic store + decode bytes
+        # over its per-launch time inside the timed tick
         "roofline": {"bound": "hbm", "kernel": launch["kernel"],
-                     "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": dec_bytes, "us_per_launch": round(dec_us, 3)},
+                     "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": layer_bytes, "us_per_launch": round(us_layer, 3)},
+        # the same tick as the reference's two launches per layer, and the decode launch alone
+        "unfused": {"decode_us_per_layer": round(dec_us, 3), "decode_gbs": round(dec_gbs, 2),
+                    "decode_frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+                    "store_us_per_layer": round(ms_sto * 1e3 / LAYERS, 3)},
+        "timing": f"median of 5 runs of {args.steps} graph replays (HIP events on the launching stream)",
         "device": {"name": props.name, "arch": getattr(props, "gcnArchName", ""), "cus": props.multi_processor_count},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+    if not args.no_configs:
+        del st, w
+        torch.cuda.empty_cache()
+        line["per_config"] = per_config(a8, torch, dev, args.steps)
     print(json.dumps(line), flush=True)
 
 

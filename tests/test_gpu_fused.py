@@ -128,9 +128,8 @@ def test_attn_stack_tick_fused_matches_unfused(a8, dev):
     bias = [(torch.randn(W, generator=g, device=dev) * 0.02).to(BF) for _ in range(L)]
     outs = []
     for k, fuse in enumerate((False, True)):
-        st[k].fuse = fuse
         st[k].attn.force_stream = (4, 8, 32)
-        outs.append(st[k].forward(qkv, bias, pos, slot, lens))
+        outs.append(st[k].forward(qkv, bias, pos, slot, lens, rowmap=False, fuse=fuse))
     torch.cuda.synchronize()
     for i in range(L):
         assert _bits_equal(outs[0][i], outs[1][i])
