@@ -71,14 +71,15 @@ class AttnStack:
     def layer(self, i, qkv, bias, pos, slot, lens, q, o, nsplit=1, rowmap=True, plan=None, fuse=False):
         """Layer i's attention (fast_engine.py:127-132): store, then attend. q / o: [R, nq, hd] buffers.
 
-        fuse=True declares that every row has a slot of its own and attends that slot's cache row (rowmap,
-        or rowmap off with slot[r] = r, as in the slow stack's decode tick, fast_engine.py:752-753); the
-        decode then stores and attends in one launch where the schedule allows
+        fuse=True declares that no row attends a cache row that another row of the call stores into (the
+        slow stack's decode tick: slot[r] = r with rowmap off, fast_engine.py:752-753; or distinct slots
+        with rowmap on); the decode then stores and attends in one launch where the schedule allows
         (DecodeAttention.store_and_attend), with the same results. Rows sharing a slot (the fast stack's
         2-token pass) must keep fuse=False."""
         if plan is None and fuse:
             return self.attn.store_and_attend(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
-                                              lens, o, nsplit=nsplit, ring=self.ring, write_q=False)
+                                              lens, o, nsplit=nsplit, rowmap=slot if rowmap else None,
+                                              ring=self.ring, write_q=False)
         bias_rope_store(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
                         self.nq, self.nkv, self.hd, ring=self.ring)
         if plan is not None:

@@ -29,8 +29,9 @@
 namespace a8 {
 
 // Inputs of the fused store (a8_store_decode_stream): the bias_rope_store arguments the decode does not
-// already take. The query row r's cache row is slot[r] (the decode's row map).
+// already take. Query row r stores into cache row slot[r] and attends cache row rowmap[r] (or r).
 struct StoreIn {
+  const int32_t *slot;
   const uint16_t *qkv;
   int64_t s_qkv;
   const uint16_t *bias;  // nullptr: no bias
@@ -57,11 +58,13 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
     uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
     float *__restrict__ ml_ws, int b, int nq, int nkv, int group, int tpw, int P,
     float sl2, StoreIn si) {
+  warm_kernargs<264>();  // the explicit arguments above span 0x000-0x10f
   // V tiles of the two pipeline buffers (NT per wave each); separate arrays, so the compiler tells
   // their DMA completions apart and waits only for the buffer it reads.
   __shared__ __attribute__((aligned(16))) uint16_t vbA[NW * NT * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vbB[NW * NT * kVTile];
   __shared__ __attribute__((aligned(16))) float mrg[2][NW * (32 + 16 * kOb)];  // per-wave m, l, O (x2)
+  __shared__ int marr[2], mseq[2];  // per merge buffer: waves arrived, last merge completed
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -70,6 +73,11 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
   const int NC = b * nkv * P;
   const int nmine = ((int)blockIdx.x < NC) ? (NC - 1 - (int)blockIdx.x) / G + 1 : 0;
   if (nmine == 0) return;
+  if (tid < 2) {
+    marr[tid] = 0;
+    mseq[tid] = tid - 2;
+  }
+  lds_barrier();
 
   constexpr uint32_t row_bytes = kRow;  // s_ks == 64, checked by the entry point
   const uint32_t full_row = (uint32_t)cache_len * row_bytes;
@@ -89,7 +97,7 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
   // first tile is requested. For the first chunk only the cache row is needed up front: its tiles
   // are requested over the whole cache row and keys past the length are masked when computed.
   struct Meta {
-    int lraw, craw, praw;
+    int lraw, craw, praw, sraw;
   };
   auto ids = [&](int i, Chunk &k) {
     const int c = (int)blockIdx.x + i * G;
@@ -102,14 +110,21 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
   const rsrc_t lens_r = make_rsrc(lens, (uint32_t)b * 4u);
   const rsrc_t map_r = make_rsrc(rowmap, rowmap ? (uint32_t)b * 4u : 0u);
   const rsrc_t pos_r = make_rsrc(si.pos, FUSED ? (uint32_t)b * 4u : 0u);
+  const rsrc_t slot_r = make_rsrc(si.slot, FUSED ? (uint32_t)b * 4u : 0u);
+  // The row map is requested first, and only when there is one: loads complete in issue order, so the
+  // first tile (which needs only the cache row) then never waits for the lengths or positions.
   auto meta_load = [&](int i) {
-    Meta m{0, 0, 0};
+    Meta m{0, 0, 0, 0};
     if (i < nmine) {
       Chunk k;
       ids(i, k);
+      m.craw = k.row;
+      if (rowmap) m.craw = bld4(map_r, (uint32_t)k.row * 4u);
       m.lraw = bld4(lens_r, (uint32_t)k.row * 4u);
-      m.craw = rowmap ? bld4(map_r, (uint32_t)k.row * 4u) : k.row;
-      if (FUSED) m.praw = bld4(pos_r, (uint32_t)k.row * 4u);
+      if (FUSED) {
+        m.praw = bld4(pos_r, (uint32_t)k.row * 4u);
+        m.sraw = bld4(slot_r, (uint32_t)k.row * 4u);
+      }
     }
     return m;
   };
@@ -178,8 +193,9 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
     r.sn[1] = bld16(sr, og + 64u);
   };
   // FUSED, at a chunk's first step: one RoPE pass per lane gives q (lanes r16 < group: the Q^T operand),
-  // the new k (lane kLaneK) and v (lane kLaneV: x narrowed, not rotated); the key column they replace;
-  // the unit's first chunk (wave 0) writes k / v to the cache and q to qo, as k_bias_rope_store would.
+  // the new k (lane kLaneK) and v (lane kLaneV: x narrowed, not rotated); the key column they replace
+  // when the row attends the cache row it stores into; the unit's first chunk (wave 0) writes k / v to
+  // the cache and q to qo, as k_bias_rope_store would.
   KVPatch pt;
   pt.col = -1;
   auto apply_qkv = [&](const Chunk &k, int i, const Meta &m, const QkvRaw &r, u32x4 &q0, u32x4 &q1) {
@@ -187,8 +203,9 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
     const int p = __builtin_amdgcn_readfirstlane(m.praw);
     const bool pv = live && p >= 0 && p < si.n_tab;
     const int crow = __builtin_amdgcn_readfirstlane(m.craw);
+    const int srow = __builtin_amdgcn_readfirstlane(m.sraw);
     const int sidx = pv ? p % si.ring : 0;
-    const bool store_ok = pv && crow >= 0 && crow < cache_rows && sidx < cache_len;
+    const bool store_ok = pv && srow >= 0 && srow < cache_rows && sidx < cache_len;
     float xl[8], xh[8], ol[8], oh[8];
     rope_x(r.w[0], r.w[1], r.bb[0], r.bb[1], si.bias != nullptr, xl, xh);
     rope_rotate_f(xl, xh, r.cs[0], r.cs[1], r.sn[0], r.sn[1], ol, oh);
@@ -203,11 +220,11 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
     const u32x4 z{0u, 0u, 0u, 0u};
     q0 = qlive ? pt.lo : z;  // unknown position: the reference reads no table row; q is zero here
     q1 = qlive ? pt.hi : z;
-    pt.col = store_ok ? sidx : -1;
+    pt.col = (store_ok && srow == crow) ? sidx : -1;
     if (k.part == 0 && w == 0) {
       uint16_t *dst = nullptr;
       if (store_ok && (tl.r16 == kLaneK || vlane))
-        dst = (vlane ? vc : kc) + (int64_t)crow * s_kb + (int64_t)k.kh * s_kh + (int64_t)sidx * s_ks;
+        dst = (vlane ? vc : kc) + (int64_t)srow * s_kb + (int64_t)k.kh * s_kh + (int64_t)sidx * s_ks;
       else if (si.qo && qlive)
         dst = si.qo + (int64_t)k.row * si.s_qo_r + (int64_t)(k.kh * group + tl.r16) * si.s_qo_h;
       if (dst) {
@@ -220,10 +237,13 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
   SoftmaxState S;
   S.reset();
 
-  // End of chunk i: every wave parks its state in LDS, then all waves merge it and write the output
-  // (a row within one chunk) or the chunk's partial. Chunks without keys are skipped by every wave
-  // alike, with no barrier, so the LDS buffer alternates with the count of merged chunks (nfin), not
-  // with i: a wave still reading one buffer is never overtaken by writes to it.
+  // End of chunk i: every wave parks its state in LDS and counts itself in; the last of the NW waves to
+  // arrive merges the partials and writes the output (a row within one chunk) or the chunk's partial,
+  // while the others go straight on to their next tiles. No wave waits for another here, so each keeps
+  // its loads flowing (a barrier would hold every wave of the workgroup for the slowest one). Chunks
+  // without keys are skipped by every wave alike, so the merge count n and its LDS buffer (n & 1) are
+  // the same in every wave; before a wave parks merge n in a buffer it waits until that buffer's merge
+  // n - 2 is complete (mseq), a wait that ends because a merging wave waits for nothing.
   int nfin = 0;
   auto finish_chunk = [&](const Chunk &k, int L) {
     const int peff = L > 0 ? (L + CH - 1) / CH : 1;  // chunks with keys (an empty row still writes 0/0)
@@ -231,43 +251,60 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
       S.reset();
       return;
     }
-    float *mb = mrg[nfin & 1], *lb = mb + NW * 16, *ob = mb + NW * 32;
-    ++nfin;
+    const int n = nfin++;
+    const int bsel = n & 1;
+    float *mb = mrg[bsel], *lb = mb + NW * 16, *ob = mb + NW * 32;
     const float lsum = sum_over_groups(S.lsum);
+    if (NW > 1) {
+      while (lds_read_word(&mseq[bsel]) < n - 2) __builtin_amdgcn_s_sleep(1);
+    }
     if (tl.g == 0) {
       mb[w * 16 + tl.r16] = S.m;
       lb[w * 16 + tl.r16] = lsum;
     }
     lds_store_4x16(ob + (w * 16 + tl.r16) * kOb + 4 * tl.g, S.o[0], S.o[1], S.o[2], S.o[3]);
     S.reset();
-    lds_barrier();  // the next chunk's loads stay in flight
-    // every wave merges a share of the (head, dim) outputs; no barrier after: the next chunk writes the
-    // other LDS buffer
-    for (int idx = tid; idx < group * 64; idx += 64 * NW) {
-      const int head = idx >> 6, d = idx & 63;
+    if (NW > 1) {
+      if (lds_add_word(&marr[bsel], 1) != NW - 1) return;
+      lds_write_word(&marr[bsel], 0);  // the buffer's next arrivals come after mseq says n is merged
+    } else {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the parked state is readable
+    }
+    // one lane per (head, 4 dims): 16-byte reads of the parked O rows, one 8-byte store per lane
+    for (int t = lane; t < group * 16; t += 64) {
+      const int head = t >> 4, d4 = (t & 15) * 4;
+      float mv[NW];
       float M = kNegInf;
 #pragma unroll
-      for (int v = 0; v < NW; ++v) M = fmaxf(M, mb[v * 16 + head]);
-      float num = 0.f, den = 0.f;
+      for (int v = 0; v < NW; ++v) {
+        mv[v] = mb[v * 16 + head];
+        M = fmaxf(M, mv[v]);
+      }
+      f32x4 num = {0.f, 0.f, 0.f, 0.f};
+      float den = 0.f;
 #pragma unroll
       for (int v = 0; v < NW; ++v) {
-        const float mv = mb[v * 16 + head];
-        const float wt = (mv == kNegInf) ? 0.f : fast_exp2((mv - M) * sl2);
-        num += wt * ob[(v * 16 + head) * kOb + d];
+        const float wt = (mv[v] == kNegInf) ? 0.f : fast_exp2((mv[v] - M) * sl2);
+        const f32x4 o = *reinterpret_cast<const f32x4 *>(ob + (v * 16 + head) * kOb + d4);
+        num += wt * o;
         den += wt * lb[v * 16 + head];
       }
       const int hq = k.kh * group + head;
       if (peff == 1) {
-        out[(int64_t)k.row * s_ob + (int64_t)hq * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
+        uint2 pk;
+        pk.x = pack_bf16x2(num[0] / den, num[1] / den);
+        pk.y = pack_bf16x2(num[2] / den, num[3] / den);
+        *reinterpret_cast<uint2 *>(out + (int64_t)k.row * s_ob + (int64_t)hq * s_oh + d4) = pk;
       } else {
         const int64_t pi = ((int64_t)k.row * nq + hq) * P + k.part;
-        acc_ws[pi * 64 + d] = num;
-        if (d == 0) {
+        *reinterpret_cast<f32x4 *>(acc_ws + pi * 64 + d4) = num;
+        if (d4 == 0) {
           ml_ws[pi * 2] = M;
           ml_ws[pi * 2 + 1] = den;
         }
       }
     }
+    if (NW > 1) lds_write_word(&mseq[bsel], n);  // after the reads above: the buffer may be reused
   };
 
   // The wave's step sequence: (chunk i, step j), i = 0..nmine-1, j = 0..spw-1, in two register
@@ -275,15 +312,16 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
   Meta mcur = meta_load(0);
   Chunk cur, nxt;
   resolve(0, mcur, /*exact=*/false, cur);
-  Meta mnxt = meta_load(1);
-  u32x4 qc0, qc1, qn0, qn1;
-  QkvRaw rc, rn;
-  if (FUSED)
-    load_qkv(cur, 0, mcur, rc);
-  else
-    load_q(cur, 0, qc0, qc1);
+  // the first tile goes out before anything that waits for the lengths or positions
   KTile A[NT], B[NT];
   load_step<NT>(A, va, cur.kr, cur.vr, (uint32_t)(cur.lo + KS * w), tl);
+  Meta mnxt = meta_load(1);
+  u32x4 qc0, qc1, qn0, qn1;
+  QkvRaw rq;  // FUSED: raw qkv / bias / table chunks of the chunk about to start
+  if (FUSED)
+    load_qkv(cur, 0, mcur, rq);
+  else
+    load_q(cur, 0, qc0, qc1);
   int i = 0, j = 0;
   int hi = 0;
   bool fresh = true;  // cur's hi not refined yet
@@ -296,10 +334,7 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
     if (last_tile) {
       resolve(i + 1, mnxt, /*exact=*/true, nxt);
       mnn = meta_load(i + 2);
-      if (FUSED)
-        load_qkv(nxt, i + 1, mnxt, rn);
-      else
-        load_q(nxt, i + 1, qn0, qn1);
+      if (!FUSED) load_q(nxt, i + 1, qn0, qn1);
     }
     {
       // one load sequence for both cases (operands selected): with two, the compiler's wait
@@ -311,11 +346,20 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
     }
     if (fresh) {
       hi = hi_of(cur, mcur, i);
-      if (FUSED) apply_qkv(cur, i, mcur, rc, qc0, qc1);
+      if (FUSED) apply_qkv(cur, i, mcur, rq, qc0, qc1);
       fresh = false;
     }
     const int t0 = cur.lo + KS * (w + NW * j);
     if (t0 < hi) compute_step<NT, FUSED>(X, xv, t0, hi, qc0, qc1, sl2, S, tl, lane, &pt);
+    if (FUSED && j == 0) {
+      // the next chunk's qkv rows go out now, a whole chunk ahead of their use, into the registers this
+      // chunk's rows were just consumed from (no copy at the transition): requested at the chunk's last
+      // step they queued behind a step's worth of tile loads and held up every transition. Their
+      // metadata arrived with the tile just computed.
+      Chunk kn;
+      ids(i + 1, kn);
+      load_qkv(kn, i + 1, mnxt, rq);
+    }
     if (last_tile) {
       const int L = (i < nmine) ? min(max(__builtin_amdgcn_readfirstlane(mcur.lraw), 0), cache_len) : 0;
       const int crow = __builtin_amdgcn_readfirstlane(mcur.craw);
@@ -325,9 +369,7 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
       cur = nxt;
       mcur = mnxt;
       mnxt = mnn;
-      if (FUSED) {
-        rc = rn;
-      } else {
+      if (!FUSED) {
         qc0 = qn0;
         qc1 = qn1;
       }
@@ -337,9 +379,13 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
     ++j;
     return true;
   };
-  for (;;) {
-    if (!step(A, va, B, vb)) break;
-    if (!step(B, vb, A, va)) break;
+  // the first step is peeled: it always takes chunk 0's q (or qkv) from the prologue's loads, so the
+  // loop never sees those loads pending (otherwise registers they wrote, reused later, cost a full drain)
+  if (step(A, va, B, vb)) {
+    for (;;) {
+      if (!step(B, vb, A, va)) break;
+      if (!step(A, va, B, vb)) break;
+    }
   }
   // the request past the last chunk still writes (zeros) into LDS: let it land before the wave ends.
   // s_waitcnt vmcnt(0).
@@ -390,8 +436,8 @@ static void launch_stream(int grid, hipStream_t st, const uint16_t *q, int64_t s
 
 static inline bool al16s(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Body of a8_decode_attn_stream and a8_store_decode_stream (fused = si.qkv != nullptr: q is unused and
-// rowmap is the store's slot array). Checks the decode arguments, launches the streaming kernel and,
+// Body of a8_decode_attn_stream and a8_store_decode_stream (fused = si.qkv != nullptr: q is unused, the
+// store's inputs are in si). Checks the decode arguments, launches the streaming kernel and,
 // for rows longer than a chunk, the merge kernel.
 static int stream_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh, void *kc, void *vc,
                         int64_t s_kb, int64_t s_kh, int64_t s_ks, int cache_rows, int cache_len,
@@ -486,7 +532,7 @@ extern "C" int a8_store_decode_stream(const void *qkv, int64_t s_qkv, const void
                                       void *qo, int64_t s_qo_r, int64_t s_qo_h,
                                       void *kc, void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
                                       int cache_rows, int cache_len, const int32_t *lens,
-                                      void *out, int64_t s_ob, int64_t s_oh,
+                                      const int32_t *rowmap, void *out, int64_t s_ob, int64_t s_oh,
                                       float *acc_ws, float *ml_ws, int64_t ws_row_splits,
                                       int b, int nq, int nkv, int hd, int ring, int waves, int tiles_per_wave,
                                       int grid, float scale, int phases, void *stream) {
@@ -502,6 +548,7 @@ extern "C" int a8_store_decode_stream(const void *qkv, int64_t s_qkv, const void
   if (b > 0 && (phases & 1) == 0)  // the store is part of the streaming kernel
     return set_error(A8_EINVAL, "store_decode_stream: phases must include the streaming kernel (bit 0)");
   StoreIn si{};
+  si.slot = slot;
   si.qkv = (const uint16_t *)qkv;
   si.s_qkv = s_qkv;
   si.bias = (const uint16_t *)bias;
@@ -516,7 +563,7 @@ extern "C" int a8_store_decode_stream(const void *qkv, int64_t s_qkv, const void
   si.ring = ring;
   if (b == 0) return 0;
   return stream_entry("store_decode_stream", nullptr, 0, 0, kc, vc, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
-                      slot, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, b, nq, nkv, hd, waves, tiles_per_wave,
+                      rowmap, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, b, nq, nkv, hd, waves, tiles_per_wave,
                       grid, scale, phases, si, stream);
 }
 

@@ -198,13 +198,13 @@ class DecodeAttention:
         return whole and b * self.nkv >= 2 * grid
 
     def store_and_attend(self, qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, lens, out, nsplit=1,
-                         ring=1 << 30, phases=3, write_q=True):
+                         rowmap=None, ring=1 << 30, phases=3, write_q=True):
         """bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, ...) then
-        self(q, kc, vc, lens, out, nsplit, rowmap=slot): the per-layer pair of fast_engine.py:127-132, in
+        self(q, kc, vc, lens, out, nsplit, rowmap=rowmap): the per-layer pair of fast_engine.py:127-132, in
         one launch (a8_store_decode_stream) when the streaming schedule applies, else as the two calls.
-        Same results bit for bit, given that rows have distinct slots (one slot per request, as in the
-        engine's decode tick; rows sharing a slot, like the fast stack's 2-token first pass, need the two
-        calls). The rotated q is an intermediate of the pair that the engine never reads back: with
+        Same results bit for bit, given that no row attends a cache row another row stores into: the
+        engine's decode tick (slot[r] = r, rowmap None, fast_engine.py:752-753) or distinct slots with
+        rowmap = slot. Rows sharing a slot, like the fast stack's 2-token first pass, need the two calls. The rotated q is an intermediate of the pair that the engine never reads back: with
         write_q=False the single launch does not write it (a saving of ~1 us per layer at the peak load;
         the two-call path always fills q). One difference where the reference is undefined: a row whose
         position lies outside the RoPE tables attends with q = 0 here (the two calls leave its q row
@@ -214,12 +214,14 @@ class DecodeAttention:
         if kind != "stream":
             bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd,
                             ring=ring)
-            return self(q, kc, vc, lens, out, nsplit=nsplit, rowmap=slot, phases=phases)
+            return self(q, kc, vc, lens, out, nsplit=nsplit, rowmap=rowmap, phases=phases)
         _check_i32("lens", lens, R)
+        if rowmap is not None:
+            _check_i32("rowmap", rowmap, R)
         _check_bf16("out", out, 3)
         _need(out.shape[0] >= R and out.shape[1] == self.nq and out.shape[2] == self.hd,
               f"out shape {tuple(out.shape)} does not match [{R}, {self.nq}, {self.hd}]")
-        _check_device(qkv=qkv, kc=kc, lens=lens, out=out, workspace=self.acc_flat)
+        _check_device(qkv=qkv, kc=kc, lens=lens, rowmap=rowmap, out=out, workspace=self.acc_flat)
         if R == 0:
             return out
         nw, tpw, grid = shape
@@ -228,8 +230,8 @@ class DecodeAttention:
             cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.stride(0), cos_tab.shape[0],
             pos.data_ptr(), slot.data_ptr(), q.data_ptr() if write_q else None, q.stride(0), q.stride(1),
             kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
-            lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
-            self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap,
+            lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None, out.data_ptr(), out.stride(0),
+            out.stride(1), self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap,
             R, self.nq, self.nkv, self.hd, ring, nw, tpw, grid, float(self.scale), int(phases), _lib.stream_of(qkv))
         _lib.check(st, "store_and_attend")
         return out

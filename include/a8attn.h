@@ -143,24 +143,27 @@ int a8_decode_choose_stream(int b, int nkv, int cache_len, int64_t cap_row_split
 
 /*
  * The decode tick's per-layer pair in one launch (serve/fast_engine.py:127-132: bias_rope_store, then
- * DecodeAttention with rowmap = slot). Same results as a8_bias_rope_store(qkv, ..., pos, slot, R = b,
- * qo, kc, vc, ...) followed by a8_decode_attn_stream(qo, ..., lens, rowmap = slot, ...) at the same launch
- * shape, bit for bit, provided the b rows have distinct slots. The streaming kernel computes each
- * row's q and new k / v from qkv + bias + RoPE with the store kernel's arithmetic, writes k / v to
- * kc / vc[slot, :, pos % ring] and q to qo (skipped when qo is NULL), and uses the new key column from
+ * DecodeAttention). Same results as a8_bias_rope_store(qkv, ..., pos, slot, R = b, qo, kc, vc, ...)
+ * followed by a8_decode_attn_stream(qo, ..., lens, rowmap, ...) at the same launch shape, bit for bit,
+ * provided no row attends a cache row that another row of the call stores into (true for the engine's
+ * tick: slot = row, rowmap NULL, fast_engine.py:752-753; and for distinct slots with rowmap = slot).
+ * The streaming kernel computes each row's q and new k / v from qkv + bias + RoPE with the store
+ * kernel's arithmetic, writes k / v to kc / vc[slot, :, pos % ring] and q to qo (skipped when qo is
+ * NULL), and, when the row attends the cache row it stores into, takes the new key column from
  * registers. A row whose pos is outside [0, n_tab) stores nothing and attends with q = 0.
- * Arguments: those of a8_bias_rope_store and a8_decode_attn_stream; phases must include bit 0.
+ * rowmap  cache row attended by query row r: rowmap[r], or r when NULL (as in a8_decode_attn_stream).
+ * Other arguments: those of a8_bias_rope_store and a8_decode_attn_stream; phases must include bit 0.
  */
 int a8_store_decode_stream(const void *qkv, int64_t s_qkv, const void *bias,
                            const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab,
                            const int32_t *pos, const int32_t *slot,
                            void *qo, int64_t s_qo_r, int64_t s_qo_h,
                            void *kc, void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
-                           int cache_rows, int cache_len, const int32_t *lens,
+                           int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap,
                            void *out, int64_t s_ob, int64_t s_oh,
                            float *acc_ws, float *ml_ws, int64_t ws_row_splits,
-                           int b, int nq, int nkv, int hd, int ring, int waves, int tiles_per_wave, int grid,
-                           float scale, int phases, void *stream);
+                           int b, int nq, int nkv, int hd, int ring, int waves, int tiles_per_wave,
+                           int grid, float scale, int phases, void *stream);
 
 /*
  * Packed causal prefill attention over keys already stored in cache rows.

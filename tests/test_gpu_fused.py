@@ -1,6 +1,8 @@
 """The fused store + decode launch (a8_store_decode_stream, DecodeAttention.store_and_attend) against the two
-calls it replaces (bias_rope_store, then DecodeAttention with rowmap = slot, fast_engine.py:127-132) at the
-same streaming launch shape: outputs, q and both caches bit for bit."""
+calls it replaces (bias_rope_store, then DecodeAttention, fast_engine.py:127-132) at the same streaming launch
+shape: outputs, q and both caches bit for bit. Both row maps the engine uses: rowmap = slot (distinct slots)
+and rowmap off (the decode tick, fast_engine.py:752-753: row r attends cache row r; here also rows that store
+into a cache row no query row attends)."""
 from __future__ import annotations
 
 import pytest
@@ -29,12 +31,13 @@ def _inputs(seed, b, rows, S, lens, pos, slot, bias=True, max_pos=4096):
                 max_pos=max_pos)
 
 
-def _run_both(a8, dev, x, shape, ring=1 << 30, write_q=True):
+def _run_both(a8, dev, x, shape, ring=1 << 30, write_q=True, use_rowmap=True):
     cos, sin = a8.rope_tables(10000.0, HD, x["max_pos"], dev)
     b = x["qkv"].shape[0]
     d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in x.items()}
     att = a8.DecodeAttention(max(16 * b, 8192), NQ, NKV, HD, 16, dev)
     att.force_stream = shape
+    rowmap = d["slot"] if use_rowmap else None
     res = []
     for fused in (False, True):
         kc, vc = d["kc"].clone(), d["vc"].clone()
@@ -42,10 +45,10 @@ def _run_both(a8, dev, x, shape, ring=1 << 30, write_q=True):
         out = torch.empty(b, NQ, HD, dtype=BF, device=dev)
         if fused:
             att.store_and_attend(d["qkv"], d["bias"], cos, sin, d["pos"], d["slot"], q, kc, vc, d["lens"], out,
-                                 ring=ring, write_q=write_q)
+                                 rowmap=rowmap, ring=ring, write_q=write_q)
         else:
             a8.bias_rope_store(d["qkv"], d["bias"], cos, sin, d["pos"], d["slot"], q, kc, vc, NQ, NKV, HD, ring=ring)
-            att(q, kc, vc, d["lens"], out, rowmap=d["slot"])
+            att(q, kc, vc, d["lens"], out, rowmap=rowmap)
         torch.cuda.synchronize()
         res.append((out.cpu(), q.cpu(), kc.cpu(), vc.cpu()))
     return res
@@ -55,18 +58,26 @@ def _bits_equal(a, b):
     return torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
-def test_store_and_attend_peak_shape(a8, dev):
-    """The C3 launch shape (whole 2048-key rows, 4 waves, 2 units per workgroup), rows at pos = lens - 1
-    in a shuffled slot order."""
-    say("case: fused store+decode, 96 rows x 2048, shape (4, 8, 48)")
+@pytest.mark.parametrize("mode", ["rowmap=slot", "tick", "rowmap off, mixed slots"])
+def test_store_and_attend_peak_shape(a8, dev, mode):
+    """The C3 launch shape (whole 2048-key rows, 4 waves, 2 units per workgroup), rows at pos = lens - 1:
+    shuffled slots attended through the row map; the tick (slot = row, no row map); no row map with some
+    rows storing into their own cache row and others into rows past the query rows (no new key seen)."""
+    say(f"case: fused store+decode, 96 rows x 2048, shape (4, 8, 48), {mode}")
     b, S = 96, 2048
     g = torch.Generator().manual_seed(41)
-    slot = torch.randperm(b + 4, generator=g)[:b].tolist()
+    if mode == "rowmap=slot":
+        slot = torch.randperm(b + 4, generator=g)[:b].tolist()
+    elif mode == "tick":
+        slot = list(range(b))
+    else:
+        slot = [r if r % 3 else b + r // 3 for r in range(b)]
     lens = [S] * (b - 8) + [1, 2, 63, 64, 65, 1000, 2047, 129]
     pos = [L - 1 for L in lens]
-    x = _inputs(41, b, b + 4, S, lens, pos, slot)
+    x = _inputs(41, b, max(slot) + 1, S, lens, pos, slot)
     for write_q in (True, False):
-        (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, (4, 8, 48), write_q=write_q)
+        (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, (4, 8, 48), write_q=write_q,
+                                                       use_rowmap=(mode == "rowmap=slot"))
         assert _bits_equal(q0, q1) if write_q else not q1.any()           # q untouched when not asked for
         assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
         assert _bits_equal(o0, o1)
@@ -92,6 +103,13 @@ def test_store_and_attend_edge_rows(a8, dev, shape):
         assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
         assert _bits_equal(o0, o1)
         assert torch.isnan(o1[12].float()).all()                       # slot 40 does not exist
+    # no row map: row r attends cache row r; rows store into their own row, rows >= b or outside the cache
+    slot2 = [r if r % 2 == 0 else (b + r if r % 4 == 1 else rows + 3) for r in range(b)]
+    x = _inputs(45, b, rows, S, lens, pos, slot2)
+    (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, shape, ring=ring, use_rowmap=False)
+    assert _bits_equal(q0, q1)
+    assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
+    assert _bits_equal(o0, o1)
 
 
 def test_store_and_attend_positions_outside_tables(a8, dev):
