@@ -28,22 +28,6 @@
 
 namespace a8 {
 
-// Inputs of the fused store (a8_store_decode_stream): the bias_rope_store arguments the decode does not
-// already take. Query row r stores into cache row slot[r] and attends cache row rowmap[r] (or r).
-struct StoreIn {
-  const int32_t *slot;
-  const uint16_t *qkv;
-  int64_t s_qkv;
-  const uint16_t *bias;  // nullptr: no bias
-  const uint16_t *cos_tab, *sin_tab;
-  int64_t s_cs;
-  int n_tab;
-  const int32_t *pos;
-  uint16_t *qo;  // nullptr: q is not written out
-  int64_t s_qo_r, s_qo_h;
-  int ring;
-};
-
 // NT = 64-key tiles per pipeline step (decode_tile.h compute_step); tpw is a multiple of NT. With
 // NT = 2, or FUSED (the next chunk's qkv / bias / table chunks are held in registers), a wave may use
 // up to 512 registers (one wave per SIMD).

@@ -149,6 +149,23 @@ struct KVPatch {
   u32x4 lo, hi;
 };
 
+// Inputs of a fused store + decode launch (a8_store_decode_stream, a8_store_decode_flat): the
+// bias_rope_store arguments the decode does not already take. Query row r stores into cache row slot[r]
+// and attends cache row rowmap[r] (or r).
+struct StoreIn {
+  const int32_t *slot;
+  const uint16_t *qkv;
+  int64_t s_qkv;
+  const uint16_t *bias;  // nullptr: no bias
+  const uint16_t *cos_tab, *sin_tab;
+  int64_t s_cs;
+  int n_tab;
+  const int32_t *pos;
+  uint16_t *qo;  // nullptr: q is not written out
+  int64_t s_qo_r, s_qo_h;
+  int ring;
+};
+
 // Replaces key column pt.col (when it lies in [t0, t0 + 64 NT)) in the tiles: its K row in the four
 // lanes that hold it (ka[c][t][*] of lanes r16 = 4 (r / 8) + r % 4, r = column % 32; the k comes from
 // lane kLaneK of the same group by a shuffle), its V row in the LDS tile (chunks permuted as the DMA

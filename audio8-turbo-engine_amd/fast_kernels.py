@@ -127,9 +127,18 @@ class DecodeAttention:
       mode "stream": a8_decode_attn_stream -- a persistent kernel that takes fixed-size key chunks in
         turn (whole rows when there are enough of them), plus a small merge kernel for rows longer than
         a chunk; launch shape from a8_decode_choose_stream.
+      mode "flat": a8_decode_attn_flat -- one launch for any mix of lengths: the kernel splits the
+        rows' actual 64-key tiles evenly over its wavefronts and merges rows spread over several of
+        them itself (counters in self.counters); launch shape from a8_decode_choose_flat. Opt-in:
+        measured on MI355X it does not beat the others at the engine's shapes (a row merged inside the
+        launch pays its memory round trips while the KV stream fills the queues).
       mode "auto" (default): "stream" when every workgroup of its grid gets at least two whole units
-        (row, kv head) of 1024+ keys -- the peak-load shape, where it is measured faster -- else
-        "split" (short, few or ragged rows, where its per-row split sizes win)."""
+        (row, kv head) of 1024+ keys -- the peak-load shape, where it is measured fastest; for the
+        fused store + decode (store_and_attend) also when rows are short (cache_len <= 512: one
+        workgroup per (row, kv head) holds the whole row, so the store, the decode and the merge take
+        one launch); else "split"."""
+
+    FLAT_MAX_ROWS = 2048
 
     def __init__(self, cap_row_splits, nq, nkv, hd, nsplit_max, device, scale=None):
         self.nq, self.nkv, self.hd = nq, nkv, hd
@@ -140,12 +149,16 @@ class DecodeAttention:
         self.scale = scale if scale is not None else hd ** -0.5
         self.acc_flat = torch.empty(self.cap * nq * hd, dtype=torch.float32, device=device)
         self.ml_flat = torch.empty(self.cap * nq * 2, dtype=torch.float32, device=device)
+        # flat mode: one arrival counter per (row, kv head); zero between calls (each call re-zeroes what
+        # it used)
+        self.counters = torch.zeros(self.cap * nkv, dtype=torch.int32, device=device)
         dev = torch.device(device)
         self.n_cu = torch.cuda.get_device_properties(dev).multi_processor_count if dev.type == "cuda" else 1
         self.mode = "auto"
         self.policy = "auto"
         self.force_shape = None   # split mode: (nsplit, waves) pins the launch shape (tuning / tests)
         self.force_stream = None  # stream mode: (waves, tiles_per_wave, grid)
+        self.force_flat = None    # flat mode: grid
         self._shapes = {}
 
     def launch_shape(self, b: int, cache_len: int, nsplit: int):
@@ -180,12 +193,43 @@ class DecodeAttention:
         self._shapes[key] = (nw.value, tpw.value, grid.value)
         return self._shapes[key]
 
-    def schedule(self, b: int, cache_len: int, nsplit: int = 1):
+    def flat_shape(self, b: int, cache_len: int):
+        """Flat mode: (workgroups,)."""
+        if self.force_flat is not None:
+            return (int(self.force_flat),)
+        key = ("flat", b, cache_len)
+        hit = self._shapes.get(key)
+        if hit is not None:
+            return hit
+        grid = ctypes.c_int(0)
+        st = _lib.load().a8_decode_choose_flat(b, self.nkv, cache_len, self.cap, self.n_cu, ctypes.byref(grid))
+        _lib.check(st, "decode_choose_flat")
+        self._shapes[key] = (grid.value,)
+        return self._shapes[key]
+
+    SHORT_ROWS = 512  # fused calls: rows of at most this many cache positions take one workgroup each
+
+    def short_rows_shape(self, b: int, cache_len: int):
+        """Stream mode for short rows: one workgroup per (row, kv head) holding the whole row (up to 4
+        waves, the rest in tiles per wave), so no row needs merging across workgroups."""
+        tiles = max(1, -(-cache_len // 64))
+        nw = 4 if tiles >= 4 else 2 if tiles >= 2 else 1
+        return nw, -(-tiles // nw), b * self.nkv
+
+    def schedule(self, b: int, cache_len: int, nsplit: int = 1, fused: bool = False):
         """The schedule a call with b rows over a cache of cache_len positions uses:
-        ("stream", (waves, tiles_per_wave, grid)) or ("split", (nsplit, waves))."""
-        if self.force_shape is None and (self.force_stream is not None or self.mode == "stream" or
-                                         (self.mode == "auto" and self._stream_pays(b, cache_len))):
-            return "stream", self.stream_shape(b, cache_len)
+        ("stream", (waves, tiles_per_wave, grid)), ("flat", (grid,)) or ("split", (nsplit, waves)).
+        fused: the call is a store_and_attend."""
+        if self.force_shape is None:
+            if self.force_stream is not None or self.mode == "stream":
+                return "stream", self.stream_shape(b, cache_len)
+            if (self.force_flat is not None or self.mode == "flat") and b <= self.FLAT_MAX_ROWS:
+                return "flat", self.flat_shape(b, cache_len)
+            if self.mode == "auto":
+                if self._stream_pays(b, cache_len):
+                    return "stream", self.stream_shape(b, cache_len)
+                if fused and 0 < cache_len <= self.SHORT_ROWS:
+                    return "stream", self.short_rows_shape(b, cache_len)
         nsplit = max(1, min(int(nsplit), self.nsplit_max))
         return "split", self.launch_shape(b, cache_len, nsplit)
 
@@ -210,8 +254,8 @@ class DecodeAttention:
         position lies outside the RoPE tables attends with q = 0 here (the two calls leave its q row
         unwritten)."""
         R = _check_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd, ring)
-        kind, shape = self.schedule(R, kc.shape[2], nsplit)
-        if kind != "stream":
+        kind, shape = self.schedule(R, kc.shape[2], nsplit, fused=True)
+        if kind == "split":
             bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd,
                             ring=ring)
             return self(q, kc, vc, lens, out, nsplit=nsplit, rowmap=rowmap, phases=phases)
@@ -224,15 +268,21 @@ class DecodeAttention:
         _check_device(qkv=qkv, kc=kc, lens=lens, rowmap=rowmap, out=out, workspace=self.acc_flat)
         if R == 0:
             return out
-        nw, tpw, grid = shape
-        st = _lib.load().a8_store_decode_stream(
-            qkv.data_ptr(), qkv.stride(0), bias.data_ptr() if bias is not None else None,
-            cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.stride(0), cos_tab.shape[0],
-            pos.data_ptr(), slot.data_ptr(), q.data_ptr() if write_q else None, q.stride(0), q.stride(1),
-            kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
-            lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None, out.data_ptr(), out.stride(0),
-            out.stride(1), self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap,
-            R, self.nq, self.nkv, self.hd, ring, nw, tpw, grid, float(self.scale), int(phases), _lib.stream_of(qkv))
+        store = (qkv.data_ptr(), qkv.stride(0), bias.data_ptr() if bias is not None else None,
+                 cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.stride(0), cos_tab.shape[0],
+                 pos.data_ptr(), slot.data_ptr(), q.data_ptr() if write_q else None, q.stride(0), q.stride(1),
+                 kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
+                 lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None, out.data_ptr(), out.stride(0),
+                 out.stride(1), self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap)
+        if kind == "flat":
+            (grid,) = shape
+            st = _lib.load().a8_store_decode_flat(*store, self.counters.data_ptr(), self.counters.numel(), R,
+                                                  self.nq, self.nkv, self.hd, ring, grid, float(self.scale),
+                                                  _lib.stream_of(qkv))
+        else:
+            nw, tpw, grid = shape
+            st = _lib.load().a8_store_decode_stream(*store, R, self.nq, self.nkv, self.hd, ring, nw, tpw, grid,
+                                                    float(self.scale), int(phases), _lib.stream_of(qkv))
         _lib.check(st, "store_and_attend")
         return out
 
@@ -266,6 +316,12 @@ class DecodeAttention:
                   lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None,
                   out.data_ptr(), out.stride(0), out.stride(1), self.acc_flat.data_ptr(), self.ml_flat.data_ptr())
         kind, shape = self.schedule(b, kc.shape[2], nsplit)
+        if kind == "flat":
+            (grid,) = shape
+            st = lib.a8_decode_attn_flat(*common, self.cap, self.counters.data_ptr(), self.counters.numel(), b,
+                                         self.nq, self.nkv, self.hd, grid, float(self.scale), _lib.stream_of(q))
+            _lib.check(st, "decode_attention")
+            return out
         if kind == "stream":
             nw, tpw, grid = shape
             st = lib.a8_decode_attn_stream(*common, self.cap, b, self.nq, self.nkv, self.hd, nw, tpw, grid,

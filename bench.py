@@ -170,7 +170,7 @@ def per_config(a8, torch, dev, steps):
                                               outs=outs, fuse=True))
         us = time_median(torch, g, steps, 10) * 1e3 / layers
         nbytes = ref_counts.decode_bytes(lens.tolist(), NQ, NKV, HD)
-        kind, shape = st.attn.schedule(b, S, nsplit)
+        kind, shape = st.attn.schedule(b, S, nsplit, fused=True)
         res[cfg] = {"us_per_layer": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
                     "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
                     "schedule": [kind, list(shape)], "rows": b, "kv_len": int(max(lens)),
@@ -196,12 +196,16 @@ def per_config(a8, torch, dev, steps):
     outs = [torch.empty(2 * b, NQ, HD, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
 
     def c5():
+        # the 2-token pass stores two rows per slot and must store before it attends; the later passes have
+        # one row per slot and no row map (fast_engine.py:710), so they store and attend in one launch
         for (pos, slot, lens_d, rmap, nr), qkv in zip(passes, qkvs):
-            st.forward(qkv, bias, pos, slot, lens_d, nsplit=1, rowmap=rmap, q=q[:nr], outs=[o[:nr] for o in outs])
+            st.forward(qkv, bias, pos, slot, lens_d, nsplit=1, rowmap=rmap, q=q[:nr], outs=[o[:nr] for o in outs],
+                       fuse=not rmap)
 
     g = capture(torch, c5)
     us = time_median(torch, g, steps, 10) * 1e3 / (len(passes) * layers)
     res["C5"] = {"us_per_pass_layer": round(us, 3), "passes": len(passes), "layers": layers, "rows": b,
+                 "schedule": [list(st.attn.schedule(2 * b, S)), list(st.attn.schedule(b, S, fused=True))],
                  "note": "latency bound (<= 1 MB of KV per pass)"}
     del g, st, qkvs, outs
     torch.cuda.empty_cache()
@@ -298,7 +302,7 @@ def main():
     if args.stream_shape:
         st.attn.force_stream = tuple(int(x) for x in args.stream_shape.split(","))
     nsplit_req = a8.ref_nsplit(b, NKV)
-    kind, shape = st.attn.schedule(b, w["S"], nsplit_req)
+    kind, shape = st.attn.schedule(b, w["S"], nsplit_req, fused=True)
     fused = kind == "stream"
     if kind == "stream":
         nw, tpw, grid = shape

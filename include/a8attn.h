@@ -142,6 +142,49 @@ int a8_decode_choose_stream(int b, int nkv, int cache_len, int64_t cap_row_split
                             int *waves_out, int *tiles_per_wave_out, int *grid_out);
 
 /*
+ * Split-K flash-decoding in one launch for any mix of row lengths (replaces the split + combine pair of
+ * serve/fast_kernels.py:193-253 behind DecodeAttention.__call__, 271-290). Same inputs, outputs and
+ * semantics as a8_decode_attn. The kernel reads lens / rowmap, splits the (row, kv head) 64-key tiles
+ * evenly over grid * 4 wavefronts, and merges rows that span several wavefronts inside the launch: the
+ * last wavefront to finish a row (counted with an atomic in counters[row * nkv + kv head]) merges its
+ * partials, in a fixed order, from acc_ws / ml_ws.
+ * counters    int32 [n_counters >= b * nkv], all zero before the first call; every call leaves them
+ *             zero. Shared by the calls of one workspace: calls that overlap on the GPU race.
+ * acc_ws ...  2 * grid * 4 partial slots of (nq / nkv) x 64 floats: grid * 8 <= ws_row_splits * nkv.
+ * b <= 2048 rows per call; grid from a8_decode_choose_flat.
+ */
+int a8_decode_attn_flat(const void *q, int64_t s_qb, int64_t s_qh,
+                        const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                        int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap,
+                        void *out, int64_t s_ob, int64_t s_oh,
+                        float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                        int32_t *counters, int64_t n_counters,
+                        int b, int nq, int nkv, int hd, int grid, float scale, void *stream);
+
+/*
+ * Launch shape of a8_decode_attn_flat / a8_store_decode_flat (replaces the split heuristic of
+ * serve/fast_engine.py:776): workgroups for b rows over a cache of cache_len positions on n_cu compute
+ * units, within a workspace of cap_row_splits row-splits.
+ */
+int a8_decode_choose_flat(int b, int nkv, int cache_len, int64_t cap_row_splits, int n_cu, int *grid_out);
+
+/*
+ * a8_bias_rope_store followed by a8_decode_attn_flat (serve/fast_engine.py:127-132) in one launch, with
+ * the contract of a8_store_decode_stream: same results bit for bit as the two calls, provided no row
+ * attends a cache row that another row of the call stores into.
+ */
+int a8_store_decode_flat(const void *qkv, int64_t s_qkv, const void *bias,
+                         const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab,
+                         const int32_t *pos, const int32_t *slot,
+                         void *qo, int64_t s_qo_r, int64_t s_qo_h,
+                         void *kc, void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                         int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap,
+                         void *out, int64_t s_ob, int64_t s_oh,
+                         float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                         int32_t *counters, int64_t n_counters,
+                         int b, int nq, int nkv, int hd, int ring, int grid, float scale, void *stream);
+
+/*
  * The decode tick's per-layer pair in one launch (serve/fast_engine.py:127-132: bias_rope_store, then
  * DecodeAttention). Same results as a8_bias_rope_store(qkv, ..., pos, slot, R = b, qo, kc, vc, ...)
  * followed by a8_decode_attn_stream(qo, ..., lens, rowmap, ...) at the same launch shape, bit for bit,

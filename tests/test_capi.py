@@ -22,7 +22,8 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     assert set(declared_functions()) == {"a8_version", "a8_last_error", "a8_hip_runtime_path", "a8_bias_rope_store",
                                          "a8_decode_attn", "a8_decode_choose", "a8_decode_attn_stream",
-                                         "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn"}
+                                         "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn",
+                                         "a8_decode_attn_flat", "a8_decode_choose_flat", "a8_store_decode_flat"}
 
 
 def test_library_exports_every_declared_symbol(a8):
@@ -172,3 +173,69 @@ def test_decode_choose_stream_contract(a8):
     # a single long row is cut into chunks to occupy the GPU
     nw, tpw, grid = _choose_stream(lib, 1, S=2048)
     assert -(-2048 // (nw * tpw * 64)) >= 8 and grid >= 8
+
+
+def _flat_args(**kw):
+    a = dict(q=16, s_qb=896, s_qh=64, kc=16, vc=16, s_kb=1024, s_kh=512, s_ks=64, rows=4, S=8, lens=16, rowmap=None,
+             out=16, s_ob=896, s_oh=64, acc=16, ml=16, ws=64, cnt=16, ncnt=8, b=4, nq=14, nkv=2, hd=64, grid=4,
+             scale=0.125, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def _store_flat_args(**kw):
+    a = dict(qkv=16, s_qkv=1152, bias=None, cos=16, sin=16, s_cs=64, n_tab=8, pos=16, slot=16, qo=None, s_qo_r=0,
+             s_qo_h=0, kc=16, vc=16, s_kb=1024, s_kh=512, s_ks=64, rows=4, S=8, lens=16, rowmap=None, out=16,
+             s_ob=896, s_oh=64, acc=16, ml=16, ws=64, cnt=16, ncnt=8, b=4, nq=14, nkv=2, hd=64, ring=1 << 30, grid=4,
+             scale=0.125, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_decode_flat_rejects_before_launch(a8):
+    """Every call here fails its argument checks (or has no rows), so nothing is launched."""
+    lib = a8.load_library()
+    f = lib.a8_decode_attn_flat
+    assert f(*_flat_args(hd=32)) == -3
+    assert f(*_flat_args(nq=34)) == -3                               # GQA group 17
+    assert f(*_flat_args(b=2049, ncnt=8192)) == -3                   # rows per call (metadata in LDS)
+    assert b"2049 rows" in lib.a8_last_error()
+    assert f(*_flat_args(grid=0)) == -1
+    assert f(*_flat_args(cnt=None)) == -1
+    assert f(*_flat_args(grid=17, ws=67)) == -4                      # 2 slots per wave: 136 > 67 * 2
+    assert f(*_flat_args(ncnt=7)) == -4                              # b * nkv counters
+    assert f(*_flat_args(q=8)) == -2
+    assert f(*_flat_args(s_oh=60)) == -2
+    assert f(*_flat_args(s_ks=128)) == -3
+    assert f(*_flat_args(b=0)) == 0
+    g = lib.a8_store_decode_flat
+    assert g(*_store_flat_args(ring=0)) == -1
+    assert g(*_store_flat_args(pos=None)) == -1
+    assert g(*_store_flat_args(qkv=24)) == -2
+    assert g(*_store_flat_args(nq=30)) == -3                         # group 15: lanes 14 / 15 hold k / v
+    assert g(*_store_flat_args(ncnt=7)) == -4
+    assert g(*_store_flat_args(b=0)) == 0
+
+
+def _choose_flat(lib, b, nkv=2, S=2048, cap=8192, n_cu=256):
+    grid = ctypes.c_int()
+    st = lib.a8_decode_choose_flat(b, nkv, S, cap, n_cu, ctypes.byref(grid))
+    return st, grid.value
+
+
+def test_decode_choose_flat_contract(a8):
+    lib = a8.load_library()
+    for b in (1, 2, 16, 64, 192, 384, 2000):
+        for S in (1, 10, 64, 385, 2048, 4096):
+            for cap in (b, 4 * b, 16 * b, 8192):
+                st, grid = _choose_flat(lib, b, S=S, cap=cap)
+                if cap * 2 < 8:                                      # not even one workgroup's slots
+                    assert st == -4
+                    continue
+                assert st == 0 and 1 <= grid <= 256
+                assert 2 * grid * 4 <= cap * 2                       # two partial slots per wave fit
+                assert grid * 4 <= max(4, b * 2 * -(-S // 64) + 3)   # no more waves than tiles (rounded up)
+    assert _choose_flat(lib, 1, S=512) == (0, 4)                     # C1: 16 tiles, one per wave
+    assert _choose_flat(lib, 64, S=4096) == (0, 256)                 # C2: the whole GPU
+    assert _choose_flat(lib, 384, S=10, cap=384) == (0, 96)          # C5 (fast stack workspace)
+

@@ -152,3 +152,24 @@ def test_attn_stack_tick_fused_matches_unfused(a8, dev):
     for i in range(L):
         assert _bits_equal(outs[0][i], outs[1][i])
         assert _bits_equal(st[0].kc[i], st[1].kc[i]) and _bits_equal(st[0].vc[i], st[1].vc[i])
+
+
+@pytest.mark.parametrize("b,S", [(1, 512), (192, 10), (64, 300), (5, 65)])
+def test_store_and_attend_short_rows_auto(a8, ref, dev, b, S):
+    """Mode "auto" runs a fused call over short rows (cache_len <= 512) as one streaming launch with one
+    workgroup per (row, kv head): the same bits as the two calls at that launch shape, and the oracle's
+    answer (the engine's tick: slot = row, no row map)."""
+    say(f"case: fused short rows auto, b={b} S={S}")
+    g = torch.Generator().manual_seed(61)
+    lens = torch.randint(1, S + 1, (b,), generator=g).tolist()
+    pos = [L - 1 for L in lens]
+    x = _inputs(61, b, b, S, lens, pos, list(range(b)), max_pos=S)
+    att = a8.DecodeAttention(max(16 * b, 64), NQ, NKV, HD, 16, dev)
+    kind, shape = att.schedule(b, S, fused=True)
+    assert kind == "stream" and shape[2] == 2 * b and shape[0] * shape[1] * 64 >= S
+    (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, shape, use_rowmap=False)
+    assert _bits_equal(k0, k1) and _bits_equal(v0, v1) and _bits_equal(q0, q1)
+    assert _bits_equal(o0, o1)
+    want = ref.decode_attention(q0, k0, v0, torch.tensor(lens, dtype=torch.int32))
+    assert (o1.float() - want.float()).abs().max().item() <= 2e-2
+
