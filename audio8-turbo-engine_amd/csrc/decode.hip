@@ -25,17 +25,23 @@
 //     exponential is exp2((s - m) * scale * log2 e).
 // This split + combine pair serves any nsplit the caller asks for; the default launch path is the
 // streaming kernel of decode_stream.hip.
+//
+// FUSED (a8_store_decode_split): q and the new k / v come from qkv + bias + RoPE (fused_qkv.h, the
+// store kernel's arithmetic) in every workgroup, split 0's first wave writes them to the cache (and q
+// to qo) like k_bias_rope_store, and the tile holding the new key takes it from registers.
 #include "decode_tile.h"
+#include "fused_qkv.h"
 
 namespace a8 {
 
-template <int NW>
+template <int NW, bool FUSED>
 __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     const uint16_t *__restrict__ q, int64_t s_qb, int64_t s_qh,
-    const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+    uint16_t *kc, uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,  // written when FUSED
     int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
     uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
-    float *__restrict__ ml_ws, int nq, int group, int ns, float scale_log2) {
+    float *__restrict__ ml_ws, int nq, int nkv, int group, int ns, float scale_log2, StoreIn si) {
+  warm_kernargs<256>();  // the explicit arguments above span 0x000-0x0ff and more
   // V tiles of the two pipeline buffers (one per wave each); separate arrays, so the compiler tells
   // their DMA completions apart and waits only for the buffer it reads.
   __shared__ __attribute__((aligned(16))) uint16_t vbA[NW * kVTile];
@@ -46,6 +52,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
 
   int L = lens[row];
   const int crow = rowmap ? rowmap[row] : row;
+  const int p = FUSED ? si.pos[row] : 0, srow = FUSED ? si.slot[row] : 0;
   if (crow < 0 || crow >= cache_rows) L = 0;  // no such cache row: attend nothing
   L = min(max(L, 0), cache_len);
   const int per = ((L + ns - 1) / ns + 63) / 64 * 64;
@@ -56,9 +63,20 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   TileLane tl;
   tl.init(lane);
   // Q^T operand: column r16 = q head kh*group + r16 (zeros past the group).
-  const rsrc_t qr = make_rsrc(q + (int64_t)row * s_qb + (int64_t)kh * group * s_qh, (uint32_t)(group * s_qh * 2));
-  const u32x4 qB0 = bld16(qr, (uint32_t)(r16 * s_qh * 2) + 16u * g);
-  const u32x4 qB1 = bld16(qr, (uint32_t)(r16 * s_qh * 2) + 16u * g + 64u);
+  u32x4 qB0, qB1;
+  KVPatch pt;
+  pt.col = -1;
+  if (FUSED) {
+    QkvRaw rx;
+    const int pu = __builtin_amdgcn_readfirstlane(p);
+    load_qkv_raw(si, true, row, kh, pu, group, nq, nkv, tl, rx);
+    apply_qkv_raw(si, rx, true, row, kh, pu, __builtin_amdgcn_readfirstlane(srow), __builtin_amdgcn_readfirstlane(crow),
+                  cache_rows, cache_len, group, kc, vc, s_kb, s_kh, s_ks, /*store=*/sp == 0 && w == 0, tl, qB0, qB1, pt);
+  } else {
+    const rsrc_t qr = make_rsrc(q + (int64_t)row * s_qb + (int64_t)kh * group * s_qh, (uint32_t)(group * s_qh * 2));
+    qB0 = bld16(qr, (uint32_t)(r16 * s_qh * 2) + 16u * g);
+    qB1 = bld16(qr, (uint32_t)(r16 * s_qh * 2) + 16u * g + 64u);
+  }
   SoftmaxState S;
   S.reset();
 
@@ -81,10 +99,10 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     KTile A[1], B[1];
     for (int k = 0;; k += 2) {
       load_step<1>(A, va, kr, vr, (uint32_t)(first + k * kStep), tl);
-      if (k > 0) compute_step<1>(B, vb, first + (k - 1) * kStep, hi, qB0, qB1, scale_log2, S, tl, lane);
+      if (k > 0) compute_step<1, FUSED>(B, vb, first + (k - 1) * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
       if (k >= n) break;
       load_step<1>(B, vb, kr, vr, (uint32_t)(first + (k + 1) * kStep), tl);
-      compute_step<1>(A, va, first + k * kStep, hi, qB0, qB1, scale_log2, S, tl, lane);
+      compute_step<1, FUSED>(A, va, first + k * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
       if (k + 1 >= n) break;
     }
   }
@@ -169,29 +187,107 @@ __global__ __launch_bounds__(256) void k_decode_combine(const float *__restrict_
   const int row = pair / nq, h = pair - row * nq, d = threadIdx.x & 63;
   const float *ml = ml_ws + (int64_t)pair * ns * 2;
   const float *acc = acc_ws + (int64_t)pair * ns * 64;
-  float M = kNegInf;
-  for (int sp = 0; sp < ns; ++sp) M = fmaxf(M, ml[2 * sp]);
-  float num = 0.f, den = 0.f;
-  for (int sp = 0; sp < ns; ++sp) {
-    const float mv = ml[2 * sp];
-    const float wt = (mv == kNegInf) ? 0.f : fast_exp2((mv - M) * scale_log2);
-    num += wt * acc[sp * 64 + d];
-    den += wt * ml[2 * sp + 1];
+  // one pass with a running maximum (earlier weights rescaled when it grows), eight splits' loads in
+  // flight at a time: the merge costs one memory round trip for up to eight splits
+  constexpr int SB = 8;
+  float M = kNegInf, num = 0.f, den = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += SB) {
+    float mv[SB], lv[SB], av[SB];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      const int sp = min(s0 + i, ns - 1);
+      mv[i] = ml[2 * sp];
+      lv[i] = ml[2 * sp + 1];
+      av[i] = acc[sp * 64 + d];
+    }
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      if (s0 + i >= ns) break;
+      if (mv[i] == kNegInf) continue;  // an empty split adds nothing
+      if (mv[i] > M) {
+        const float sc = (M == kNegInf) ? 0.f : fast_exp2((M - mv[i]) * scale_log2);
+        num *= sc;
+        den *= sc;
+        M = mv[i];
+      }
+      const float wt = fast_exp2((mv[i] - M) * scale_log2);
+      num += wt * av[i];
+      den += wt * lv[i];
+    }
   }
   out[(int64_t)row * s_ob + (int64_t)h * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
 }
 
 static inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <int NW>
+template <int NW, bool FUSED>
 static void launch_split(int ns, int nkv, int b, hipStream_t st, const uint16_t *q, int64_t s_qb, int64_t s_qh,
-                         const uint16_t *kc, const uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
-                         int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap, uint16_t *out,
-                         int64_t s_ob, int64_t s_oh, float *acc_ws, float *ml_ws, int nq, int group,
-                         float scale_log2) {
-  hipLaunchKernelGGL(k_decode_split<NW>, dim3(ns, nkv, b), dim3(64 * NW), 0, st, q, s_qb, s_qh, kc, vc, s_kb,
-                     s_kh, s_ks, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, nq, group,
-                     ns, scale_log2);
+                         uint16_t *kc, uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks, int cache_rows,
+                         int cache_len, const int32_t *lens, const int32_t *rowmap, uint16_t *out, int64_t s_ob,
+                         int64_t s_oh, float *acc_ws, float *ml_ws, int nq, int group, float scale_log2,
+                         const StoreIn &si) {
+  auto kern = k_decode_split<NW, FUSED>;
+  hipLaunchKernelGGL(kern, dim3(ns, nkv, b), dim3(64 * NW), 0, st, q, s_qb, s_qh, kc, vc, s_kb, s_kh, s_ks,
+                     cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, nq, nkv, group, ns,
+                     scale_log2, si);
+}
+
+// Body of a8_decode_attn and a8_store_decode_split (fused = si.qkv != nullptr: q is unused, the store's
+// inputs are in si).
+static int split_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh, void *kc, void *vc, int64_t s_kb,
+                       int64_t s_kh, int64_t s_ks, int cache_rows, int cache_len, const int32_t *lens,
+                       const int32_t *rowmap, void *out, int64_t s_ob, int64_t s_oh, float *acc_ws, float *ml_ws,
+                       int64_t ws_row_splits, int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
+                       int phases, const StoreIn &si, void *stream) {
+  const bool fused = si.qkv != nullptr;
+  if (hd != 64) return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64 only)", fn, hd);
+  if (b < 0 || nq <= 0 || nkv <= 0 || nq % nkv || cache_rows < 0 || cache_len < 0 || nsplit < 1 || b > 65535)
+    return set_error(A8_EINVAL, "%s: bad sizes b=%d nq=%d nkv=%d nsplit=%d", fn, b, nq, nkv, nsplit);
+  const int group = nq / nkv;
+  if (group > (fused ? kLaneK : 16))
+    return set_error(A8_EUNSUP, "%s: GQA group %d > %d not supported", fn, group, fused ? kLaneK : 16);
+  if (waves != 1 && waves != 2 && waves != 4 && waves != 8)
+    return set_error(A8_EINVAL, "%s: waves must be 1, 2, 4 or 8 (got %d)", fn, waves);
+  if (b == 0) return 0;
+  if ((!fused && !q) || !kc || !vc || !lens || !out) return set_error(A8_EINVAL, "%s: null pointer", fn);
+  if (nsplit > 1 && (!acc_ws || !ml_ws || (int64_t)b * nsplit > ws_row_splits))
+    return set_error(A8_EWSPACE, "%s: workspace holds %lld row-splits, need b*nsplit = %lld", fn,
+                     (long long)ws_row_splits, (long long)b * nsplit);
+  if (s_ks != hd)
+    return set_error(A8_EUNSUP, "%s: cache positions must be contiguous rows (s_ks %lld)", fn, (long long)s_ks);
+  if ((!fused && !al16(q)) || !al16(kc) || !al16(vc) || !al16(out) || (nsplit > 1 && !al16(acc_ws)) ||
+      ((fused ? 0 : (s_qb | s_qh)) | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
+    return set_error(A8_EALIGN, "%s: pointers must be 16-byte aligned and strides multiples of 8", fn);
+  const hipStream_t st = (hipStream_t)stream;
+  const float sl2 = scale * kLog2e;
+  const auto *qq = (const uint16_t *)q;
+  auto *kk = (uint16_t *)kc;
+  auto *vv = (uint16_t *)vc;
+  auto *oo = (uint16_t *)out;
+  if (phases & 1) {
+#define A8_SPLIT_ARGS nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens, \
+                      rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2, si
+    switch (waves * 2 + (fused ? 1 : 0)) {
+      case 2: launch_split<1, false>(A8_SPLIT_ARGS); break;
+      case 3: launch_split<1, true>(A8_SPLIT_ARGS); break;
+      case 4: launch_split<2, false>(A8_SPLIT_ARGS); break;
+      case 5: launch_split<2, true>(A8_SPLIT_ARGS); break;
+      case 8: launch_split<4, false>(A8_SPLIT_ARGS); break;
+      case 9: launch_split<4, true>(A8_SPLIT_ARGS); break;
+      case 17: launch_split<8, true>(A8_SPLIT_ARGS); break;
+      default: launch_split<8, false>(A8_SPLIT_ARGS); break;
+    }
+#undef A8_SPLIT_ARGS
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  if ((phases & 2) && nsplit > 1) {
+    const unsigned grid = (unsigned)(((int64_t)b * nq + 3) / 4);
+    hipLaunchKernelGGL(k_decode_combine, dim3(grid), dim3(256), 0, st, acc_ws, ml_ws, oo, s_ob, s_oh, b, nq,
+                       nsplit, sl2);
+    return (int)hipGetLastError();
+  }
+  return 0;
 }
 
 }  // namespace a8
@@ -205,50 +301,48 @@ extern "C" int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
                               int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
                               int phases, void *stream) {
   using namespace a8;
-  if (hd != 64) return set_error(A8_EUNSUP, "decode_attn: head_dim %d not supported (64 only)", hd);
-  if (b < 0 || nq <= 0 || nkv <= 0 || nq % nkv || cache_rows < 0 || cache_len < 0 || nsplit < 1 || b > 65535)
-    return set_error(A8_EINVAL, "decode_attn: bad sizes b=%d nq=%d nkv=%d nsplit=%d", b, nq, nkv, nsplit);
-  const int group = nq / nkv;
-  if (group > 16) return set_error(A8_EUNSUP, "decode_attn: GQA group %d > 16 not supported", group);
-  if (waves != 1 && waves != 2 && waves != 4 && waves != 8)
-    return set_error(A8_EINVAL, "decode_attn: waves must be 1, 2, 4 or 8 (got %d)", waves);
-  if (b == 0) return 0;
-  if (!q || !kc || !vc || !lens || !out) return set_error(A8_EINVAL, "decode_attn: null pointer");
-  if (nsplit > 1 && (!acc_ws || !ml_ws || (int64_t)b * nsplit > ws_row_splits))
-    return set_error(A8_EWSPACE, "decode_attn: workspace holds %lld row-splits, need b*nsplit = %lld",
-                     (long long)ws_row_splits, (long long)b * nsplit);
-  if (s_ks != hd) return set_error(A8_EUNSUP, "decode_attn: cache positions must be contiguous rows (s_ks %lld)",
-                                   (long long)s_ks);
-  if (!al16(q) || !al16(kc) || !al16(vc) || !al16(out) || (nsplit > 1 && !al16(acc_ws)) ||
-      (s_qb | s_qh | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
-    return set_error(A8_EALIGN, "decode_attn: pointers must be 16-byte aligned and strides multiples of 8");
-  const hipStream_t st = (hipStream_t)stream;
-  const float sl2 = scale * kLog2e;
-  const auto *qq = (const uint16_t *)q;
-  const auto *kk = (const uint16_t *)kc;
-  const auto *vv = (const uint16_t *)vc;
-  auto *oo = (uint16_t *)out;
-  if (phases & 1) {
-    switch (waves) {
-      case 1: launch_split<1>(nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
-                              lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2); break;
-      case 2: launch_split<2>(nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
-                              lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2); break;
-      case 4: launch_split<4>(nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
-                              lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2); break;
-      default: launch_split<8>(nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len,
-                               lens, rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2); break;
-    }
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-  }
-  if ((phases & 2) && nsplit > 1) {
-    const unsigned grid = (unsigned)(((int64_t)b * nq + 3) / 4);
-    hipLaunchKernelGGL(k_decode_combine, dim3(grid), dim3(256), 0, st, acc_ws, ml_ws, oo, s_ob, s_oh, b, nq,
-                       nsplit, sl2);
-    return (int)hipGetLastError();
-  }
-  return 0;
+  const StoreIn none{};
+  return split_entry("decode_attn", q, s_qb, s_qh, const_cast<void *>(kc), const_cast<void *>(vc), s_kb, s_kh, s_ks,
+                     cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, b, nq, nkv,
+                     hd, nsplit, waves, scale, phases, none, stream);
+}
+
+extern "C" int a8_store_decode_split(const void *qkv, int64_t s_qkv, const void *bias,
+                                     const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab,
+                                     const int32_t *pos, const int32_t *slot,
+                                     void *qo, int64_t s_qo_r, int64_t s_qo_h,
+                                     void *kc, void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                                     int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap,
+                                     void *out, int64_t s_ob, int64_t s_oh,
+                                     float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                                     int b, int nq, int nkv, int hd, int ring, int nsplit, int waves, float scale,
+                                     int phases, void *stream) {
+  using namespace a8;
+  if (ring <= 0 || n_tab < 0) return set_error(A8_EINVAL, "store_decode_split: bad ring %d / n_tab %d", ring, n_tab);
+  if (b > 0 && (!qkv || !cos_tab || !sin_tab || !pos || !slot))
+    return set_error(A8_EINVAL, "store_decode_split: null pointer");
+  if (b > 0 && (!al16(qkv) || !al16(cos_tab) || !al16(sin_tab) || (bias && !al16(bias)) || (qo && !al16(qo)) ||
+                (s_qkv | s_cs | (qo ? (s_qo_r | s_qo_h) : 0)) & 7))
+    return set_error(A8_EALIGN, "store_decode_split: pointers must be 16-byte aligned and strides multiples of 8");
+  if (b > 0 && (phases & 1) == 0)  // the store is part of the split kernel
+    return set_error(A8_EINVAL, "store_decode_split: phases must include the split kernel (bit 0)");
+  StoreIn si{};
+  si.slot = slot;
+  si.qkv = (const uint16_t *)qkv;
+  si.s_qkv = s_qkv;
+  si.bias = (const uint16_t *)bias;
+  si.cos_tab = (const uint16_t *)cos_tab;
+  si.sin_tab = (const uint16_t *)sin_tab;
+  si.s_cs = s_cs;
+  si.n_tab = n_tab;
+  si.pos = pos;
+  si.qo = (uint16_t *)qo;
+  si.s_qo_r = s_qo_r;
+  si.s_qo_h = s_qo_h;
+  si.ring = ring;
+  return split_entry("store_decode_split", nullptr, 0, 0, kc, vc, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
+                     rowmap, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, b, nq, nkv, hd, nsplit, waves, scale,
+                     phases, si, stream);
 }
 
 // Launch-shape policy (measured on MI355X at 192 slots x 2048 keys: one split of 4 waves per
@@ -275,7 +369,10 @@ extern "C" int a8_decode_choose(int b, int nkv, int cache_len, int nsplit_req, i
   if (ns > tiles) ns = tiles;
   if (cap_row_splits >= 1 && ns > cap_row_splits / b) ns = cap_row_splits / b;
   if (ns < 1) ns = 1;
+  // once the splits give every compute unit a workgroup, one wave per split: no merge across waves
+  // (measured at 64 ragged rows over a 4096-key cache: 4 x 1 waves 15.1 us/layer against 4 x 4 15.8)
+  const int nw_out = (ns > 1 && units * ns >= n_cu) ? 1 : nw;
   *nsplit_out = (int)ns;
-  *waves_out = nw;
+  *waves_out = nw_out;
   return 0;
 }

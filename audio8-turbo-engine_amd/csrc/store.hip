@@ -22,6 +22,7 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     uint16_t *__restrict__ qo, int64_t s_qo_r, int64_t s_qo_h,
     uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
     int cache_rows, int cache_len, int nq, int nkv, int ring) {
+  warm_kernargs<164>();  // the explicit arguments above span 0x00-0xa3
   const int H = nq + 2 * nkv;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (int64_t)R * H * 4) return;

@@ -244,21 +244,18 @@ class DecodeAttention:
     def store_and_attend(self, qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, lens, out, nsplit=1,
                          rowmap=None, ring=1 << 30, phases=3, write_q=True):
         """bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, ...) then
-        self(q, kc, vc, lens, out, nsplit, rowmap=rowmap): the per-layer pair of fast_engine.py:127-132, in
-        one launch (a8_store_decode_stream) when the streaming schedule applies, else as the two calls.
+        self(q, kc, vc, lens, out, nsplit, rowmap=rowmap): the per-layer pair of fast_engine.py:127-132 with
+        the store done by the decode's own kernel (a8_store_decode_stream / _split / _flat, whichever
+        schedule the call takes): one launch, or two with the split schedule's combine.
         Same results bit for bit, given that no row attends a cache row another row stores into: the
         engine's decode tick (slot[r] = r, rowmap None, fast_engine.py:752-753) or distinct slots with
-        rowmap = slot. Rows sharing a slot, like the fast stack's 2-token first pass, need the two calls. The rotated q is an intermediate of the pair that the engine never reads back: with
-        write_q=False the single launch does not write it (a saving of ~1 us per layer at the peak load;
-        the two-call path always fills q). One difference where the reference is undefined: a row whose
-        position lies outside the RoPE tables attends with q = 0 here (the two calls leave its q row
-        unwritten)."""
+        rowmap = slot. Rows sharing a slot, like the fast stack's 2-token first pass, need the two calls.
+        The rotated q is an intermediate of the pair that the engine never reads back: with write_q=False
+        it is not written (a saving of ~1 us per layer at the peak load). One difference where the
+        reference is undefined: a row whose position lies outside the RoPE tables attends with q = 0 here
+        (the two calls leave its q row unwritten)."""
         R = _check_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd, ring)
         kind, shape = self.schedule(R, kc.shape[2], nsplit, fused=True)
-        if kind == "split":
-            bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd,
-                            ring=ring)
-            return self(q, kc, vc, lens, out, nsplit=nsplit, rowmap=rowmap, phases=phases)
         _check_i32("lens", lens, R)
         if rowmap is not None:
             _check_i32("rowmap", rowmap, R)
@@ -274,7 +271,11 @@ class DecodeAttention:
                  kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
                  lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None, out.data_ptr(), out.stride(0),
                  out.stride(1), self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap)
-        if kind == "flat":
+        if kind == "split":
+            ns, nw = shape
+            st = _lib.load().a8_store_decode_split(*store, R, self.nq, self.nkv, self.hd, ring, ns, nw,
+                                                   float(self.scale), int(phases), _lib.stream_of(qkv))
+        elif kind == "flat":
             (grid,) = shape
             st = _lib.load().a8_store_decode_flat(*store, self.counters.data_ptr(), self.counters.numel(), R,
                                                   self.nq, self.nkv, self.hd, ring, grid, float(self.scale),

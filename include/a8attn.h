@@ -142,6 +142,23 @@ int a8_decode_choose_stream(int b, int nkv, int cache_len, int64_t cap_row_split
                             int *waves_out, int *tiles_per_wave_out, int *grid_out);
 
 /*
+ * a8_bias_rope_store followed by a8_decode_attn (serve/fast_engine.py:127-132) with the store done by
+ * the split kernel: two launches (split, combine) instead of three, with the contract of
+ * a8_store_decode_stream (same results bit for bit as the two calls at the same nsplit / waves, provided
+ * no row attends a cache row that another row of the call stores into). phases must include bit 0.
+ */
+int a8_store_decode_split(const void *qkv, int64_t s_qkv, const void *bias,
+                          const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab,
+                          const int32_t *pos, const int32_t *slot,
+                          void *qo, int64_t s_qo_r, int64_t s_qo_h,
+                          void *kc, void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                          int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap,
+                          void *out, int64_t s_ob, int64_t s_oh,
+                          float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                          int b, int nq, int nkv, int hd, int ring, int nsplit, int waves, float scale,
+                          int phases, void *stream);
+
+/*
  * Split-K flash-decoding in one launch for any mix of row lengths (replaces the split + combine pair of
  * serve/fast_kernels.py:193-253 behind DecodeAttention.__call__, 271-290). Same inputs, outputs and
  * semantics as a8_decode_attn. The kernel reads lens / rowmap, splits the (row, kv head) 64-key tiles
