@@ -101,6 +101,22 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max(a, b, c) as one v_maximum3_f32 (IEEE 754-2019 maximum: a NaN input gives NaN). fmaxf() on values
+// the compiler cannot prove canonical (MFMA results) first quiets each input with a v_max x, x of its own;
+// maximum needs no quieting. Written with the builtin (not asm) so the compiler still inserts the wait
+// states between an MFMA and a VALU read of its result.
+__device__ __forceinline__ float max3_ieee(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+__device__ __forceinline__ float max_ieee(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+// max_over_groups with maximum instead of fmaxf
+__device__ __forceinline__ float max_over_groups_ieee(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = max_ieee(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return max_ieee(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // Cross-lane reductions over the four 16-lane groups of a wave (lanes l, l^16, l^32, l^48), with the
 // gfx950 lane swaps (VALU, no LDS round trip): v_permlane16_swap(v, v) yields the values of the even and
 // the odd 16-lane row of each row pair, v_permlane32_swap(v, v) those of the lower and the upper 32

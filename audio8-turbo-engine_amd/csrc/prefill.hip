@@ -24,11 +24,14 @@
 //     wholly below the causal diagonal skip the mask; the accumulator rescale is skipped when no max
 //     moved), O^T += V^T . P^T with the S^T C-layout reused as the P^T B operand (key rows permuted
 //     within 32-key chunks, as in the decode kernel).
+#include <type_traits>
+
 #include "decode_tile.h"
 
 namespace a8 {
 
-constexpr int kPfMaxHW = 8;   // q heads (waves) per workgroup
+constexpr int kPfMaxHW = 4;   // q heads (waves) per workgroup: two workgroups fit a compute unit's LDS
+constexpr float kPfLazy = 8.f;  // exp2 units a column's running max may lag behind its scores
 
 // K chunk permutation of tile row r (see above).
 __device__ __forceinline__ int pf_kswz(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
@@ -56,11 +59,14 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     const int32_t *__restrict__ bq0, const int32_t *__restrict__ bn, const int32_t *__restrict__ bslot,
     const int32_t *__restrict__ bpos0, int group, int hsplit, int hpw, float sl2) {
   warm_kernargs<152>();  // the explicit arguments above span 0x00-0x97
-  // two K and two V tile buffers, separate arrays so the compiler tells their DMA apart
+  // a ring of three K and three V tile buffers (tiles are requested two ahead), separate arrays so the
+  // compiler tells their DMA apart
   __shared__ __attribute__((aligned(16))) uint16_t kA[kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t kB[kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t kC[kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vA[kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vB[kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t vC[kVTile];
   // Q^T operands of every wave's query groups, parked in LDS (8 KB per wave) to keep registers for the
   // accumulators: [wave][group][dim half][lane] x 16 bytes
   __shared__ __attribute__((aligned(16))) uint16_t qs[kPfMaxHW * 4 * 2 * 64 * 8];
@@ -133,13 +139,32 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   auto issue = [&](int t, uint16_t *kt, uint16_t *vt) __attribute__((always_inline)) {
     for (int i = w; i < 16; i += nw) pf_dma(i, (uint32_t)(64 * t), kr, vr, kt, vt, kd0, kd1, vd0, vd1);
   };
-  // tile t (in kt / vt) requested by every wave: own DMA complete, then meet (which also retires the
-  // previous tile's LDS reads before its buffers are refilled). s_waitcnt vmcnt(0).
-  auto ready = [&]() __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+  // tile t requested by every wave: this wave's share of it complete (with the next tile's share still in
+  // flight when `ahead`: loads complete in order and every wave issues at least 16 / nw instructions a
+  // tile, so at most that many may stay outstanding), then meet -- which also retires every wave's LDS
+  // reads of the buffer the next request will refill.
+  auto ready = [&](bool ahead) __attribute__((always_inline)) {
+    if (ahead) {
+      switch (nw) {  // s_waitcnt vmcnt(16 / nw)
+        case 1: __builtin_amdgcn_s_waitcnt(0x4F70); break;
+        case 2: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+        case 3: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+        default: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+      }
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    }
     lds_barrier();
   };
-  auto compute = [&](int t, const uint16_t *kt, const uint16_t *vtile) __attribute__((always_inline)) {
+  // Lazy running maximum: a column's max (the exp2 offset) is raised only when a tile's score exceeds it
+  // by more than kPfLazy in exp2 units, so most tiles skip the accumulator rescale; until then its
+  // weights stay below 2^kPfLazy (well inside bf16's range; the sums are fp32). Same softmax, the
+  // rounding happens at other points.
+  const float thr = kPfLazy / sl2;  // in raw score units
+  // MASKED: a tile that crosses the causal diagonal or the range end. The two kinds run in separate
+  // loops (all full tiles first), so no scores move between registers for a shared continuation.
+  auto compute = [&](auto masked_tag, int t, const uint16_t *kt, const uint16_t *vtile) __attribute__((always_inline)) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     if (!active) return;
     const int kt0 = 64 * t;
     // operands of the tile, read once: K rows (A of S^T; tile (c, tt) row 4g+i <-> key
@@ -161,8 +186,6 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
         const u32x2 lo = lds_tr16(vp), hi2 = lds_tr16(vp + 4 * kRow);
         va[dt][c] = u32x4{lo[0], lo[1], hi2[0], hi2[1]};
       }
-    // tiles wholly below the causal diagonal and inside the range skip the mask
-    const bool full = kt0 + 63 <= p0 && kt0 + 64 <= hi;
 #pragma unroll
     for (int k = 0; k < UPW; ++k) {
       // one query group at a time: no interleaving of the groups' score / weight registers
@@ -174,32 +197,34 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
           s[c][tt] = mfma16x16x32(ka[c][tt][1], qb1, mfma16x16x32(ka[c][tt][0], qb0, f32x4{0.f, 0.f, 0.f, 0.f}));
-      float mt = kNegInf;
-      if (full) {
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
-            mt = fmaxf(mt, fmaxf(fmaxf(s[c][tt][0], s[c][tt][1]), fmaxf(s[c][tt][2], s[c][tt][3])));
-      } else {
+      if (MASKED) {
         const int lim = min(p0 + 16 * qt_of[k] + r16, hi - 1);  // keys <= query position (and < hi)
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int key = kt0 + 32 * c + 8 * g + 4 * tt + i;
-              const float v = key <= lim ? s[c][tt][i] : kNegInf;
-              s[c][tt][i] = v;
-              mt = fmaxf(mt, v);
-            }
+            for (int i = 0; i < 4; ++i)
+              if (kt0 + 32 * c + 8 * g + 4 * tt + i > lim) s[c][tt][i] = kNegInf;
       }
-      mt = max_over_groups(mt);
-      const float mn = fmaxf(mrun[k], mt);
-      // mn stays -inf only for a column with no key yet (a padding row): keep it inert.
-      const float mc = mn == kNegInf ? 0.f : mn * sl2;
-      const float alpha = (mrun[k] == kNegInf) ? 0.f : fast_exp2(__builtin_fmaf(mrun[k], sl2, -mc));
+      float mt = max3_ieee(s[0][0][0], s[0][0][1], s[0][0][2]);
+      mt = max3_ieee(mt, s[0][0][3], s[0][1][0]);
+      mt = max3_ieee(mt, s[0][1][1], s[0][1][2]);
+      mt = max3_ieee(mt, s[0][1][3], s[1][0][0]);
+      mt = max3_ieee(mt, s[1][0][1], s[1][0][2]);
+      mt = max3_ieee(mt, s[1][0][3], s[1][1][0]);
+      mt = max3_ieee(mt, s[1][1][1], s[1][1][2]);
+      mt = max_over_groups_ieee(max_ieee(mt, s[1][1][3]));
+      if (__ballot(mt > mrun[k] + thr)) {  // some column's max moved by more than kPfLazy: raise all
+        const float mn = fmaxf(mrun[k], mt);
+        const float alpha = (mrun[k] == kNegInf) ? 0.f : fast_exp2((mrun[k] - mn) * sl2);
+        lrun[k] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[k][dt] *= alpha;
+        mrun[k] = mn;
+      }
+      // mrun stays -inf only for a column with no key yet (a padding row): keep it inert.
+      const float mc = mrun[k] == kNegInf ? 0.f : mrun[k] * sl2;
       float ps = 0.f;
       u32x4 pB[2];
 #pragma unroll
@@ -215,12 +240,7 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
           pB[c][2 * tt] = pack_bf16x2(pv[0], pv[1]);
           pB[c][2 * tt + 1] = pack_bf16x2(pv[2], pv[3]);
         }
-      lrun[k] = lrun[k] * alpha + ps;
-      mrun[k] = mn;
-      if (__ballot(alpha != 1.f)) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[k][dt] *= alpha;
-      }
+      lrun[k] += ps;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -228,16 +248,46 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     }
   };
 
+  // tiles [0, nfull) lie wholly below the causal diagonal (every query row sees every key) and inside the
+  // range; the rest -- at most two, as a block holds at most 64 positions -- cross it. Tile t sits in
+  // buffer t % 3; tiles t + 1 and t + 2 are in flight while t is computed.
+  const int nfull = min(max((p0 + 1) / 64, 0), hi / 64);
   issue(0, kA, vA);
-  for (int t = 0;; t += 2) {
-    ready();
-    if (t + 1 < ntile) issue(t + 1, kB, vB);
-    compute(t, kA, vA);
-    if (t + 1 >= ntile) break;
-    ready();
-    if (t + 2 < ntile) issue(t + 2, kA, vA);
-    compute(t + 1, kB, vB);
-    if (t + 2 >= ntile) break;
+  if (ntile > 1) issue(1, kB, vB);
+  int t = 0;
+  if (nfull > 0) {
+    for (;; t += 3) {
+      ready(t + 1 < ntile);
+      if (t + 2 < ntile) issue(t + 2, kC, vC);
+      compute(std::false_type{}, t, kA, vA);
+      if (t + 1 >= nfull) {
+        t += 1;
+        break;
+      }
+      ready(t + 2 < ntile);
+      if (t + 3 < ntile) issue(t + 3, kA, vA);
+      compute(std::false_type{}, t + 1, kB, vB);
+      if (t + 2 >= nfull) {
+        t += 2;
+        break;
+      }
+      ready(t + 3 < ntile);
+      if (t + 4 < ntile) issue(t + 4, kB, vB);
+      compute(std::false_type{}, t + 2, kC, vC);
+      if (t + 3 >= nfull) {
+        t += 3;
+        break;
+      }
+    }
+  }
+  // the diagonal tiles: every request has gone out (t + 2 >= ntile here), so one instantiation with the
+  // buffer picked at run time costs no overlap
+  for (; t < ntile; ++t) {
+    ready(false);
+    const int bsel = t % 3;
+    const uint16_t *kt = bsel == 0 ? kA : bsel == 1 ? kB : kC;
+    const uint16_t *vtb = bsel == 0 ? vA : bsel == 1 ? vB : vC;
+    compute(std::true_type{}, t, kt, vtb);
   }
   // the last request may still write (zeros, past the range) into LDS: let it land before the end
   __builtin_amdgcn_s_waitcnt(0x0F70);

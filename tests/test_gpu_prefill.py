@@ -84,6 +84,31 @@ def test_prefill_c4_full(a8, ref, dev):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("seed", [0, 1])
+def test_prefill_random_cache(a8, ref, dev, seed):
+    """16 requests, n ~ U[40, 400], after a 300-position prefix, over a cache and queries drawn at random
+    (no store first): every output row finite and within the bar of the oracle."""
+    say(f"case: prefill random cache, seed {seed}")
+    g = torch.Generator().manual_seed(100 + seed)
+    ns = torch.randint(40, 401, (16,), generator=g).tolist()
+    p0, S, nreq = 300, 704, 16
+    R = sum(ns)
+    kc, vc = randn_bf16(g, nreq + 1, NKV, S, HD), randn_bf16(g, nreq + 1, NKV, S, HD)
+    q = randn_bf16(g, R, NQ, HD)
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    want = torch.zeros(R, NQ, HD, dtype=BF)
+    ref.prefill_attention(q, kc, vc, *ref.prefill_plan(r0s, ns, list(range(nreq)), [p0] * nreq), want, 7)
+    out = torch.full((R, NQ, HD), float("nan"), dtype=BF, device=dev)
+    a8.prefill_attention(q.to(dev), kc.to(dev), vc.to(dev), a8.PrefillPlan(r0s, ns, list(range(nreq)), [p0] * nreq, dev),
+                         out, 7)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert torch.isfinite(got.float()).all()
+    err = maxabs(got, want)
+    say(f"  R={R} max-abs {err:.3e}")
+    assert err <= TOL
+
+
 def test_prefill_graph_mode_plan(a8, ref, dev):
     """The graph-mode plan buffer (padding blocks point at the scratch row with n = 0) gives the same rows as
     an exact PrefillPlan, and leaves rows past the packed tokens untouched."""
