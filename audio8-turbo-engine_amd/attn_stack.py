@@ -19,7 +19,7 @@ from types import SimpleNamespace
 import numpy as np
 import torch
 
-from .fast_kernels import DecodeAttention, PrefillPlan, bias_rope_store, prefill_attention
+from .fast_kernels import DecodeAttention, PrefillPlan, bias_rope_store, heaviest_first, prefill_attention
 
 
 def rope_tables(base, hd, n, dev):
@@ -120,21 +120,22 @@ class PrefillMeta:
 
     def host(self, nt, slots, ns, starts):
         """Host int32 contents for requests of ns tokens at positions starts.. in slots, packed in order
-        (fast_engine.py:837-853)."""
+        (fast_engine.py:837-853); the query blocks are listed heaviest first (see PrefillPlan)."""
         BM, o = PrefillPlan.BM, self.off
         m = np.zeros(int(o[-1]), np.int32)
         pos, slot, q0, n, bslot, p0, last, st, cpos = (m[o[i]:o[i + 1]] for i in range(9))
         slot[:], bslot[:], st[:] = self.scr, self.scr, self.scr
-        r0 = bi = 0
+        r0, blocks = 0, []
         for k, (s, cnt, a) in enumerate(zip(slots, ns, starts)):
             pos[r0:r0 + cnt] = np.arange(a, a + cnt)
             slot[r0:r0 + cnt] = s
-            for off in range(0, cnt, BM):
-                q0[bi], n[bi], bslot[bi], p0[bi] = r0 + off, min(BM, cnt - off), s, a + off
-                bi += 1
+            blocks += [(r0 + off, min(BM, cnt - off), s, a + off) for off in range(0, cnt, BM)]
             last[k], st[k], cpos[k] = r0 + cnt - 1, s, a + cnt
             r0 += cnt
+        bi = len(blocks)
         assert r0 <= nt and bi <= nt // BM + self.NR and len(slots) <= self.NR
+        if bi:  # heaviest first, as in PrefillPlan
+            q0[:bi], n[:bi], bslot[:bi], p0[:bi] = zip(*heaviest_first(blocks))
         return m
 
     def load(self, nt, slots, ns, starts):

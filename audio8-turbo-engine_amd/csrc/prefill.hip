@@ -57,8 +57,8 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
     int cache_rows, int cache_len, uint16_t *__restrict__ out, int64_t s_or, int64_t s_oh,
     const int32_t *__restrict__ bq0, const int32_t *__restrict__ bn, const int32_t *__restrict__ bslot,
-    const int32_t *__restrict__ bpos0, int group, int hsplit, int hpw, float sl2) {
-  warm_kernargs<152>();  // the explicit arguments above span 0x00-0x97
+    const int32_t *__restrict__ bpos0, int group, int hsplit, int hpw, float sl2, int nh) {
+  warm_kernargs<156>();  // the explicit arguments above span 0x00-0x9b
   // a ring of three K and three V tile buffers (tiles are requested two ahead), separate arrays so the
   // compiler tells their DMA apart
   __shared__ __attribute__((aligned(16))) uint16_t kA[kVTile];
@@ -70,8 +70,10 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // Q^T operands of every wave's query groups, parked in LDS (8 KB per wave) to keep registers for the
   // accumulators: [wave][group][dim half][lane] x 16 bytes
   __shared__ __attribute__((aligned(16))) uint16_t qs[kPfMaxHW * 4 * 2 * 64 * 8];
-  const int blk = blockIdx.x;
-  const int kh = blockIdx.y / hsplit, hs = blockIdx.y - kh * hsplit;
+  // workgroups in block-major order (the nh = nkv x hsplit head shares of one block are adjacent), so
+  // a plan that lists its heaviest blocks first is dispatched heaviest-first
+  const int blk = blockIdx.x / nh, hid = blockIdx.x - blk * nh;
+  const int kh = hid / hsplit, hs = hid - kh * hsplit;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nw = __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6));
@@ -114,7 +116,9 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // Q^T operands: column r16 <-> query row 16qt + r16, slot (g, j) <-> dim 8g+j / 32+8g+j
   uint16_t *qw = qs + w * (4 * 2 * 64 * 8) + lane * 8;
   f32x4 o[UPW][4];   // O^T rows d = 16dt + 4g + i, column = query row 16qt + r16
-  float mrun[UPW], lrun[UPW];
+  float mrun[UPW];
+  f32x4 lacc[UPW];  // column sums of the weights (all four rows alike)
+  const u32x4 ones{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
     live[k] = active;
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     st16(qw + (2 * k) * 64 * 8, q0v);
     st16(qw + (2 * k + 1) * 64 * 8, q1v);
     mrun[k] = kNegInf;
-    lrun[k] = 0.f;
+    lacc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[k][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
@@ -161,8 +165,29 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // weights stay below 2^kPfLazy (well inside bf16's range; the sums are fp32). Same softmax, the
   // rounding happens at other points.
   const float thr = kPfLazy / sl2;  // in raw score units
-  // MASKED: a tile that crosses the causal diagonal or the range end. The two kinds run in separate
-  // loops (all full tiles first), so no scores move between registers for a shared continuation.
+  // S^T of query group k against the tile's K rows (8 MFMAs)
+  auto scores = [&](int k, const u32x4 (&ka)[2][2][2], f32x4 (&s)[2][2]) __attribute__((always_inline)) {
+    const u32x4 qb0 = ld16(qw + (2 * k) * 64 * 8), qb1 = ld16(qw + (2 * k + 1) * 64 * 8);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+        s[c][tt] = mfma16x16x32(ka[c][tt][1], qb1, mfma16x16x32(ka[c][tt][0], qb0, f32x4{0.f, 0.f, 0.f, 0.f}));
+  };
+  // O^T += V^T . P^T for query group k, and the weights' column sums by the same products with a ones
+  // operand (10 MFMAs, no VALU adds)
+  auto weigh = [&](int k, const u32x4 (&va)[4][2], const u32x4 (&pB)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) o[k][dt] = mfma16x16x32(va[dt][c], pB[c], o[k][dt]);
+    lacc[k] = mfma16x16x32(ones, pB[1], mfma16x16x32(ones, pB[0], lacc[k]));
+  };
+  // One tile. The four query groups are software-pipelined: while group k's softmax runs on the VALU,
+  // the matrix cores compute group k+1's scores and group k-1's products (the scheduler is asked to
+  // interleave them), so one wave keeps both units busy. MASKED: a tile that crosses the causal diagonal
+  // or the range end; the two kinds run in separate loops (all full tiles first), so no scores move
+  // between registers for a shared continuation.
   auto compute = [&](auto masked_tag, int t, const uint16_t *kt, const uint16_t *vtile) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     if (!active) return;
@@ -186,17 +211,17 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
         const u32x2 lo = lds_tr16(vp), hi2 = lds_tr16(vp + 4 * kRow);
         va[dt][c] = u32x4{lo[0], lo[1], hi2[0], hi2[1]};
       }
+    f32x4 s[2][2];
+    u32x4 pP[2];  // the previous group's weights
+    scores(0, ka, s);
 #pragma unroll
     for (int k = 0; k < UPW; ++k) {
-      // one query group at a time: no interleaving of the groups' score / weight registers
-      __builtin_amdgcn_sched_barrier(0);
-      const u32x4 qb0 = ld16(qw + (2 * k) * 64 * 8), qb1 = ld16(qw + (2 * k + 1) * 64 * 8);
-      f32x4 s[2][2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-          s[c][tt] = mfma16x16x32(ka[c][tt][1], qb1, mfma16x16x32(ka[c][tt][0], qb0, f32x4{0.f, 0.f, 0.f, 0.f}));
+      // group k+1's Q^T operands, early enough for its score products below
+      u32x4 qn0, qn1;
+      if (k + 1 < UPW) {
+        qn0 = ld16(qw + (2 * k + 2) * 64 * 8);
+        qn1 = ld16(qw + (2 * k + 3) * 64 * 8);
+      }
       if (MASKED) {
         const int lim = min(p0 + 16 * qt_of[k] + r16, hi - 1);  // keys <= query position (and < hi)
 #pragma unroll
@@ -207,45 +232,63 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
             for (int i = 0; i < 4; ++i)
               if (kt0 + 32 * c + 8 * g + 4 * tt + i > lim) s[c][tt][i] = kNegInf;
       }
-      float mt = max3_ieee(s[0][0][0], s[0][0][1], s[0][0][2]);
-      mt = max3_ieee(mt, s[0][0][3], s[0][1][0]);
-      mt = max3_ieee(mt, s[0][1][1], s[0][1][2]);
-      mt = max3_ieee(mt, s[0][1][3], s[1][0][0]);
-      mt = max3_ieee(mt, s[1][0][1], s[1][0][2]);
-      mt = max3_ieee(mt, s[1][0][3], s[1][1][0]);
-      mt = max3_ieee(mt, s[1][1][1], s[1][1][2]);
-      mt = max_over_groups_ieee(max_ieee(mt, s[1][1][3]));
+      // group k's column max on the VALU, one step beside each of group k-1's products (the
+      // scheduling barriers keep the interleave: a wave issues in order, so a run of MFMAs would stall
+      // it while the VALU idles)
+      const float *sf = reinterpret_cast<const float *>(&s[0][0]);
+      float mt = max3_ieee(sf[0], sf[1], sf[2]);
+#pragma unroll
+      for (int j = 0; j < 7; ++j) {
+        if (k > 0) {
+          const int dt = j >> 1, c = j & 1;
+          o[k - 1][dt] = mfma16x16x32(va[dt][c], pP[c], o[k - 1][dt]);
+        }
+        mt = j < 6 ? max3_ieee(mt, sf[3 + 2 * j], sf[4 + 2 * j]) : max_ieee(mt, sf[15]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (k > 0) {
+        o[k - 1][3] = mfma16x16x32(va[3][1], pP[1], o[k - 1][3]);
+        lacc[k - 1] = mfma16x16x32(ones, pP[1], mfma16x16x32(ones, pP[0], lacc[k - 1]));
+      }
+      mt = max_over_groups_ieee(mt);
       if (__ballot(mt > mrun[k] + thr)) {  // some column's max moved by more than kPfLazy: raise all
         const float mn = fmaxf(mrun[k], mt);
         const float alpha = (mrun[k] == kNegInf) ? 0.f : fast_exp2((mrun[k] - mn) * sl2);
-        lrun[k] *= alpha;
+        lacc[k] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[k][dt] *= alpha;
         mrun[k] = mn;
       }
       // mrun stays -inf only for a column with no key yet (a padding row): keep it inert.
       const float mc = mrun[k] == kNegInf ? 0.f : mrun[k] * sl2;
-      float ps = 0.f;
+      // group k's weights on the VALU, one score product of group k+1 beside each quarter tile
+      f32x4 sn[2][2];
       u32x4 pB[2];
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
+          if (k + 1 < UPW) sn[c][tt] = mfma16x16x32(ka[c][tt][0], qn0, f32x4{0.f, 0.f, 0.f, 0.f});
           float pv[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            pv[i] = fast_exp2(__builtin_fmaf(s[c][tt][i], sl2, -mc));
-            ps += pv[i];
-          }
+          pv[0] = fast_exp2(__builtin_fmaf(s[c][tt][0], sl2, -mc));
+          pv[1] = fast_exp2(__builtin_fmaf(s[c][tt][1], sl2, -mc));
           pB[c][2 * tt] = pack_bf16x2(pv[0], pv[1]);
+          __builtin_amdgcn_sched_barrier(0);
+          if (k + 1 < UPW) sn[c][tt] = mfma16x16x32(ka[c][tt][1], qn1, sn[c][tt]);
+          pv[2] = fast_exp2(__builtin_fmaf(s[c][tt][2], sl2, -mc));
+          pv[3] = fast_exp2(__builtin_fmaf(s[c][tt][3], sl2, -mc));
           pB[c][2 * tt + 1] = pack_bf16x2(pv[2], pv[3]);
+          __builtin_amdgcn_sched_barrier(0);
         }
-      lrun[k] += ps;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int c = 0; c < 2; ++c) {
+        pP[c] = pB[c];
+        if (k + 1 < UPW)
 #pragma unroll
-        for (int c = 0; c < 2; ++c) o[k][dt] = mfma16x16x32(va[dt][c], pB[c], o[k][dt]);
+          for (int tt = 0; tt < 2; ++tt) s[c][tt] = sn[c][tt];
+      }
     }
+    weigh(UPW - 1, va, pP);
   };
 
   // tiles [0, nfull) lie wholly below the causal diagonal (every query row sees every key) and inside the
@@ -295,7 +338,7 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
     if (!live[k]) continue;
-    const float l = sum_over_groups(lrun[k]);
+    const float l = lacc[k][0];
     const int mrow = 16 * qt_of[k] + r16;
     if (mrow >= nv) continue;
     uint16_t *op = out + (int64_t)(q0 + mrow) * s_or + (int64_t)head[k] * s_oh + 4 * g;
@@ -332,10 +375,12 @@ extern "C" int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
   const int nkv = nq / group;
   const int hpw = group < kPfMaxHW ? group : kPfMaxHW;  // q heads (waves) per workgroup
   const int hsplit = (group + hpw - 1) / hpw;
-  if ((int64_t)nkv * hsplit > 65535) return set_error(A8_EUNSUP, "prefill_attn: too many heads");
-  hipLaunchKernelGGL(k_prefill, dim3(nblk, nkv * hsplit), dim3(64 * hpw), 0, (hipStream_t)stream,
+  const int nh = nkv * hsplit;
+  if ((int64_t)nblk * nh * 64 * hpw > (int64_t)UINT32_MAX)  // the launch counts its threads in 32 bits
+    return set_error(A8_EUNSUP, "prefill_attn: too many blocks x heads (%d x %d)", nblk, nh);
+  hipLaunchKernelGGL(k_prefill, dim3(nblk * nh), dim3(64 * hpw), 0, (hipStream_t)stream,
                      (const uint16_t *)q, s_qr, s_qh, R, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, s_ks,
                      cache_rows, cache_len, (uint16_t *)out, s_or, s_oh, bq0, bn, bslot, bpos0, group, hsplit, hpw,
-                     scale * kLog2e);
+                     scale * kLog2e, nh);
   return (int)hipGetLastError();
 }

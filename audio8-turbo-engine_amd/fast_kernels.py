@@ -336,20 +336,24 @@ class DecodeAttention:
         return out
 
 
+def heaviest_first(blocks):
+    """(q0, n, slot, pos0) query blocks sorted by their key count pos0 + n, largest first; stable."""
+    return sorted(blocks, key=lambda b: -(b[3] + b[1]))
+
+
 class PrefillPlan:
     """Query-block schedule for a packed prefill: request i's rows [r0_i, r0_i+n_i) sit at
     positions [p0_i, p0_i+n_i) of cache row slot_i (keys [0, p0_i) are an already-stored prefix)
-    (fast_kernels.py:335-347)."""
+    (fast_kernels.py:335-347). The blocks are the reference's; they are listed heaviest first (most keys,
+    ties in request order) instead of in request order, so the kernel, which dispatches its workgroups
+    in list order, starts the long blocks first and the short ones fill the end. Every block writes its
+    own rows, so the order changes no result."""
     BM = 64
 
     def __init__(self, r0s, ns, slots, p0s, device):
-        q0, cnt, sl, ps = [], [], [], []
-        for r0, n, s, p0 in zip(r0s, ns, slots, p0s):
-            for off in range(0, n, self.BM):
-                q0.append(r0 + off)
-                cnt.append(min(self.BM, n - off))
-                sl.append(s)
-                ps.append(p0 + off)
+        blocks = heaviest_first([(r0 + off, min(self.BM, n - off), s, p0 + off)
+                                 for r0, n, s, p0 in zip(r0s, ns, slots, p0s) for off in range(0, n, self.BM)])
+        q0, cnt, sl, ps = (list(c) for c in zip(*blocks)) if blocks else ([], [], [], [])
         t = torch.tensor([q0, cnt, sl, ps], dtype=torch.int32)
         if torch.device(device).type == "cuda":
             t = t.pin_memory().to(device, non_blocking=True)

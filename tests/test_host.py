@@ -24,14 +24,26 @@ def test_helpers_match_oracle(a8, ref):
         assert a8.ref_nsplit(b, 2) == ref.ref_nsplit(b, 2)
 
 
+def _heaviest_first_of(got, want):
+    """got (q0, n, slot, pos0 columns) lists the blocks of want in order of key count pos0 + n, largest
+    first, ties in want's order."""
+    got, want = list(zip(*[list(map(int, c)) for c in got])), list(zip(*[list(map(int, c)) for c in want]))
+    assert sorted(got) == sorted(want)
+    assert got == sorted(want, key=lambda b: -(b[3] + b[1]))
+    keys = [b[3] + b[1] for b in got]
+    assert keys == sorted(keys, reverse=True)
+
+
 def test_prefill_plan_matches_oracle(a8, ref):
     r0s, ns, slots, p0s = [0, 70, 75], [70, 5, 200], [3, 1, 0], [300, 0, 64]
     p = a8.PrefillPlan(r0s, ns, slots, p0s, "cpu")
     want = ref.prefill_plan(r0s, ns, slots, p0s)
     assert p.nblk == len(want[0]) == 2 + 1 + 4
-    for t, w in zip((p.q0, p.n, p.slot, p.pos0), want):
-        assert t.dtype == torch.int32 and t.tolist() == list(w)
+    assert all(t.dtype == torch.int32 for t in (p.q0, p.n, p.slot, p.pos0))
+    _heaviest_first_of((p.q0.tolist(), p.n.tolist(), p.slot.tolist(), p.pos0.tolist()), want)
+    assert p.pos0.tolist()[:2] == [300 + 64, 300]  # request 0's blocks (keys 370 and 364) lead
     assert a8.PrefillPlan.BM == 64
+    assert a8.PrefillPlan([], [], [], [], "cpu").nblk == 0
 
 
 def test_prefill_meta_matches_oracle(a8, ref):
@@ -39,11 +51,20 @@ def test_prefill_meta_matches_oracle(a8, ref):
     for slots, ns, starts, nt in (([], [], [], 2048), ([5, 9], [300, 64], [300, 300], 512),
                                   (list(range(64)), [1] * 64, list(range(64)), 64)):
         h = meta.host(nt, slots, ns, starts)
-        np.testing.assert_array_equal(h, ref.pf_meta_host(nt, slots, ns, starts, 2048, 64, 192))
+        w = ref.pf_meta_host(nt, slots, ns, starts, 2048, 64, 192)
+        o = meta.off
+        blk = slice(o[2], o[6])  # q0, n, bslot, pos0: the same blocks, heaviest first
+        np.testing.assert_array_equal(np.delete(h, np.r_[blk]), np.delete(w, np.r_[blk]))
+        nb = int((w[o[3]:o[4]] > 0).sum())
+        cols = [lambda m, i=i: m[o[i]:o[i] + nb] for i in (2, 3, 4, 5)]
+        _heaviest_first_of([c(h) for c in cols], [c(w) for c in cols])
+        for i in (2, 3, 4, 5):
+            np.testing.assert_array_equal(h[o[i] + nb:o[i + 1]], w[o[i] + nb:o[i + 1]])  # padding blocks
     meta.load(512, [5, 9], [300, 64], [300, 300])
     plan = meta.plan(512)
     assert plan.nblk == 512 // 64 + 64 and plan.BM == 64
-    assert plan.n[:6].tolist() == [64, 64, 64, 64, 44, 64] and (plan.n[6:] == 0).all()
+    assert plan.n[:6].tolist() == [44, 64, 64, 64, 64, 64] and (plan.n[6:] == 0).all()
+    assert plan.pos0[:6].tolist() == [556, 492, 428, 364, 300, 300]
     assert (plan.slot[6:] == 192).all()
 
 
