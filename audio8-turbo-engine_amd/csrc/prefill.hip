@@ -52,6 +52,8 @@ __device__ __forceinline__ void pf_dma(int i, uint32_t t0, rsrc_t kr, rsrc_t vr,
 
 // UPW = 16-row query groups per wave (the block's 64 rows).
 constexpr int UPW = 4;
+// NW = waves (q heads) per workgroup, 1..kPfMaxHW.
+template <int NW>
 __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     const uint16_t *__restrict__ q, int64_t s_qr, int64_t s_qh, int R,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
@@ -76,7 +78,7 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   const int kh = hid / hsplit, hs = hid - kh * hsplit;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nw = __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6));
+  constexpr int nw = NW;
   const int r16 = lane & 15, g = lane >> 4;
 
   // Block metadata is uniform over the workgroup, so early exits happen before any barrier.
@@ -119,20 +121,24 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   float mrun[UPW];
   f32x4 lacc[UPW];  // column sums of the weights (all four rows alike)
   const u32x4 ones{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
+  // The Q^T operands go from HBM straight into LDS by DMA (requested before the first K / V tiles, so the
+  // first wait covers both): lane l of request (k, half) reads dims 8g.. (+32) of query row 16k + r16, and
+  // rows past nv read as zeros (the descriptor ends at row nv - 1; the host keeps s_qr >= hd).
+  if (active) {
+    const rsrc_t qrs = make_rsrc(q + (int64_t)q0 * s_qr + (int64_t)(kh * group + gi) * s_qh,
+                                 (uint32_t)((int64_t)(nv - 1) * s_qr * 2 + 128));
+#pragma unroll
+    for (int k = 0; k < UPW; ++k)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        bld16_lds<0>(qrs, reinterpret_cast<char *>(qs) + (w * 8 + 2 * k + h) * 1024,
+                     (uint32_t)(((int64_t)(16 * k + r16) * s_qr + 8 * g + 32 * h) * 2), 0u);
+  }
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
     live[k] = active;
     head[k] = kh * group + gi;
     qt_of[k] = k;
-    const int mrow = 16 * qt_of[k] + r16;
-    u32x4 q0v{0u, 0u, 0u, 0u}, q1v{0u, 0u, 0u, 0u};
-    if (live[k] && mrow < nv) {
-      const uint16_t *qp = q + (int64_t)(q0 + mrow) * s_qr + (int64_t)head[k] * s_qh + 8 * g;
-      q0v = ld16(qp);
-      q1v = ld16(qp + 32);
-    }
-    st16(qw + (2 * k) * 64 * 8, q0v);
-    st16(qw + (2 * k + 1) * 64 * 8, q1v);
     mrun[k] = kNegInf;
     lacc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -149,12 +155,10 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // reads of the buffer the next request will refill.
   auto ready = [&](bool ahead) __attribute__((always_inline)) {
     if (ahead) {
-      switch (nw) {  // s_waitcnt vmcnt(16 / nw)
-        case 1: __builtin_amdgcn_s_waitcnt(0x4F70); break;
-        case 2: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-        case 3: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-        default: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-      }
+      if (nw == 1) __builtin_amdgcn_s_waitcnt(0x4F70);  // s_waitcnt vmcnt(16 / nw)
+      if (nw == 2) __builtin_amdgcn_s_waitcnt(0x0F78);
+      if (nw == 3) __builtin_amdgcn_s_waitcnt(0x0F75);
+      if (nw == 4) __builtin_amdgcn_s_waitcnt(0x0F74);
     } else {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     }
@@ -188,9 +192,19 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // interleave them), so one wave keeps both units busy. MASKED: a tile that crosses the causal diagonal
   // or the range end; the two kinds run in separate loops (all full tiles first), so no scores move
   // between registers for a shared continuation.
-  auto compute = [&](auto masked_tag, int t, const uint16_t *kt, const uint16_t *vtile) __attribute__((always_inline)) {
+  // ISSUE: tile tn's requests (into kn / vn) go out from inside the computation, this wave's share a
+  // quarter at a time at the start of each query group, so the load queue of the compute unit drains
+  // between them instead of holding every wave at once behind a burst right after the barrier. A tile past
+  // the range (tn >= ntile) reads as zeros into a buffer no later tile uses: requested anyway, so no
+  // branch splits the scheduled code.
+  auto compute = [&](auto masked_tag, int t, const uint16_t *kt, const uint16_t *vtile, auto issue_tag, int tn,
+                     uint16_t *kn, uint16_t *vn) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
-    if (!active) return;
+    constexpr bool ISSUE = decltype(issue_tag)::value;
+    if (!active) {
+      if (ISSUE) issue(tn, kn, vn);
+      return;
+    }
     const int kt0 = 64 * t;
     // operands of the tile, read once: K rows (A of S^T; tile (c, tt) row 4g+i <-> key
     // kt0 + 32c + 8g + 4tt + i) and V^T (A of O^T)
@@ -216,6 +230,10 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     scores(0, ka, s);
 #pragma unroll
     for (int k = 0; k < UPW; ++k) {
+      if (ISSUE)  // this wave's instructions i = w + nw * j with j = k mod 4 (no branch unless nw is 3)
+#pragma unroll
+        for (int j = k; j * nw < 16; j += 4)
+          if (nw != 3 || w + nw * j < 16) pf_dma(w + nw * j, (uint32_t)(64 * tn), kr, vr, kn, vn, kd0, kd1, vd0, vd1);
       // group k+1's Q^T operands, early enough for its score products below
       u32x4 qn0, qn1;
       if (k + 1 < UPW) {
@@ -235,15 +253,27 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
       // group k's column max on the VALU, one step beside each of group k-1's products (the
       // scheduling barriers keep the interleave: a wave issues in order, so a run of MFMAs would stall
       // it while the VALU idles)
+      // (as a tree of depth three: five independent triples, then two, then one)
       const float *sf = reinterpret_cast<const float *>(&s[0][0]);
-      float mt = max3_ieee(sf[0], sf[1], sf[2]);
+      float mA[5], mB0 = 0.f, mB1 = 0.f, mt = 0.f;
 #pragma unroll
       for (int j = 0; j < 7; ++j) {
         if (k > 0) {
           const int dt = j >> 1, c = j & 1;
           o[k - 1][dt] = mfma16x16x32(va[dt][c], pP[c], o[k - 1][dt]);
         }
-        mt = j < 6 ? max3_ieee(mt, sf[3 + 2 * j], sf[4 + 2 * j]) : max_ieee(mt, sf[15]);
+        if (j < 2) {
+          mA[2 * j] = max3_ieee(sf[6 * j], sf[6 * j + 1], sf[6 * j + 2]);
+          mA[2 * j + 1] = max3_ieee(sf[6 * j + 3], sf[6 * j + 4], sf[6 * j + 5]);
+        } else if (j == 2) {
+          mA[4] = max3_ieee(sf[12], sf[13], sf[14]);
+        } else if (j == 3) {
+          mB0 = max3_ieee(mA[0], mA[1], mA[2]);
+        } else if (j == 4) {
+          mB1 = max3_ieee(mA[3], mA[4], sf[15]);
+        } else if (j == 5) {
+          mt = max_ieee(mB0, mB1);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       if (k > 0) {
@@ -301,22 +331,19 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   if (nfull > 0) {
     for (;; t += 3) {
       ready(t + 1 < ntile);
-      if (t + 2 < ntile) issue(t + 2, kC, vC);
-      compute(std::false_type{}, t, kA, vA);
+      compute(std::false_type{}, t, kA, vA, std::true_type{}, t + 2, kC, vC);
       if (t + 1 >= nfull) {
         t += 1;
         break;
       }
       ready(t + 2 < ntile);
-      if (t + 3 < ntile) issue(t + 3, kA, vA);
-      compute(std::false_type{}, t + 1, kB, vB);
+      compute(std::false_type{}, t + 1, kB, vB, std::true_type{}, t + 3, kA, vA);
       if (t + 2 >= nfull) {
         t += 2;
         break;
       }
       ready(t + 3 < ntile);
-      if (t + 4 < ntile) issue(t + 4, kB, vB);
-      compute(std::false_type{}, t + 2, kC, vC);
+      compute(std::false_type{}, t + 2, kC, vC, std::true_type{}, t + 4, kB, vB);
       if (t + 3 >= nfull) {
         t += 3;
         break;
@@ -330,7 +357,7 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     const int bsel = t % 3;
     const uint16_t *kt = bsel == 0 ? kA : bsel == 1 ? kB : kC;
     const uint16_t *vtb = bsel == 0 ? vA : bsel == 1 ? vB : vC;
-    compute(std::true_type{}, t, kt, vtb);
+    compute(std::true_type{}, t, kt, vtb, std::false_type{}, 0, kA, vA);
   }
   // the last request may still write (zeros, past the range) into LDS: let it land before the end
   __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -338,14 +365,16 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
     if (!live[k]) continue;
-    const float l = lacc[k][0];
     const int mrow = 16 * qt_of[k] + r16;
     if (mrow >= nv) continue;
+    // a live row has l >= 1 (its largest weight is 2^0 .. 2^kPfLazy): one hardware reciprocal (1 ulp)
+    // instead of sixteen IEEE divisions
+    const float rl = __builtin_amdgcn_rcpf(lacc[k][0]);
     uint16_t *op = out + (int64_t)(q0 + mrow) * s_or + (int64_t)head[k] * s_oh + 4 * g;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
-      st8(op + 16 * dt, u32x2{pack_bf16x2(o[k][dt][0] / l, o[k][dt][1] / l),
-                              pack_bf16x2(o[k][dt][2] / l, o[k][dt][3] / l)});
+      st8(op + 16 * dt, u32x2{pack_bf16x2(o[k][dt][0] * rl, o[k][dt][1] * rl),
+                              pack_bf16x2(o[k][dt][2] * rl, o[k][dt][3] * rl)});
   }
 }
 
@@ -376,9 +405,13 @@ extern "C" int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
   const int hpw = group < kPfMaxHW ? group : kPfMaxHW;  // q heads (waves) per workgroup
   const int hsplit = (group + hpw - 1) / hpw;
   const int nh = nkv * hsplit;
+  if (s_qr < hd || s_qr >= (1 << 25))  // the Q requests' 32-bit byte offsets (63 rows) and their row range
+    return set_error(A8_EUNSUP, "prefill_attn: q row stride %lld outside [%d, 2^25)", (long long)s_qr, hd);
   if ((int64_t)nblk * nh * 64 * hpw > (int64_t)UINT32_MAX)  // the launch counts its threads in 32 bits
     return set_error(A8_EUNSUP, "prefill_attn: too many blocks x heads (%d x %d)", nblk, nh);
-  hipLaunchKernelGGL(k_prefill, dim3(nblk * nh), dim3(64 * hpw), 0, (hipStream_t)stream,
+  static_assert(kPfMaxHW == 4, "one instantiation per workgroup size");
+  auto kern = hpw == 1 ? k_prefill<1> : hpw == 2 ? k_prefill<2> : hpw == 3 ? k_prefill<3> : k_prefill<4>;
+  hipLaunchKernelGGL(kern, dim3(nblk * nh), dim3(64 * hpw), 0, (hipStream_t)stream,
                      (const uint16_t *)q, s_qr, s_qh, R, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, s_ks,
                      cache_rows, cache_len, (uint16_t *)out, s_or, s_oh, bq0, bn, bslot, bpos0, group, hsplit, hpw,
                      scale * kLog2e, nh);
