@@ -118,7 +118,9 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // Q^T operands: column r16 <-> query row 16qt + r16, slot (g, j) <-> dim 8g+j / 32+8g+j
   uint16_t *qw = qs + w * (4 * 2 * 64 * 8) + lane * 8;
   f32x4 o[UPW][4];   // O^T rows d = 16dt + 4g + i, column = query row 16qt + r16
-  float mrun[UPW];
+  // per query group: the running max (raw score units), the level above which a score raises it
+  // (mrun + the lazy margin) and the exp2 offset mrun * sl2 (0 while mrun is -inf)
+  float mrun[UPW], mlim[UPW], mcs[UPW];
   f32x4 lacc[UPW];  // column sums of the weights (all four rows alike)
   const u32x4 ones{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
   // The Q^T operands go from HBM straight into LDS by DMA (requested before the first K / V tiles, so the
@@ -140,6 +142,8 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     head[k] = kh * group + gi;
     qt_of[k] = k;
     mrun[k] = kNegInf;
+    mlim[k] = kNegInf;
+    mcs[k] = 0.f;
     lacc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[k][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -280,17 +284,20 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
         o[k - 1][3] = mfma16x16x32(va[3][1], pP[1], o[k - 1][3]);
         lacc[k - 1] = mfma16x16x32(ones, pP[1], mfma16x16x32(ones, pP[0], lacc[k - 1]));
       }
-      mt = max_over_groups_ieee(mt);
-      if (__ballot(mt > mrun[k] + thr)) {  // some column's max moved by more than kPfLazy: raise all
-        const float mn = fmaxf(mrun[k], mt);
-        const float alpha = (mrun[k] == kNegInf) ? 0.f : fast_exp2((mrun[k] - mn) * sl2);
+      // mt is this lane group's max (16 of the column's 64 scores): a raise is needed iff some lane group
+      // of some column exceeds its column's limit, and only then is the column max formed
+      if (__ballot(mt > mlim[k])) {  // some column's max moved by more than kPfLazy: raise all
+        const float mn = fmaxf(mrun[k], max_over_groups_ieee(mt));
+        const float alpha = (mrun[k] == kNegInf) ? 0.f : fast_exp2(mcs[k] - mn * sl2);
         lacc[k] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[k][dt] *= alpha;
         mrun[k] = mn;
+        mlim[k] = mn + thr;
+        // mrun stays -inf only for a column with no key yet (a padding row): keep it inert.
+        mcs[k] = mn == kNegInf ? 0.f : mn * sl2;
       }
-      // mrun stays -inf only for a column with no key yet (a padding row): keep it inert.
-      const float mc = mrun[k] == kNegInf ? 0.f : mrun[k] * sl2;
+      const float mc = mcs[k];
       // group k's weights on the VALU, one score product of group k+1 beside each quarter tile
       f32x4 sn[2][2];
       u32x4 pB[2];
