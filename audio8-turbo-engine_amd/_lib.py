@@ -28,7 +28,7 @@ SIGNATURES = {
     "a8_bias_rope_store": (_I, [_P, _L, _P, _P, _P, _L, _I, _P, _P, _I, _P, _L, _L,
                                 _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _P]),
     "a8_decode_attn": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _I, _P, _P, _P, _L, _L,
-                            _P, _P, _L, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
+                            _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
     "a8_decode_choose": (_I, [_I, _I, _I, _I, _I, _L, _I, _IP, _IP]),
     "a8_decode_attn_stream": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _I, _P, _P, _P, _L, _L,
                                    _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
@@ -38,7 +38,7 @@ SIGNATURES = {
                                     _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
     "a8_store_decode_split": (_I, [_P, _L, _P, _P, _P, _L, _I, _P, _P, _P, _L, _L,
                                    _P, _P, _L, _L, _L, _I, _I, _P, _P, _P, _L, _L,
-                                   _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
+                                   _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
     "a8_decode_attn_flat": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _I, _P, _P, _P, _L, _L,
                                  _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _F, _P]),
     "a8_decode_choose_flat": (_I, [_I, _I, _I, _L, _I, _IP]),

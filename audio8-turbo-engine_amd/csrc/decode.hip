@@ -40,7 +40,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     uint16_t *kc, uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,  // written when FUSED
     int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
     uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, float *__restrict__ acc_ws,
-    float *__restrict__ ml_ws, int nq, int nkv, int group, int ns, float scale_log2, StoreIn si) {
+    float *__restrict__ ml_ws, int32_t *__restrict__ counters, int nq, int nkv, int group, int ns, float scale_log2,
+    StoreIn si) {
   warm_kernargs<256>();  // the explicit arguments above span 0x000-0x0ff and more
   // V tiles of the two pipeline buffers (one per wave each); separate arrays, so the compiler tells
   // their DMA completions apart and waits only for the buffer it reads.
@@ -115,15 +116,19 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
 
   // Lane (r16, g) holds O^T[d = 16dt + 4g + i][head r16].
   if (NW == 1) {
-    if (r16 >= group) return;
+    const bool mine = r16 < group;
     const int hq = kh * group + r16;
     if (ns == 1) {
+      if (!mine) return;
       uint16_t *op = out + (int64_t)row * s_ob + (int64_t)hq * s_oh + 4 * g;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
         st8(op + 16 * dt, u32x2{pack_bf16x2(o[dt][0] / lsum, o[dt][1] / lsum),
                                 pack_bf16x2(o[dt][2] / lsum, o[dt][3] / lsum)});
-    } else {
+      return;
+    }
+    if (!counters) {  // the combine kernel merges
+      if (!mine) return;
       const int64_t pi = ((int64_t)row * nq + hq) * ns + sp;
       float *ap = acc_ws + pi * 64 + 4 * g;
 #pragma unroll
@@ -132,6 +137,33 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
         ml_ws[pi * 2] = m;
         ml_ws[pi * 2 + 1] = lsum;
       }
+      return;
+    }
+    // In-kernel merge: the (row, kv head)'s partials [group heads][ns splits] as agent-coherent buffers.
+    const int64_t p0i = ((int64_t)row * nq + (int64_t)kh * group) * ns;
+    const rsrc_t acc_r = make_rsrc(acc_ws + p0i * 64, (uint32_t)(group * ns * 64 * 4));
+    const rsrc_t ml_r = make_rsrc(ml_ws + p0i * 2, (uint32_t)(group * ns * 2 * 4));
+    if (mine) {
+      const uint32_t ao = (uint32_t)(((r16 * ns + sp) * 64 + 4 * g) * 4);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[dt]), acc_r, ao + 64u * dt, 0, kSC1);
+      if (g == 0) {
+        const uint32_t mo = (uint32_t)((r16 * ns + sp) * 2 * 4);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m), ml_r, mo, 0, kSC1);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lsum), ml_r, mo + 4u, 0, kSC1);
+      }
+    }
+    if (!last_arrival(counters + (int64_t)row * nkv + kh, ns)) return;
+    if (mine) {
+      f32x4 num[4];
+      float den;
+      merge_partials(acc_r, ml_r, r16, g, ns, scale_log2, num, den);
+      uint16_t *op = out + (int64_t)row * s_ob + (int64_t)hq * s_oh + 4 * g;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        st8(op + 16 * dt, u32x2{pack_bf16x2(num[dt][0] / den, num[dt][1] / den),
+                                pack_bf16x2(num[dt][2] / den, num[dt][3] / den)});
     }
     return;
   }
@@ -149,6 +181,10 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) *reinterpret_cast<f32x4 *>(ob + (w * 16 + r16) * kOb + 16 * dt + 4 * g) = o[dt];
   __syncthreads();
+  const bool merge_here = ns > 1 && counters;
+  const int64_t p0i = ((int64_t)row * nq + (int64_t)kh * group) * ns;
+  const rsrc_t acc_r = make_rsrc(acc_ws + (merge_here ? p0i * 64 : 0), (uint32_t)(group * ns * 64 * 4));
+  const rsrc_t ml_r = make_rsrc(ml_ws + (merge_here ? p0i * 2 : 0), (uint32_t)(group * ns * 2 * 4));
   for (int idx = threadIdx.x; idx < group * 64; idx += 64 * NW) {
     const int head = idx >> 6, d = idx & 63;
     float M = kNegInf;
@@ -165,14 +201,39 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     const int hq = kh * group + head;
     if (ns == 1) {
       out[(int64_t)row * s_ob + (int64_t)hq * s_oh + d] = (uint16_t)(pack_bf16x2(num / den, 0.f) & 0xffffu);
-    } else {
+    } else if (!merge_here) {
       const int64_t pi = ((int64_t)row * nq + hq) * ns + sp;
       acc_ws[pi * 64 + d] = num;
       if (d == 0) {
         ml_ws[pi * 2] = M;
         ml_ws[pi * 2 + 1] = den;
       }
+    } else {
+      const uint32_t e = (uint32_t)(head * ns + sp);
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(num), acc_r, (e * 64 + d) * 4, 0, kSC1);
+      if (d == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M), ml_r, e * 8, 0, kSC1);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(den), ml_r, e * 8 + 4u, 0, kSC1);
+      }
     }
+  }
+  if (!merge_here) return;
+  // every thread's partial stores complete, then one arrival for the workgroup
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  __shared__ int last_flag;
+  if (threadIdx.x < 64) {
+    const bool last = last_arrival(counters + (int64_t)row * nkv + kh, ns);
+    if (threadIdx.x == 0) last_flag = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  for (int idx = threadIdx.x; idx < group * 64; idx += 64 * NW) {
+    const int head = idx >> 6, d = idx & 63;
+    const float v = merge_partial_elem(acc_r, ml_r, head, d, ns, scale_log2);
+    out[(int64_t)row * s_ob + (int64_t)(kh * group + head) * s_oh + d] = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu);
   }
 }
 
@@ -224,12 +285,12 @@ template <int NW, bool FUSED>
 static void launch_split(int ns, int nkv, int b, hipStream_t st, const uint16_t *q, int64_t s_qb, int64_t s_qh,
                          uint16_t *kc, uint16_t *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks, int cache_rows,
                          int cache_len, const int32_t *lens, const int32_t *rowmap, uint16_t *out, int64_t s_ob,
-                         int64_t s_oh, float *acc_ws, float *ml_ws, int nq, int group, float scale_log2,
-                         const StoreIn &si) {
+                         int64_t s_oh, float *acc_ws, float *ml_ws, int32_t *counters, int nq, int group,
+                         float scale_log2, const StoreIn &si) {
   auto kern = k_decode_split<NW, FUSED>;
   hipLaunchKernelGGL(kern, dim3(ns, nkv, b), dim3(64 * NW), 0, st, q, s_qb, s_qh, kc, vc, s_kb, s_kh, s_ks,
-                     cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, nq, nkv, group, ns,
-                     scale_log2, si);
+                     cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, counters, nq, nkv, group,
+                     ns, scale_log2, si);
 }
 
 // Body of a8_decode_attn and a8_store_decode_split (fused = si.qkv != nullptr: q is unused, the store's
@@ -237,8 +298,8 @@ static void launch_split(int ns, int nkv, int b, hipStream_t st, const uint16_t 
 static int split_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh, void *kc, void *vc, int64_t s_kb,
                        int64_t s_kh, int64_t s_ks, int cache_rows, int cache_len, const int32_t *lens,
                        const int32_t *rowmap, void *out, int64_t s_ob, int64_t s_oh, float *acc_ws, float *ml_ws,
-                       int64_t ws_row_splits, int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
-                       int phases, const StoreIn &si, void *stream) {
+                       int64_t ws_row_splits, int32_t *counters, int64_t n_counters, int b, int nq, int nkv, int hd,
+                       int nsplit, int waves, float scale, int phases, const StoreIn &si, void *stream) {
   const bool fused = si.qkv != nullptr;
   if (hd != 64) return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64 only)", fn, hd);
   if (b < 0 || nq <= 0 || nkv <= 0 || nq % nkv || cache_rows < 0 || cache_len < 0 || nsplit < 1 || b > 65535)
@@ -255,6 +316,13 @@ static int split_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh
                      (long long)ws_row_splits, (long long)b * nsplit);
   if (s_ks != hd)
     return set_error(A8_EUNSUP, "%s: cache positions must be contiguous rows (s_ks %lld)", fn, (long long)s_ks);
+  if (counters && (int64_t)b * nkv > n_counters)
+    return set_error(A8_EWSPACE, "%s: %lld counters, need b*nkv = %lld", fn, (long long)n_counters,
+                     (long long)b * nkv);
+  if (counters && nsplit > 1 && (int64_t)group * nsplit * 64 * 4 > (int64_t)UINT32_MAX)
+    return set_error(A8_EUNSUP, "%s: %d splits too many for the in-kernel merge", fn, nsplit);
+  if (counters && nsplit > 1 && (phases & 1) == 0)
+    return set_error(A8_EINVAL, "%s: with counters the merge is part of the split kernel (phases bit 0)", fn);
   if ((!fused && !al16(q)) || !al16(kc) || !al16(vc) || !al16(out) || (nsplit > 1 && !al16(acc_ws)) ||
       ((fused ? 0 : (s_qb | s_qh)) | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
     return set_error(A8_EALIGN, "%s: pointers must be 16-byte aligned and strides multiples of 8", fn);
@@ -266,7 +334,7 @@ static int split_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh
   auto *oo = (uint16_t *)out;
   if (phases & 1) {
 #define A8_SPLIT_ARGS nsplit, nkv, b, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens, \
-                      rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, nq, group, sl2, si
+                      rowmap, oo, s_ob, s_oh, acc_ws, ml_ws, counters, nq, group, sl2, si
     switch (waves * 2 + (fused ? 1 : 0)) {
       case 2: launch_split<1, false>(A8_SPLIT_ARGS); break;
       case 3: launch_split<1, true>(A8_SPLIT_ARGS); break;
@@ -281,7 +349,7 @@ static int split_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
-  if ((phases & 2) && nsplit > 1) {
+  if ((phases & 2) && nsplit > 1 && !counters) {
     const unsigned grid = (unsigned)(((int64_t)b * nq + 3) / 4);
     hipLaunchKernelGGL(k_decode_combine, dim3(grid), dim3(256), 0, st, acc_ws, ml_ws, oo, s_ob, s_oh, b, nq,
                        nsplit, sl2);
@@ -298,13 +366,14 @@ extern "C" int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
                               const int32_t *lens, const int32_t *rowmap,
                               void *out, int64_t s_ob, int64_t s_oh,
                               float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                              int32_t *counters, int64_t n_counters,
                               int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
                               int phases, void *stream) {
   using namespace a8;
   const StoreIn none{};
   return split_entry("decode_attn", q, s_qb, s_qh, const_cast<void *>(kc), const_cast<void *>(vc), s_kb, s_kh, s_ks,
-                     cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, b, nq, nkv,
-                     hd, nsplit, waves, scale, phases, none, stream);
+                     cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, counters,
+                     n_counters, b, nq, nkv, hd, nsplit, waves, scale, phases, none, stream);
 }
 
 extern "C" int a8_store_decode_split(const void *qkv, int64_t s_qkv, const void *bias,
@@ -315,6 +384,7 @@ extern "C" int a8_store_decode_split(const void *qkv, int64_t s_qkv, const void 
                                      int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap,
                                      void *out, int64_t s_ob, int64_t s_oh,
                                      float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                                     int32_t *counters, int64_t n_counters,
                                      int b, int nq, int nkv, int hd, int ring, int nsplit, int waves, float scale,
                                      int phases, void *stream) {
   using namespace a8;
@@ -341,8 +411,8 @@ extern "C" int a8_store_decode_split(const void *qkv, int64_t s_qkv, const void 
   si.s_qo_h = s_qo_h;
   si.ring = ring;
   return split_entry("store_decode_split", nullptr, 0, 0, kc, vc, s_kb, s_kh, s_ks, cache_rows, cache_len, lens,
-                     rowmap, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, b, nq, nkv, hd, nsplit, waves, scale,
-                     phases, si, stream);
+                     rowmap, out, s_ob, s_oh, acc_ws, ml_ws, ws_row_splits, counters, n_counters, b, nq, nkv, hd,
+                     nsplit, waves, scale, phases, si, stream);
 }
 
 // Launch-shape policy (measured on MI355X at 192 slots x 2048 keys: one split of 4 waves per

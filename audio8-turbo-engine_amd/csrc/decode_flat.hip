@@ -29,7 +29,6 @@
 namespace a8 {
 
 constexpr int kFlatNW = 4;          // waves per workgroup
-constexpr int kSC1 = 16;            // buffer cache policy: sc1, coherent across the device (agent scope)
 constexpr int kFlatMaxRows = 2048;  // rows per call: the per-row metadata lives in LDS
 constexpr int kFlatMaxGrid = 1024;  // with fewer than 2^20 tiles, the partition arithmetic fits 32 bits
 constexpr int kFlatMaxTiles = 1 << 20;

@@ -267,4 +267,97 @@ __device__ __forceinline__ void compute_step(KTile (&T)[NT], uint16_t *vbuf, int
   }
 }
 
+// ---- Partials exchanged between the workgroups of one launch (the in-kernel merges) ----
+// A partial goes out with agent-coherent (sc1) buffer stores, which write through the XCD's L2; once they
+// have completed (vmcnt(0)) an atomic on the unit's counter makes the arrival known, and the last arrival
+// reads every partial with sc1 loads issued after its atomic returned. Only the bytes exchanged are kept
+// coherent: an agent-scope fence would write back and invalidate the whole L2 for every partial.
+constexpr int kSC1 = 16;  // buffer cache policy: sc1, coherent across the device (agent scope)
+
+// Called by a whole wave after its partial's stores: true in the wave that brings the count to `arrivals`,
+// which also puts the counter back to 0 for the next launch (every arrival of this one is in).
+__device__ __forceinline__ bool last_arrival(int32_t *ctr, int arrivals) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial has reached the coherent level
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  int old = 0;
+  if (__lane_id() == 0) old = atomicAdd(ctr, 1);
+  old = __shfl(old, 0);
+  const bool last = old == arrivals - 1;
+  if (last && __lane_id() == 0) *ctr = 0;
+  return last;
+}
+
+// Merge of one (row, kv head)'s partials laid out [head][split] (acc 64 floats, ml 2 floats each), in
+// split order with a running maximum -- the arithmetic of k_decode_combine (fast_kernels.py:238-253),
+// eight splits' loads in flight at a time. merge_partials: lane (r16, g) gets dims 16dt + 4g + i of head
+// r16; merge_partial_elem: one (head, dim) element, out = num / den.
+__device__ __forceinline__ void merge_partials(rsrc_t acc_r, rsrc_t ml_r, int head, int g, int ns, float sl2,
+                                               f32x4 (&num)[4], float &den) {
+  constexpr int SB = 8;
+  float M = kNegInf;
+  den = 0.f;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) num[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < ns; s0 += SB) {
+    float mv[SB], lv[SB];
+    f32x4 av[SB][4];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      const uint32_t e = (uint32_t)(head * ns + min(s0 + i, ns - 1));
+      mv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ml_r, e * 8, 0, kSC1));
+      lv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ml_r, e * 8 + 4u, 0, kSC1));
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        av[i][dt] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(acc_r, (e * 64 + 16 * dt + 4 * g) * 4, 0, kSC1));
+    }
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      if (s0 + i >= ns) break;
+      if (mv[i] == kNegInf) continue;  // an empty split adds nothing
+      if (mv[i] > M) {
+        const float sc = (M == kNegInf) ? 0.f : fast_exp2((M - mv[i]) * sl2);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) num[dt] *= sc;
+        den *= sc;
+        M = mv[i];
+      }
+      const float wt = fast_exp2((mv[i] - M) * sl2);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) num[dt] += wt * av[i][dt];
+      den += wt * lv[i];
+    }
+  }
+}
+__device__ __forceinline__ float merge_partial_elem(rsrc_t acc_r, rsrc_t ml_r, int head, int d, int ns, float sl2) {
+  constexpr int SB = 8;
+  float M = kNegInf, num = 0.f, den = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += SB) {
+    float mv[SB], lv[SB], av[SB];
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      const uint32_t e = (uint32_t)(head * ns + min(s0 + i, ns - 1));
+      mv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ml_r, e * 8, 0, kSC1));
+      lv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ml_r, e * 8 + 4u, 0, kSC1));
+      av[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(acc_r, (e * 64 + d) * 4, 0, kSC1));
+    }
+#pragma unroll
+    for (int i = 0; i < SB; ++i) {
+      if (s0 + i >= ns) break;
+      if (mv[i] == kNegInf) continue;
+      if (mv[i] > M) {
+        const float sc = (M == kNegInf) ? 0.f : fast_exp2((M - mv[i]) * sl2);
+        num *= sc;
+        den *= sc;
+        M = mv[i];
+      }
+      const float wt = fast_exp2((mv[i] - M) * sl2);
+      num += wt * av[i];
+      den += wt * lv[i];
+    }
+  }
+  return num / den;
+}
+
 }  // namespace a8

@@ -24,18 +24,17 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     int cache_rows, int cache_len, int nq, int nkv, int ring) {
   warm_kernargs<164>();  // the explicit arguments above span 0x00-0xa3
   const int H = nq + 2 * nkv;
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= (int64_t)R * H * 4) return;
-  const int r = (int)(t / (H * 4));
-  const int rem = (int)(t - (int64_t)r * H * 4);
+  const uint32_t per = 4u * (uint32_t)H;  // threads per row (the host keeps R * per below 2^31)
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= (uint32_t)R * per) return;
+  const int r = (int)(t / per);
+  const int rem = (int)(t - (uint32_t)r * per);
   const int h = rem >> 2, c = rem & 3;
 
+  // Every load that does not depend on the position goes out before anything waits for it; the position
+  // check only decides the stores (so the loads are not held behind it).
   const int p = pos[r];
-  if (p < 0 || p >= n_tab) return;  // position outside the RoPE tables: the row writes nothing
   const int64_t sl = slot[r];
-  const int sidx = p % ring;
-  const bool store_ok = sl >= 0 && sl < cache_rows && sidx < cache_len;
-
   const uint16_t *src = qkv + (int64_t)r * s_qkv + h * 64;
   const u32x4 wlo = ld16(src + 8 * c), whi = ld16(src + 32 + 8 * c);
   u32x4 blo{0u, 0u, 0u, 0u}, bhi{0u, 0u, 0u, 0u};
@@ -43,6 +42,9 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     blo = ld16(bias + h * 64 + 8 * c);
     bhi = ld16(bias + h * 64 + 32 + 8 * c);
   }
+  const bool in_tab = p >= 0 && p < n_tab;  // a position outside the RoPE tables: the row writes nothing
+  const int sidx = p % ring;
+  const bool store_ok = in_tab && sl >= 0 && sl < cache_rows && sidx < cache_len;
   float xl[8], xh[8];
   rope_x(wlo, whi, blo, bhi, bias != nullptr, xl, xh);
 
@@ -56,9 +58,11 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     return;
   }
 
-  const uint16_t *crow = cos_tab + (int64_t)p * s_cs, *srow = sin_tab + (int64_t)p * s_cs;
+  const int pc = in_tab ? p : 0;  // the host launches nothing when the tables are empty
+  const uint16_t *crow = cos_tab + (int64_t)pc * s_cs, *srow = sin_tab + (int64_t)pc * s_cs;
   rope_rotate(xl, xh, ld16(crow + 8 * c), ld16(crow + 32 + 8 * c), ld16(srow + 8 * c), ld16(srow + 32 + 8 * c),
               olo, ohi);
+  if (!in_tab) return;
   uint16_t *dst;
   if (h < nq) {
     dst = qo + (int64_t)r * s_qo_r + (int64_t)h * s_qo_h;
@@ -93,6 +97,8 @@ extern "C" int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bi
       (bias && !al16(bias)) || (s_qkv | s_cs | s_qo_r | s_qo_h | s_kb | s_kh | s_ks) & 7)
     return set_error(A8_EALIGN, "bias_rope_store: pointers must be 16-byte aligned and strides multiples of 8");
   const int64_t threads = (int64_t)R * (nq + 2 * nkv) * 4;
+  if (threads >= (int64_t)1 << 31) return set_error(A8_EUNSUP, "bias_rope_store: %d rows x %d heads too many", R, nq + 2 * nkv);
+  if (n_tab == 0) return 0;  // no position is inside the tables: nothing is written
   const unsigned grid = (unsigned)((threads + 255) / 256);
   hipLaunchKernelGGL(k_bias_rope_store, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t *)qkv, s_qkv, (const uint16_t *)bias, (const uint16_t *)cos_tab,

@@ -123,7 +123,11 @@ class DecodeAttention:
     Two launch schedules compute the same softmax (split boundaries are not part of the contract):
       mode "split": a8_decode_attn -- the reference's split kernel + combine kernel structure, launch
         shape from a8_decode_choose for this GPU's compute-unit count; the caller's `nsplit` is a lower
-        bound on the splits (policy "auto") or exact (policy "caller").
+        bound on the splits (policy "auto") or exact (policy "caller"). merge_in_kernel = True makes the
+        split kernel merge the splits itself (the last split of each (row, kv head) to finish, counters
+        in self.counters), so no combine launch follows. Opt-in: measured on MI355X at C2 (64 ragged
+        rows, 4 splits) it is slower than the combine launch (15.5 against 15.0 us/layer; the last
+        arrival waits for its partial's write-through and the counter's round trip)
       mode "stream": a8_decode_attn_stream -- a persistent kernel that takes fixed-size key chunks in
         turn (whole rows when there are enough of them), plus a small merge kernel for rows longer than
         a chunk; launch shape from a8_decode_choose_stream.
@@ -149,9 +153,10 @@ class DecodeAttention:
         self.scale = scale if scale is not None else hd ** -0.5
         self.acc_flat = torch.empty(self.cap * nq * hd, dtype=torch.float32, device=device)
         self.ml_flat = torch.empty(self.cap * nq * 2, dtype=torch.float32, device=device)
-        # flat mode: one arrival counter per (row, kv head); zero between calls (each call re-zeroes what
-        # it used)
+        # flat mode and the split mode's in-kernel merge: one arrival counter per (row, kv head); zero
+        # between calls (each call re-zeroes what it used)
         self.counters = torch.zeros(self.cap * nkv, dtype=torch.int32, device=device)
+        self.merge_in_kernel = False
         dev = torch.device(device)
         self.n_cu = torch.cuda.get_device_properties(dev).multi_processor_count if dev.type == "cuda" else 1
         self.mode = "auto"
@@ -273,8 +278,8 @@ class DecodeAttention:
                  out.stride(1), self.acc_flat.data_ptr(), self.ml_flat.data_ptr(), self.cap)
         if kind == "split":
             ns, nw = shape
-            st = _lib.load().a8_store_decode_split(*store, R, self.nq, self.nkv, self.hd, ring, ns, nw,
-                                                   float(self.scale), int(phases), _lib.stream_of(qkv))
+            st = _lib.load().a8_store_decode_split(*store, *self._split_counters(), R, self.nq, self.nkv, self.hd,
+                                                   ring, ns, nw, float(self.scale), int(phases), _lib.stream_of(qkv))
         elif kind == "flat":
             (grid,) = shape
             st = _lib.load().a8_store_decode_flat(*store, self.counters.data_ptr(), self.counters.numel(), R,
@@ -286,6 +291,11 @@ class DecodeAttention:
                                                     float(self.scale), int(phases), _lib.stream_of(qkv))
         _lib.check(st, "store_and_attend")
         return out
+
+    def _split_counters(self):
+        """(counters, n_counters) for the split entry points: the in-kernel merge, or (None, 0) for the
+        split + combine launches."""
+        return (self.counters.data_ptr(), self.counters.numel()) if self.merge_in_kernel else (None, 0)
 
     def __call__(self, q, kc, vc, lens, out, nsplit=1, bn=64, rowmap=None, phases=3):
         """q: [b, nq, hd]; kc/vc: [rows, nkv, S, hd]; query row i reads cache row rowmap[i]
@@ -330,8 +340,8 @@ class DecodeAttention:
             _lib.check(st, "decode_attention")
             return out
         ns, nw = shape
-        st = lib.a8_decode_attn(*common, self.cap, b, self.nq, self.nkv, self.hd, ns, nw, float(self.scale),
-                                int(phases), _lib.stream_of(q))
+        st = lib.a8_decode_attn(*common, self.cap, *self._split_counters(), b, self.nq, self.nkv, self.hd, ns, nw,
+                                float(self.scale), int(phases), _lib.stream_of(q))
         _lib.check(st, "decode_attention")
         return out
 

@@ -85,11 +85,16 @@ int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bias,
  * out     [b, nq, hd] strides (s_ob, s_oh, 1)
  * acc_ws  fp32 workspace, >= ws_row_splits * nq * hd floats (DecodeAttention.acc_flat)
  * ml_ws   fp32 workspace, >= ws_row_splits * nq * 2 floats  (DecodeAttention.ml_flat)
+ * counters  NULL, or int32 [>= b * nkv] that start at 0 (DecodeAttention.counters; every launch leaves
+ *         them at 0): with counters the split kernel merges the splits itself -- the last split
+ *         workgroup of each (row, kv head) to finish combines the row's partials with the combine
+ *         kernel's arithmetic -- and no combine launch follows (one launch instead of two). Calls that
+ *         share counters or the workspace must not overlap in time (one stream).
  * nsplit  key-range splits per row (>= 1; b * nsplit <= ws_row_splits). With nsplit == 1 the
  *         split kernel writes `out` directly and no combine runs.
  * waves   wavefronts per workgroup that share one split's key range: 1, 2, 4 or 8.
  * phases  bit 0: run the split kernel, bit 1: run the combine kernel (3 = both; the normal value).
- *         Running them separately lets a caller time each kernel.
+ *         Running them separately lets a caller time each kernel. With counters, bit 1 is ignored.
  * Rows with lens == 0 produce NaN (0/0), exactly as the reference's combine does.
  * The cache positions must be contiguous rows (s_ks == hd == 64, true of every reference cache view);
  * otherwise A8_EUNSUP.
@@ -100,6 +105,7 @@ int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
                    const int32_t *lens, const int32_t *rowmap,
                    void *out, int64_t s_ob, int64_t s_oh,
                    float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                   int32_t *counters, int64_t n_counters,
                    int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
                    int phases, void *stream);
 
@@ -155,6 +161,7 @@ int a8_store_decode_split(const void *qkv, int64_t s_qkv, const void *bias,
                           int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap,
                           void *out, int64_t s_ob, int64_t s_oh,
                           float *acc_ws, float *ml_ws, int64_t ws_row_splits,
+                          int32_t *counters, int64_t n_counters,
                           int b, int nq, int nkv, int hd, int ring, int nsplit, int waves, float scale,
                           int phases, void *stream);
 

@@ -59,8 +59,8 @@ def test_store_rejects_before_launch(a8):
 
 def _decode_args(**kw):
     a = dict(q=16, s_qb=896, s_qh=64, kc=16, vc=16, s_kb=1024, s_kh=512, s_ks=64, rows=1, S=8, lens=16,
-             rowmap=None, out=16, s_ob=896, s_oh=64, acc=16, ml=16, ws=4, b=1, nq=14, nkv=2, hd=64, nsplit=1,
-             waves=4, scale=0.125, phases=3, stream=None)
+             rowmap=None, out=16, s_ob=896, s_oh=64, acc=16, ml=16, ws=4, counters=None, n_counters=0, b=1, nq=14,
+             nkv=2, hd=64, nsplit=1, waves=4, scale=0.125, phases=3, stream=None)
     a.update(kw)
     return list(a.values())
 
@@ -75,6 +75,10 @@ def test_decode_rejects_before_launch(a8):
     assert lib.a8_decode_attn(*_decode_args(b=3, nsplit=2, ws=5)) == -4  # workspace: 6 row-splits needed
     assert lib.a8_decode_attn(*_decode_args(out=8)) == -2
     assert lib.a8_decode_attn(*_decode_args(b=0)) == 0
+    # the in-kernel merge: one counter per (row, kv head), and the split kernel must run
+    assert lib.a8_decode_attn(*_decode_args(b=3, nsplit=2, ws=6, counters=16, n_counters=5)) == -4
+    assert b"counters" in lib.a8_last_error()
+    assert lib.a8_decode_attn(*_decode_args(nsplit=2, ws=4, counters=16, n_counters=2, phases=2)) == -1
 
 
 def _prefill_args(**kw):

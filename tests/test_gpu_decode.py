@@ -93,6 +93,39 @@ def test_decode_launch_shapes(a8, ref, dev, ns, nw):
     assert maxabs(out, want) <= TOL
 
 
+@pytest.mark.parametrize("ns,nw", [(2, 1), (4, 1), (16, 1), (3, 2), (4, 4), (9, 8)])
+def test_decode_merge_in_kernel(a8, ref, dev, ns, nw):
+    """The split kernel's own merge (last split to finish, arrival counters) gives the bits of the split +
+    combine launches, leaves every counter at zero, and the next call (fewer rows) is right as well."""
+    say(f"case: decode in-kernel merge nsplit={ns} waves={nw}")
+    g = torch.Generator().manual_seed(26)
+    b, S = 12, 1100
+    q = randn_bf16(g, b, NQ, HD).to(dev)
+    kc, vc = randn_bf16(g, b, NKV, S, HD).to(dev), randn_bf16(g, b, NKV, S, HD).to(dev)
+    lens = torch.tensor([1, 2, 63, 64, 65, 127, 128, 129, 500, 1023, 1100, 0], dtype=torch.int32).to(dev)
+    att = a8.DecodeAttention(b * 16, NQ, NKV, HD, 16, dev)
+    att.force_shape = (ns, nw)
+    outs = {}
+    for merge in (False, True, True):
+        att.merge_in_kernel = merge
+        o = torch.full((b, NQ, HD), 7.0, dtype=BF, device=dev)
+        att(q, kc, vc, lens, o)
+        torch.cuda.synchronize()
+        outs.setdefault(merge, []).append(o.cpu())
+        assert int(att.counters.abs().sum()) == 0
+    assert torch.equal(outs[True][0].view(torch.int16), outs[False][0].view(torch.int16))
+    assert torch.equal(outs[True][1].view(torch.int16), outs[False][0].view(torch.int16))
+    want = ref.decode_attention(q.cpu()[:11], kc.cpu()[:11], vc.cpu()[:11], lens.cpu()[:11], nsplit=1)
+    assert maxabs(outs[True][0][:11], want) <= TOL
+    assert torch.isnan(outs[True][0][11].float()).all()  # lens 0: 0/0 as the reference
+    # a smaller call through the same counters and workspace
+    o = torch.empty(5, NQ, HD, dtype=BF, device=dev)
+    att(q[:5], kc, vc, lens[:5], o)
+    torch.cuda.synchronize()
+    assert torch.equal(o.cpu().view(torch.int16), outs[False][0][:5].view(torch.int16))
+    assert int(att.counters.abs().sum()) == 0
+
+
 def test_decode_edge_lengths(a8, dev):
     say("case: decode L=0 / L=1 / lens > S")
     g = torch.Generator().manual_seed(23)
@@ -141,6 +174,7 @@ def test_decode_phases_split_then_combine(a8, ref, dev):
     kc, vc = randn_bf16(g, b, NKV, S, HD).to(dev), randn_bf16(g, b, NKV, S, HD).to(dev)
     lens = torch.randint(1, S + 1, (b,), generator=g).int().to(dev)
     att = a8.DecodeAttention(16 * b, NQ, NKV, HD, 16, dev)
+    att.merge_in_kernel = False  # the split + combine launches (the in-kernel merge has one phase)
     for split, stream in (((5, 2), None), (None, (2, 1, 9))):
         att.force_shape, att.force_stream = split, stream
         o1, o2 = torch.empty(b, NQ, HD, dtype=BF, device=dev), torch.empty(b, NQ, HD, dtype=BF, device=dev)

@@ -31,11 +31,12 @@ def _inputs(seed, b, rows, S, lens, pos, slot, bias=True, max_pos=4096):
                 max_pos=max_pos)
 
 
-def _run_both(a8, dev, x, shape, ring=1 << 30, write_q=True, use_rowmap=True, split=False):
+def _run_both(a8, dev, x, shape, ring=1 << 30, write_q=True, use_rowmap=True, split=False, merge=False):
     cos, sin = a8.rope_tables(10000.0, HD, x["max_pos"], dev)
     b = x["qkv"].shape[0]
     d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in x.items()}
     att = a8.DecodeAttention(max(16 * b, 8192), NQ, NKV, HD, 16, dev)
+    att.merge_in_kernel = merge
     if split:
         att.force_shape = shape   # (nsplit, waves): the split + combine schedule, store in the split kernel
     else:
@@ -177,13 +178,15 @@ def test_store_and_attend_short_rows_auto(a8, ref, dev, b, S):
     assert (o1.float() - want.float()).abs().max().item() <= 2e-2
 
 
-@pytest.mark.parametrize("shape", [(1, 1), (1, 4), (3, 2), (4, 1), (8, 4), (16, 1)])
-def test_store_and_attend_split_schedule(a8, dev, shape):
+@pytest.mark.parametrize("shape,merge", [((1, 1), False), ((1, 4), False), ((3, 2), False), ((4, 1), False),
+                                         ((8, 4), False), ((16, 1), False), ((3, 2), True), ((4, 1), True),
+                                         ((16, 1), True)])
+def test_store_and_attend_split_schedule(a8, dev, shape, merge):
     """The store done by the split kernel (a8_store_decode_split) equals bias_rope_store then the split
     decode at the same (nsplit, waves), bit for bit: the edge rows of the streaming test (new key at the end,
     inside or past the attended range, ring wrap, a slot outside the cache, no bias), with rowmap = slot and
-    with no row map."""
-    say(f"case: fused store + split decode, shape {shape}")
+    with no row map; also with the splits merged inside the split kernel (merge)."""
+    say(f"case: fused store + split decode, shape {shape}, merge in kernel {merge}")
     S, rows, ring = 1024, 40, 1000
     lens = [1, 2, 64, 65, 1000, 700, 512, 1000, 300, 5, 900, 1000, 640, 1, 128, 999]
     pos = [0, 1, 63, 64, 999, 100, 900, 1500, 299, 4, 2, 1999, 639, 0, 127, 998]
@@ -191,7 +194,7 @@ def test_store_and_attend_split_schedule(a8, dev, shape):
     b = len(lens)
     for bias in (True, False):
         x = _inputs(71 + bias, b, rows, S, lens, pos, slot, bias=bias)
-        (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, shape, ring=ring, split=True)
+        (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, shape, ring=ring, split=True, merge=merge)
         assert _bits_equal(q0, q1)
         assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
         assert _bits_equal(o0, o1)
@@ -200,7 +203,7 @@ def test_store_and_attend_split_schedule(a8, dev, shape):
     x = _inputs(73, b, rows, S, lens, pos, slot2)
     for write_q in (True, False):
         (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, shape, ring=ring, write_q=write_q,
-                                                       use_rowmap=False, split=True)
+                                                       use_rowmap=False, split=True, merge=merge)
         assert _bits_equal(q0, q1) if write_q else not q1.any()
         assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
         assert _bits_equal(o0, o1)
