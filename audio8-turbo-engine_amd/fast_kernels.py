@@ -398,3 +398,36 @@ def prefill_attention(q, kc, vc, plan, out, group, scale=None):
         nq, group, hd, float(scale), _lib.stream_of(q))
     _lib.check(st, "prefill_attention")
     return out
+
+
+def prefix_copy(k, v, kc_all, vc_all, slots):
+    """kc_all[:, slots, :, :Lp] = k.unsqueeze(1) and vc_all[:, slots, :, :Lp] = v.unsqueeze(1) in one launch:
+    a voice prefix's K/V ([layers, nkv, Lp, hd] each, from _prefix_kv) into the cache rows of the requests
+    that use it (fast_engine.py:1098-1103; caches [layers, rows, nkv, S, hd]). `slots` is an int32 tensor on
+    the device (or a list, uploaded here). A slot outside the cache is skipped (the reference's index-put
+    would raise)."""
+    _check_bf16("k", k, 4)
+    _check_bf16("v", v, 4)
+    _need(k.shape == v.shape and k.stride() == v.stride(), "k and v must have the same shape and strides")
+    _check_bf16("kc_all", kc_all, 5)
+    _check_bf16("vc_all", vc_all, 5)
+    _need(kc_all.shape == vc_all.shape and kc_all.stride() == vc_all.stride(),
+          "kc_all and vc_all must have the same shape and strides")
+    layers, nkv, Lp, hd = k.shape
+    _need(kc_all.shape[0] == layers and kc_all.shape[2] == nkv and kc_all.shape[4] == hd,
+          f"cache shape {tuple(kc_all.shape)} does not match [{layers}, rows, {nkv}, S, {hd}]")
+    _need(Lp <= kc_all.shape[3], f"prefix of {Lp} positions does not fit a cache of {kc_all.shape[3]}")
+    if not isinstance(slots, torch.Tensor):
+        slots = torch.tensor(list(slots), dtype=_I32)
+        if kc_all.is_cuda:
+            slots = slots.pin_memory().to(kc_all.device, non_blocking=True)
+    _check_i32("slots", slots, 0)
+    _check_device(k=k, v=v, kc_all=kc_all, vc_all=vc_all, slots=slots)
+    n = slots.shape[0]
+    if n == 0 or layers == 0 or Lp == 0:
+        return
+    st = _lib.load().a8_prefix_copy(
+        k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        kc_all.data_ptr(), vc_all.data_ptr(), kc_all.stride(0), kc_all.stride(1), kc_all.stride(2), kc_all.stride(3),
+        slots.data_ptr(), n, layers, nkv, Lp, hd, kc_all.shape[1], kc_all.shape[3], _lib.stream_of(kc_all))
+    _lib.check(st, "prefix_copy")

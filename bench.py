@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--no-configs", action="store_true", help="skip the other configs' figures (C1, C2, C4, C5)")
     p.add_argument("--traffic-probe", action="store_true",
                    help="only launch one layer's decode 4x and a 256 MiB copy (target of rocprofv3 --pmc passes)")
+    p.add_argument("--prefill-probe", action="store_true",
+                   help="only launch the C4 prefill 3x (target of rocprofv3 --pmc passes)")
     return p.parse_args()
 
 
@@ -210,6 +212,39 @@ def per_config(a8, torch, dev, steps):
     del g, st, qkvs, outs
     torch.cuda.empty_cache()
 
+    # Codec window transformer (beside configs C1-C5): the same kernels on a 128-position
+    # ring with caches that are views into a per-row byte arena (fast_engine.py:337-341, 368-387, 470-477),
+    # 192 rows with a full window (lens 128, positions past the wrap). The codec's own head shape needs the
+    # checkpoint (absent offline), so the slow stack's 14 / 2 x 64 stands in.
+    b, S, layers = 192, 128, 4
+    st = a8.AttnStack(layers, NQ, NKV, HD, 10000.0, max_rows=b, cache_rows=b, cache_len=S, max_pos=4096, dev=dev,
+                      nsplit_max=1, ring=S)
+    per = NKV * S * HD
+    arena = torch.zeros(b, layers * 2 * (per + 8), dtype=torch.bfloat16, device=dev)
+    for i in range(layers):
+        o = i * 2 * (per + 8)
+        st.kc[i] = arena[:, o:o + per].view(b, NKV, S, HD)
+        st.vc[i] = arena[:, o + per + 8:o + 2 * per + 8].view(b, NKV, S, HD)
+        st.kc[i].normal_(generator=gen)
+        st.vc[i].normal_(generator=gen)
+    pos = torch.full((b,), 1000, dtype=torch.int32, device=dev)
+    lens_d = torch.full((b,), S, dtype=torch.int32, device=dev)
+    slot = torch.arange(b, dtype=torch.int32, device=dev)
+    qkv = [randn(b, W) for _ in range(layers)]
+    bias = [randn(W, std=0.02) for _ in range(layers)]
+    q = torch.empty(b, NQ, HD, dtype=torch.bfloat16, device=dev)
+    outs = [torch.empty(b, NQ, HD, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+    g = capture(torch, lambda: st.forward(qkv, bias, pos, slot, lens_d, nsplit=1, rowmap=False, q=q, outs=outs,
+                                          fuse=True))
+    us = time_median(torch, g, steps, 10) * 1e3 / layers
+    nbytes = ref_counts.decode_bytes([S] * b, NQ, NKV, HD)
+    res["codec_window"] = {"us_per_layer": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1), "rows": b,
+                           "kv_len": S, "ring": S, "schedule": list(st.attn.schedule(b, S, fused=True)),
+                           "note": "fused store + decode on the 128-position ring, arena-strided caches; "
+                                   "latency bound (~13 MB per layer)"}
+    del g, st, qkv, outs, arena
+    torch.cuda.empty_cache()
+
     # C4: 64 requests, n ~ U[40, 400], after a 300-position voice prefix; store + packed prefill per layer
     ns = torch.randint(40, 401, (64,), generator=torch.Generator().manual_seed(0)).tolist()
     p0, nreq, layers = 300, 64, LAYERS
@@ -238,7 +273,33 @@ def per_config(a8, torch, dev, steps):
     g = capture(torch, pf_only)
     us_pf = time_median(torch, g, steps, 10) * 1e3 / layers
     flops = ref_counts.prefill_flops(ns, [p0] * nreq, NQ, HD)
+    # the admission step before it: the voices' prefix K/V into the 64 slots (4 voices x 16 slots, all layers;
+    # fast_engine.py:1098-1103), one a8_prefix_copy per voice, against the reference's torch index-puts
+    pk = [randn(layers, NKV, p0, HD) for _ in range(4)]
+    pv = [randn(layers, NKV, p0, HD) for _ in range(4)]
+    groups = [torch.arange(16 * j, 16 * j + 16, dtype=torch.int32, device=dev) for j in range(4)]
+
+    def pcopy():
+        for j in range(4):
+            a8.prefix_copy(pk[j], pv[j], st.kc_all, st.vc_all, groups[j])
+
+    def pcopy_torch():
+        for j in range(4):
+            idx = groups[j].long()
+            st.kc_all[:, idx, :, :p0] = pk[j].unsqueeze(1)
+            st.vc_all[:, idx, :, :p0] = pv[j].unsqueeze(1)
+
+    g = capture(torch, pcopy)
+    us_pc = time_median(torch, g, steps, 10) * 1e3
+    del g
+    g = capture(torch, pcopy_torch)
+    us_pc_torch = time_median(torch, g, steps, 10) * 1e3
+    pc_bytes = 2 * layers * NKV * p0 * HD * 2 * (nreq + 4)  # K+V written into 64 slots + the 4 prefixes read
     res["C4"] = {"us_per_layer": round(us, 3), "prefill_us_per_layer": round(us_pf, 3),
+                 "prefix_copy": {"us": round(us_pc, 3), "GB/s": round(pc_bytes / us_pc / 1e3, 1),
+                                 "frac_hbm": round(pc_bytes / us_pc / 1e3 / HBM_PEAK_GBS, 4), "bytes": pc_bytes,
+                                 "torch_index_put_us": round(us_pc_torch, 3),
+                                 "note": "4 voices x 16 slots x 24 layers x 300 positions, K and V"},
                  "prefill_TFLOP/s": round(flops / us_pf / 1e6, 1),
                  "frac_mfma_bf16": round(flops / us_pf / 1e6 / MFMA_BF16_TFLOPS, 4), "flops_per_layer": flops,
                  "rows": R, "blocks": plan.nblk,
@@ -280,6 +341,26 @@ def traffic_probe(torch, st, w, nsplit_req):
     print("traffic probe: 4 tick-layer launches, 2 copies of 268435456 bytes", flush=True)
 
 
+def prefill_probe(a8, torch, dev):
+    """Counter target for the prefill: the C4 workload (64 requests, n ~ U[40, 400] after a 300-position
+    prefix, 13,745 packed rows) launched 3 times. Run under rocprofv3 --pmc with one counter group a pass."""
+    import numpy as np
+    g = torch.Generator(device=dev).manual_seed(7)
+    ns = torch.randint(40, 401, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+    p0, S, nreq = 300, 704, 64
+    R = sum(ns)
+    kc = torch.randn(nreq + 1, NKV, S, HD, generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn(nreq + 1, NKV, S, HD, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(R, NQ, HD, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    plan = a8.PrefillPlan(r0s, ns, list(range(nreq)), [p0] * nreq, dev)
+    for _ in range(3):
+        a8.prefill_attention(q, kc, vc, plan, out, NQ // NKV)
+    torch.cuda.synchronize()
+    print(f"prefill probe: 3 launches, {R} rows, {plan.nblk} blocks", flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -294,6 +375,9 @@ def main():
     from oracle import attn_ref as ref_counts  # byte counts only (the timed GPU path never touches it)
 
     dev = torch.device("cuda:0")
+    if args.prefill_probe:
+        prefill_probe(a8, torch, dev)
+        return
     props = torch.cuda.get_device_properties(dev)
     w = build_workload(a8, torch, args.config, dev)
     st, b = w["st"], w["b"]

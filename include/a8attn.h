@@ -8,6 +8,9 @@
  *   a8_decode_attn       split-K flash-decoding over the slot cache (GQA), split + combine
  *   a8_prefill_attn      packed variable-length causal prefill attention over cache rows
  *
+ * and the admission copy of a cached voice prefix's K/V into slots (a8_prefix_copy, an index-put of
+ * serve/fast_engine.py), plus the launch-shape choosers and fused / alternative schedules below.
+ *
  * Conventions shared by every entry point:
  *   - All tensors are bf16 (stored as 16-bit words) unless the argument says otherwise; index
  *     tensors are int32. Every pointer is a device pointer (hipMalloc'ed or a view into one).
@@ -252,6 +255,23 @@ int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
                     const int32_t *bq0, const int32_t *bn, const int32_t *bslot,
                     const int32_t *bpos0, int nblk, int bm,
                     int nq, int group, int hd, float scale, void *stream);
+
+/*
+ * A voice prefix's K and V into the cache rows of the requests that use it, one launch for all layers
+ * and slots. Replaces the two index-puts of serve/fast_engine.py:1102-1103 (FastEngine._prefill step 1:
+ * kc_all[:, idx, :, :Lp] = k.unsqueeze(1), vc_all likewise), whose k / v come from _prefix_kv
+ * (fast_engine.py:1073-1087).
+ *
+ * k, v            [layers, nkv, Lp, hd] strides (s_l, s_h, s_p, 1)
+ * kc_all, vc_all  [layers, cache_rows, nkv, cache_len, hd] strides (d_l, d_r, d_h, d_p, 1) (shared)
+ * slots           [n] int32: kc_all[l, slots[i], h, p] = k[l, h, p] and vc_all likewise, p < Lp.
+ *                 A slot outside [0, cache_rows) is skipped (the reference would raise).
+ * Positions must be contiguous rows on both sides (s_p == d_p == hd == 64); Lp <= cache_len.
+ */
+int a8_prefix_copy(const void *k, const void *v, int64_t s_l, int64_t s_h, int64_t s_p,
+                   void *kc_all, void *vc_all, int64_t d_l, int64_t d_r, int64_t d_h, int64_t d_p,
+                   const int32_t *slots, int n, int layers, int nkv, int Lp, int hd, int cache_rows,
+                   int cache_len, void *stream);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,7 @@ def test_header_declares_the_entry_points():
                                          "a8_decode_attn", "a8_decode_choose", "a8_decode_attn_stream",
                                          "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn",
                                          "a8_decode_attn_flat", "a8_decode_choose_flat", "a8_store_decode_flat",
-                                         "a8_store_decode_split"}
+                                         "a8_store_decode_split", "a8_prefix_copy"}
 
 
 def test_library_exports_every_declared_symbol(a8):
@@ -244,3 +244,25 @@ def test_decode_choose_flat_contract(a8):
     assert _choose_flat(lib, 64, S=4096) == (0, 256)                 # C2: the whole GPU
     assert _choose_flat(lib, 384, S=10, cap=384) == (0, 96)          # C5 (fast stack workspace)
 
+
+
+def _prefix_args(**kw):
+    a = dict(k=16, v=16, s_l=2 * 300 * 64, s_h=300 * 64, s_p=64, kc=16, vc=16, d_l=70 * 2 * 704 * 64,
+             d_r=2 * 704 * 64, d_h=704 * 64, d_p=64, slots=16, n=4, layers=24, nkv=2, Lp=300, hd=64, rows=70, S=704,
+             stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_prefix_copy_rejects_before_launch(a8):
+    lib = a8.load_library()
+    assert lib.a8_prefix_copy(*_prefix_args(hd=128)) == -3
+    assert lib.a8_prefix_copy(*_prefix_args(Lp=705)) == -1          # the prefix does not fit the cache
+    assert b"705" in lib.a8_last_error()
+    assert lib.a8_prefix_copy(*_prefix_args(s_p=128)) == -3         # positions must be contiguous rows
+    assert lib.a8_prefix_copy(*_prefix_args(k=24)) == -2            # misaligned
+    assert lib.a8_prefix_copy(*_prefix_args(d_r=100)) == -2         # stride not a multiple of 8
+    assert lib.a8_prefix_copy(*_prefix_args(slots=None)) == -1
+    assert lib.a8_prefix_copy(*_prefix_args(n=-1)) == -1
+    for zero in (dict(n=0), dict(layers=0), dict(Lp=0)):
+        assert lib.a8_prefix_copy(*_prefix_args(**zero)) == 0     # nothing to do, nothing launched
