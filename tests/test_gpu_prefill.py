@@ -134,6 +134,88 @@ def test_prefill_graph_mode_plan(a8, ref, dev):
     assert torch.equal(out[R:].cpu(), sentinel[R:].cpu())
 
 
+def test_prefill_graph_replay_admissions(a8, ref, dev):
+    """The engine's prefill graph per token bucket (fast_engine.py:797-812, 820-853, 1109-1116): the stack's
+    store + prefill captured once over a PrefillMeta buffer, then replayed for admissions with other slots,
+    lengths and prefixes (each written by one host-to-device copy, and each admission's prefix K/V put into
+    its slots by prefix_copy first). Every replay equals the eager forward on the same inputs bit for bit, and
+    the eager forward matches the oracle."""
+    say("case: prefill graph captured once, replayed for three admissions")
+    g = torch.Generator().manual_seed(35)
+    NT, NR, rows, S, layers = 512, 8, 9, 640, 2
+    SCR = rows - 1
+    W = (NQ + 2 * NKV) * HD
+    st = a8.AttnStack(layers, NQ, NKV, HD, 10000.0, max_rows=NT, cache_rows=rows, cache_len=S, max_pos=S, dev=dev)
+    meta = a8.PrefillMeta(NT, NR, SCR, dev)
+    nt = 512
+    qkv = [torch.zeros(NT, W, dtype=BF, device=dev) for _ in range(layers)]
+    bias = [randn_bf16(g, W, std=0.02).to(dev) for _ in range(layers)]
+    q = torch.empty(NT, NQ, HD, dtype=BF, device=dev)
+    outs = [torch.zeros(NT, NQ, HD, dtype=BF, device=dev) for _ in range(layers)]
+    v = meta.v
+
+    def body():
+        st.forward(qkv, bias, v.pos[:nt], v.slot[:nt], None, plan=meta.plan(nt), q=q, outs=outs)
+
+    admissions = [([0, 3, 1], [130, 7, 64], [200, 0, 17]), ([5, 2], [300, 190], [100, 0]),
+                  ([7, 6, 4, 0, 1], [1, 64, 65, 100, 250], [300, 300, 0, 20, 300])]
+    meta.load(nt, *admissions[0])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body()
+    torch.cuda.synchronize()
+    prefix_k = randn_bf16(g, layers, NKV, 300, HD).to(dev)
+    prefix_v = randn_bf16(g, layers, NKV, 300, HD).to(dev)
+    for slots, ns, starts in admissions:
+        R = sum(ns)
+        kc0 = randn_bf16(g, layers, rows, NKV, S, HD).to(dev)
+        vc0 = randn_bf16(g, layers, rows, NKV, S, HD).to(dev)
+        x = [randn_bf16(g, R, W).to(dev) for _ in range(layers)]
+        res = []
+        for mode in ("graph", "eager"):
+            st.kc_all.copy_(kc0)
+            st.vc_all.copy_(vc0)
+            a8.prefix_copy(prefix_k, prefix_v, st.kc_all, st.vc_all, [s_ for s_, a in zip(slots, starts) if a == 300])
+            meta.load(nt, slots, ns, starts)
+            for i in range(layers):
+                qkv[i].zero_()
+                qkv[i][:R].copy_(x[i])
+                outs[i].zero_()
+            if mode == "graph":
+                graph.replay()
+            else:
+                body()
+            torch.cuda.synchronize()
+            res.append(([o[:R].cpu() for o in outs], st.kc_all.cpu(), st.vc_all.cpu()))
+        (og, kg, vg), (oe, ke, ve) = res
+        assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(og, oe))
+        assert torch.equal(kg.view(torch.int16), ke.view(torch.int16))
+        assert torch.equal(vg.view(torch.int16), ve.view(torch.int16))
+        # the oracle on the last layer: the initial cache, the prefix put into its slots, the store, the prefill
+        r0s = [int(r) for r in np.cumsum([0] + ns[:-1])]
+        qo = torch.zeros(R, NQ, HD, dtype=BF)
+        pos = torch.cat([torch.arange(a, a + n) for a, n in zip(starts, ns)]).int()
+        slot = torch.cat([torch.full((n,), s_) for s_, n in zip(slots, ns)]).int()
+        kl, vl = kc0[layers - 1].cpu(), vc0[layers - 1].cpu()
+        for s_, a in zip(slots, starts):
+            if a == 300:
+                kl[s_, :, :300] = prefix_k[layers - 1].cpu()
+                vl[s_, :, :300] = prefix_v[layers - 1].cpu()
+        cos, sin = ref.rope_tables(10000.0, HD, S)
+        ref.bias_rope_store(x[layers - 1].cpu(), bias[layers - 1].cpu(), cos, sin, pos, slot, qo, kl, vl, NQ, NKV, HD)
+        # (the padding rows store into the scratch row SCR, as in the reference; the other rows must match)
+        assert torch.equal(kl[:SCR].view(torch.int16), ke[layers - 1, :SCR].view(torch.int16))
+        assert torch.equal(vl[:SCR].view(torch.int16), ve[layers - 1, :SCR].view(torch.int16))
+        want = torch.zeros(R, NQ, HD, dtype=BF)
+        ref.prefill_attention(qo, kl, vl, *ref.prefill_plan(r0s, ns, slots, starts), want, NQ // NKV)
+        assert maxabs(oe[layers - 1], want) <= TOL
+
+
 def test_prefill_rows_match_decode(a8, dev):
     """HIP prefill row j == HIP decode with lens = p0 + j + 1 on the same cache row (two independent kernels)."""
     say("case: prefill vs decode cross-check")
