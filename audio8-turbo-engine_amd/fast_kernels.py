@@ -431,3 +431,48 @@ def prefix_copy(k, v, kc_all, vc_all, slots):
         kc_all.data_ptr(), vc_all.data_ptr(), kc_all.stride(0), kc_all.stride(1), kc_all.stride(2), kc_all.stride(3),
         slots.data_ptr(), n, layers, nkv, Lp, hd, kc_all.shape[1], kc_all.shape[3], _lib.stream_of(kc_all))
     _lib.check(st, "prefix_copy")
+
+
+def rmsnorm(x, w, eps, residual=None, out=None, res_out=None):
+    """x: [..., N] bf16. With residual: h = x + residual (bf16, stored to res_out, default in place into
+    residual) and returns (rmsnorm(h), h); without: returns rmsnorm(x) (fast_kernels.py:49-69, kernel 30-46:
+    fp32 sum of squares, xn rounded to bf16, then weight * xn rounded to bf16)."""
+    _need(isinstance(x, torch.Tensor) and x.dtype == _BF16, "x must be a bfloat16 tensor", TypeError)
+    N = x.shape[-1]
+    x2 = x.reshape(-1, N)
+    y = out if out is not None else torch.empty_like(x)
+    y2 = y.reshape(-1, N)
+    _check_bf16("w", w, 1)
+    _need(w.shape[0] == N, f"w has {w.shape[0]} entries, {N} needed")
+    for name, t in (("x", x2), ("out", y2)):
+        _need(t.stride(-1) == 1, f"{name}: the last dim must be contiguous")
+    r2 = ro2 = None
+    if residual is not None:
+        _need(residual.dtype == _BF16 and residual.shape[-1] == N, "residual must be bfloat16 of the same width")
+        ro = res_out if res_out is not None else residual
+        r2, ro2 = residual.reshape(-1, N), ro.reshape(-1, N)
+        _need(r2.shape[0] == x2.shape[0] and ro2.shape[0] == x2.shape[0], "residual rows must match x")
+        _need(r2.stride(-1) == 1 and ro2.stride(-1) == 1, "residual: the last dim must be contiguous")
+    _check_device(x=x2, w=w, out=y2, residual=r2, res_out=ro2)
+    st = _lib.load().a8_rmsnorm(x2.data_ptr(), x2.stride(0), r2.data_ptr() if r2 is not None else None,
+                                r2.stride(0) if r2 is not None else 0, w.data_ptr(), y2.data_ptr(), y2.stride(0),
+                                ro2.data_ptr() if ro2 is not None else None, ro2.stride(0) if ro2 is not None else 0,
+                                x2.shape[0], N, float(eps), _lib.stream_of(x2))
+    _lib.check(st, "rmsnorm")
+    return (y, ro) if residual is not None else y
+
+
+def silu_mul(gu, out=None):
+    """gu: [..., 2I] bf16 -> [..., I]: bf16(bf16(silu(g)) * u) with g, u the two halves
+    (fast_kernels.py:537-545, kernel 526-534)."""
+    _need(isinstance(gu, torch.Tensor) and gu.dtype == _BF16, "gu must be a bfloat16 tensor", TypeError)
+    I = gu.shape[-1] // 2
+    g2 = gu.reshape(-1, 2 * I)
+    y = out if out is not None else torch.empty(*gu.shape[:-1], I, dtype=gu.dtype, device=gu.device)
+    y2 = y.reshape(-1, I)
+    _need(g2.stride(-1) == 1 and y2.stride(-1) == 1, "gu / out: the last dim must be contiguous")
+    _check_device(gu=g2, out=y2)
+    st = _lib.load().a8_silu_mul(g2.data_ptr(), g2.stride(0), y2.data_ptr(), y2.stride(0), g2.shape[0], I,
+                                 _lib.stream_of(g2))
+    _lib.check(st, "silu_mul")
+    return y

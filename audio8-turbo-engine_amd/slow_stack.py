@@ -1,0 +1,78 @@
+"""The slow AR's transformer stack around the attention path (reference serve/fast_engine.py:82-138, _Stack).
+
+Per layer (fast_engine.py:117-138): qkv = h @ wqkv^T -> bias + RoPE + K/V store -> decode (or packed prefill)
+attention -> a = o @ wo^T -> (h, res) = rmsnorm(a, ln2, residual=res) -> m = silu_mul(h @ w13^T) @ w2^T ->
+(h, res) = rmsnorm(m, next ln1 or the final norm, residual=res). The attention is AttnStack (this package's
+kernels, the reference's cache layout and store-then-attend order); the norms and the gated activation are
+this package's kernels (rmsnorm, silu_mul); the four projections are plain library GEMMs (torch.matmul ->
+hipBLASLt), exactly the reference's default `mm` (fast_engine.py:90).
+
+Weights are the reference's fused layout per layer: wqkv [(nq+2nkv)hd, hidden] (q/k rows already in
+rotate_half order, fast_engine.py:100-101), bqkv or None, wo [hidden, nq hd], w13 = cat(w1, w3) [2 inter,
+hidden], w2 [hidden, inter], ln1 / ln2 [hidden], and the final norm. Without a checkpoint (none exists
+offline) `random_weights` draws a synthetic set of that shape."""
+from __future__ import annotations
+
+import torch
+
+from .attn_stack import AttnStack
+from .fast_kernels import rmsnorm, silu_mul
+
+
+def random_weights(n_layers, hidden, nq, nkv, hd, inter, dev, seed=0, dt=torch.bfloat16):
+    """Synthetic weights of the slow AR's shapes: projections ~ N(0, 1/fan_in) (unit-variance outputs),
+    biases ~ N(0, 0.02^2), norm weights ~ 1 + N(0, 0.05^2)."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+
+    def lin(n, k):
+        return (torch.randn(n, k, generator=g, device=dev) / k ** 0.5).to(dt)
+
+    def vec(n, mean, std):
+        return (mean + std * torch.randn(n, generator=g, device=dev)).to(dt)
+
+    W = (nq + 2 * nkv) * hd
+    layers = [dict(wqkv=lin(W, hidden), bqkv=vec(W, 0.0, 0.02), wo=lin(hidden, nq * hd), w13=lin(2 * inter, hidden),
+                   w2=lin(hidden, inter), ln1=vec(hidden, 1.0, 0.05), ln2=vec(hidden, 1.0, 0.05))
+              for _ in range(n_layers)]
+    return layers, vec(hidden, 1.0, 0.05)
+
+
+class SlowStack:
+    """forward(x, pos, slot, lens, nsplit=1, rowmap=True, plan=None) as _Stack.forward (fast_engine.py:117-138):
+    R independent token rows, row r at RoPE position pos[r], its K/V stored into cache row slot[r] and
+    attending columns [0, lens[r]) of cache row slot[r] (rowmap) or r; with a PrefillPlan the packed causal
+    prefill instead. Returns the final-normed hidden [R, hidden]; `x` is consumed (the residual stream is
+    updated in place), as in the reference. fuse=True lets the store and the decode share one launch where
+    every row attends its own slot (AttnStack.forward)."""
+
+    def __init__(self, layers, norm, nq, nkv, hd, eps, rope_base, max_rows, cache_rows, cache_len, max_pos, dev,
+                 nsplit_max=16, ring=None):
+        self.layers = layers
+        self.norm = norm
+        self.nq, self.nkv, self.hd, self.eps = nq, nkv, hd, float(eps)
+        self.attn = AttnStack(len(layers), nq, nkv, hd, rope_base, max_rows, cache_rows, cache_len, max_pos, dev,
+                              nsplit_max=nsplit_max, ring=ring)
+        self.kc_all, self.vc_all = self.attn.kc_all, self.attn.vc_all
+        self.kc, self.vc = self.attn.kc, self.attn.vc
+
+    @staticmethod
+    def mm(x, w):
+        return torch.matmul(x, w.t())
+
+    def forward(self, x, pos, slot, lens, nsplit=1, rowmap=True, plan=None, fuse=False):
+        R = x.shape[0]
+        nl = len(self.layers)
+        h = rmsnorm(x, self.layers[0]["ln1"], self.eps)
+        res = x
+        q = torch.empty(R, self.nq, self.hd, dtype=x.dtype, device=x.device)
+        o = torch.empty_like(q)
+        for i, L in enumerate(self.layers):
+            qkv = self.mm(h, L["wqkv"])
+            self.attn.layer(i, qkv, L["bqkv"], pos, slot, lens, q, o, nsplit=nsplit, rowmap=rowmap, plan=plan,
+                            fuse=fuse)
+            a = self.mm(o.view(R, -1), L["wo"])
+            h, res = rmsnorm(a, L["ln2"], self.eps, residual=res)
+            m = self.mm(silu_mul(self.mm(h, L["w13"])), L["w2"])
+            nxt = self.layers[i + 1]["ln1"] if i + 1 < nl else self.norm
+            h, res = rmsnorm(m, nxt, self.eps, residual=res)
+        return h

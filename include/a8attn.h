@@ -273,6 +273,20 @@ int a8_prefix_copy(const void *k, const void *v, int64_t s_l, int64_t s_h, int64
                    const int32_t *slots, int n, int layers, int nkv, int Lp, int hd, int cache_rows,
                    int cache_len, void *stream);
 
+/*
+ * The slow-AR layer's steps around the attention (the widening beside the path):
+ * a8_rmsnorm replaces serve/fast_kernels.py:49-69 (rmsnorm, kernel 30-46): for each of `rows` rows of
+ * width N (a multiple of 8, <= 2048), with residual != NULL: h = bf16(f32(x) + f32(residual)) is
+ * written to res_out (may alias residual) and normalised; else h = x. y = bf16(f32(w) *
+ * f32(bf16(f32(h) * rsqrt(mean(f32(h)^2) + eps)))). x, residual, y, res_out row strides sx, sr, sy, sro.
+ * a8_silu_mul replaces serve/fast_kernels.py:537-545 (silu_mul, kernel 526-534): gu [rows, 2I] row
+ * stride s_gu -> y [rows, I] row stride s_y, y = bf16(f32(bf16(g / (1 + exp(-g)))) * f32(u)) with
+ * g = gu[:, :I], u = gu[:, I:]; I a multiple of 8.
+ */
+int a8_rmsnorm(const void *x, int64_t sx, const void *residual, int64_t sr, const void *w, void *y, int64_t sy,
+               void *res_out, int64_t sro, int rows, int N, float eps, void *stream);
+int a8_silu_mul(const void *gu, int64_t s_gu, void *y, int64_t s_y, int rows, int I, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,7 +24,7 @@ def test_header_declares_the_entry_points():
                                          "a8_decode_attn", "a8_decode_choose", "a8_decode_attn_stream",
                                          "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn",
                                          "a8_decode_attn_flat", "a8_decode_choose_flat", "a8_store_decode_flat",
-                                         "a8_store_decode_split", "a8_prefix_copy"}
+                                         "a8_store_decode_split", "a8_prefix_copy", "a8_rmsnorm", "a8_silu_mul"}
 
 
 def test_library_exports_every_declared_symbol(a8):
@@ -266,3 +266,17 @@ def test_prefix_copy_rejects_before_launch(a8):
     assert lib.a8_prefix_copy(*_prefix_args(n=-1)) == -1
     for zero in (dict(n=0), dict(layers=0), dict(Lp=0)):
         assert lib.a8_prefix_copy(*_prefix_args(**zero)) == 0     # nothing to do, nothing launched
+
+
+def test_layer_ops_reject_before_launch(a8):
+    lib = a8.load_library()
+    args = dict(x=16, sx=896, r=None, sr=0, w=16, y=16, sy=896, ro=None, sro=0, rows=4, N=896, eps=1e-6, stream=None)
+    assert lib.a8_rmsnorm(*{**args, "N": 900}.values()) == -3               # not a multiple of 8
+    assert lib.a8_rmsnorm(*{**args, "N": 4096}.values()) == -3              # wider than 2048
+    assert lib.a8_rmsnorm(*{**args, "r": 16}.values()) == -1                # a residual needs res_out
+    assert lib.a8_rmsnorm(*{**args, "x": 24}.values()) == -2
+    assert lib.a8_rmsnorm(*{**args, "rows": 0}.values()) == 0
+    assert lib.a8_silu_mul(16, 2048, 16, 1024, 4, 1020, None) == -3
+    assert lib.a8_silu_mul(16, 2047, 16, 1024, 4, 1024, None) == -2
+    assert lib.a8_silu_mul(None, 2048, 16, 1024, 4, 1024, None) == -1
+    assert lib.a8_silu_mul(16, 2048, 16, 1024, 0, 1024, None) == 0

@@ -1,0 +1,182 @@
+"""The slow-AR layer around the attention path on the GPU (the widening beside the path): the rmsnorm and
+silu_mul kernels against the oracle (oracle/layer_ref.py, itself pinned to torch's rms_norm / silu), and the
+whole stack (SlowStack: GEMMs by hipBLASLt, this package's norms, activation and attention) against the
+oracle's _Stack.forward restatement, for the decode tick, the packed prefill and a captured graph."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import randn_bf16
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+NQ, NKV, HD = 14, 2, 64
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def lref():
+    from oracle import layer_ref
+    return layer_ref
+
+
+def _ulps(a, b):
+    return (a.view(torch.int16).int() - b.view(torch.int16).int()).abs()
+
+
+@pytest.mark.parametrize("N,rows", [(896, 1), (896, 192), (1024, 37), (2048, 5), (8, 3)])
+def test_rmsnorm_kernel(a8, lref, dev, N, rows):
+    say(f"case: rmsnorm N={N} rows={rows}")
+    g = torch.Generator().manual_seed(N + rows)
+    x, r = randn_bf16(g, rows, N, std=3.0), randn_bf16(g, rows, N)
+    w = (1 + 0.1 * torch.randn(N, generator=g)).to(BF)
+    want_y, want_h = lref.rmsnorm(x, w, 1e-6, residual=r)
+    xd, rd, wd = x.to(dev), r.to(dev), w.to(dev)
+    y, h = a8.rmsnorm(xd, wd, 1e-6, residual=rd)            # in place into the residual, as the reference
+    torch.cuda.synchronize()
+    assert h is rd and torch.equal(h.cpu().view(torch.int16), want_h.view(torch.int16))
+    d = _ulps(y.cpu(), want_y)
+    assert d.max() <= 1 and (d == 0).float().mean() >= 0.99
+    y0 = a8.rmsnorm(xd, wd, 1e-6)
+    d0 = _ulps(y0.cpu(), lref.rmsnorm(x, w, 1e-6)[0])
+    assert d0.max() <= 1 and (d0 == 0).float().mean() >= 0.99
+
+
+def test_rmsnorm_strided_and_separate_outputs(a8, lref, dev):
+    say("case: rmsnorm on row-strided views, res_out apart from the residual")
+    g = torch.Generator().manual_seed(71)
+    big = randn_bf16(g, 40, 1024).to(dev)
+    x = big[:, 64:64 + 896]
+    r = randn_bf16(g, 40, 896).to(dev)
+    r0 = r.clone()
+    w = (1 + 0.1 * torch.randn(896, generator=g)).to(BF).to(dev)
+    out = torch.zeros(40, 960, dtype=BF, device=dev)[:, :896]
+    ro = torch.empty(40, 896, dtype=BF, device=dev)
+    y, h = a8.rmsnorm(x, w, 1e-5, residual=r, out=out, res_out=ro)
+    torch.cuda.synchronize()
+    want_y, want_h = lref.rmsnorm(x.cpu(), w.cpu(), 1e-5, residual=r0.cpu())
+    assert torch.equal(r, r0) and h is ro and torch.equal(ro.cpu(), want_h)
+    assert _ulps(out.cpu(), want_y).max() <= 1
+
+
+@pytest.mark.parametrize("I,rows", [(4864, 192), (1024, 3), (8, 1)])
+def test_silu_mul_kernel(a8, lref, dev, I, rows):
+    say(f"case: silu_mul I={I} rows={rows}")
+    g = torch.Generator().manual_seed(I + rows)
+    gu = randn_bf16(g, rows, 2 * I, std=4.0)
+    y = a8.silu_mul(gu.to(dev))
+    torch.cuda.synchronize()
+    d = _ulps(y.cpu(), lref.silu_mul(gu))
+    assert d.max() <= 1 and (d == 0).float().mean() >= 0.99
+
+
+def _stack(a8, dev, n_layers, hidden, inter, rows, S, seed):
+    from importlib import import_module
+    ss = import_module(a8.__name__ + ".slow_stack")
+    layers, norm = ss.random_weights(n_layers, hidden, NQ, NKV, HD, inter, dev, seed=seed)
+    st = a8.SlowStack(layers, norm, NQ, NKV, HD, 1e-6, 10000.0, max_rows=max(rows, 64), cache_rows=rows + 1,
+                      cache_len=S, max_pos=S, dev=dev)
+    g = torch.Generator(device=dev).manual_seed(seed + 1)
+    st.kc_all.normal_(generator=g)
+    st.vc_all.normal_(generator=g)
+    return st, layers, norm
+
+
+def _cpu(layers):
+    return [{k: (v.cpu() if v is not None else None) for k, v in L.items()} for L in layers]
+
+
+def _close(got, want):
+    """(max-abs, mean-abs, max |want|). The bar for the stack: max-abs <= 2 % of max |h| and mean-abs <= 5e-3
+    -- rounding-order noise of bf16 GEMMs and fp32 sums (the oracle itself sits 0.6 % / 3.4e-3 from a float64
+    evaluation, tests/test_oracle.py); a wrong term or weight moves h by O(0.1 - 1)."""
+    err = (got.float().cpu() - want.float()).abs()
+    return err.max().item(), err.mean().item(), want.float().abs().max().item()
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_slow_stack_decode_tick(a8, ref, lref, dev, fuse):
+    """Two layers of the slow stack's decode tick (slot = row, rowmap off) against the oracle."""
+    say(f"case: slow stack decode tick, fused {fuse}")
+    n_layers, hidden, inter, b, S = 2, 896, 1024, 8, 512
+    st, layers, norm = _stack(a8, dev, n_layers, hidden, inter, b, S, seed=3)
+    g = torch.Generator().manual_seed(4)
+    x = randn_bf16(g, b, hidden)
+    lens = torch.randint(1, S + 1, (b,), generator=g).int()
+    pos, slot = lens - 1, torch.arange(b, dtype=torch.int32)
+    kc = [t.cpu() for t in st.kc]
+    vc = [t.cpu() for t in st.vc]
+    want = lref.slow_stack(x.clone(), pos, slot, lens, _cpu(layers), norm.cpu(), NQ, NKV, HD, 1e-6,
+                           st.attn.cos.cpu(), st.attn.sin.cpu(), kc, vc, rowmap=False)
+    got = st.forward(x.to(dev), pos.to(dev), slot.to(dev), lens.to(dev), rowmap=False, fuse=fuse)
+    torch.cuda.synchronize()
+    emax, emean, vmax = _close(got, want)
+    say(f"  max-abs {emax:.3e} mean-abs {emean:.3e} (max |h| {vmax:.2f})")
+    assert emax <= 0.02 * vmax and emean <= 5e-3
+    for i in range(n_layers):   # the new keys / values: the stores saw the same qkv rows up to GEMM rounding
+        dk = (st.kc[i].cpu().float() - kc[i].float()).abs().max().item()
+        assert dk <= 0.05, dk
+
+
+def test_slow_stack_prefill_and_graph(a8, ref, lref, dev):
+    """The packed prefill through the stack (two requests after a cached prefix) against the oracle, and a
+    decode tick captured as a graph replays to the eager bits."""
+    say("case: slow stack prefill + graph replay")
+    n_layers, hidden, inter, S = 2, 896, 512, 512
+    st, layers, norm = _stack(a8, dev, n_layers, hidden, inter, 4, S, seed=5)
+    g = torch.Generator().manual_seed(6)
+    ns, p0s, slots = [70, 130], [100, 37], [1, 3]
+    R = sum(ns)
+    x = randn_bf16(g, R, hidden)
+    pos = torch.cat([torch.arange(a, a + n) for a, n in zip(p0s, ns)]).int()
+    slot = torch.cat([torch.full((n,), s) for s, n in zip(slots, ns)]).int()
+    r0s = [int(v) for v in np.cumsum([0] + ns[:-1])]
+    kc = [t.cpu() for t in st.kc]
+    vc = [t.cpu() for t in st.vc]
+    want = lref.slow_stack(x.clone(), pos, slot, None, _cpu(layers), norm.cpu(), NQ, NKV, HD, 1e-6,
+                           st.attn.cos.cpu(), st.attn.sin.cpu(), kc, vc, plan=ref.prefill_plan(r0s, ns, slots, p0s))
+    plan = a8.PrefillPlan(r0s, ns, slots, p0s, dev)
+    got = st.forward(x.to(dev), pos.to(dev), slot.to(dev), None, plan=plan)
+    torch.cuda.synchronize()
+    emax, emean, vmax = _close(got, want)
+    say(f"  prefill max-abs {emax:.3e} mean-abs {emean:.3e} (max |h| {vmax:.2f})")
+    assert emax <= 0.02 * vmax and emean <= 5e-3
+    # decode tick as a graph: x is consumed (residual stream), so each run starts from a fresh copy
+    b = 4
+    xt = randn_bf16(g, b, hidden).to(dev)
+    lens = torch.tensor([S, 200, 1, 77], dtype=torch.int32, device=dev)
+    pos_t, slot_t = lens - 1, torch.arange(b, dtype=torch.int32, device=dev)
+    xbuf = xt.clone()
+    kc0, vc0 = st.kc_all.clone(), st.vc_all.clone()
+
+    def tick():
+        return st.forward(xbuf, pos_t, slot_t, lens, rowmap=False, fuse=True)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        tick()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    xbuf.copy_(xt)
+    with torch.cuda.graph(graph):
+        hg = tick()
+    outs = []
+    for run in range(3):
+        st.kc_all.copy_(kc0)
+        st.vc_all.copy_(vc0)
+        xbuf.copy_(xt)
+        if run == 0:
+            h = tick().clone()
+        else:
+            graph.replay()
+            h = hg.clone()
+        torch.cuda.synchronize()
+        outs.append(h.cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert torch.equal(outs[1].view(torch.int16), outs[2].view(torch.int16))

@@ -312,3 +312,114 @@ def test_algorithmic_counts(ref):
     """The byte / FLOP counts bench.py divides by: C3 per layer and a hand-checkable prefill case."""
     assert ref.decode_bytes([2048] * 192, 14, 2, 64) == 201_326_592 + 688_128 + 986_880
     assert ref.prefill_flops([2], [3], 14, 64) == 4 * 14 * 64 * (4 + 5)
+
+
+# ---- the slow-AR layer steps (oracle/layer_ref.py) ----
+
+@pytest.fixture(scope="module")
+def lref():
+    from oracle import layer_ref
+    return layer_ref
+
+
+def _ulps(a, b):
+    """bf16 distance in units in the last place (same-sign finite values)."""
+    return (a.view(torch.int16).int() - b.view(torch.int16).int()).abs()
+
+
+def test_layer_rmsnorm_against_library(lref):
+    g = torch.Generator().manual_seed(61)
+    for N in (896, 1024):
+        x, r = randn_bf16(g, 64, N, std=3.0), randn_bf16(g, 64, N)
+        w = (1 + 0.1 * torch.randn(N, generator=g)).to(torch.bfloat16)
+        y, h = lref.rmsnorm(x, w, 1e-6, residual=r)
+        h64 = x.double() + r.double()
+        assert torch.equal(h, h64.to(torch.bfloat16))                       # one rounding of the exact sum
+        xn = torch.nn.functional.rms_norm(h.double(), (N,), eps=1e-6).to(torch.bfloat16)
+        want = (w.double() * xn.double()).to(torch.bfloat16)
+        d = _ulps(y, want)
+        assert d.max() <= 1 and (d == 0).float().mean() >= 0.995
+        y0, h0 = lref.rmsnorm(x, w, 1e-6)                                     # no residual: h is x
+        assert h0 is x and _ulps(y0, (w.double() * torch.nn.functional.rms_norm(
+            x.double(), (N,), eps=1e-6).to(torch.bfloat16).double()).to(torch.bfloat16)).max() <= 1
+    # a planted mistake (the weight applied before the bf16 rounding of xn) is caught
+    x = randn_bf16(g, 64, 896, std=3.0)
+    w = (1 + 0.1 * torch.randn(896, generator=g)).to(torch.bfloat16)
+    wrong = (w.double() * torch.nn.functional.rms_norm(x.double(), (896,), eps=1e-6)).to(torch.bfloat16)
+    assert (_ulps(lref.rmsnorm(x, w, 1e-6)[0], wrong) > 0).float().mean() > 0.05
+
+
+def test_layer_silu_mul_against_library(lref):
+    g = torch.Generator().manual_seed(62)
+    gu = randn_bf16(g, 32, 2 * 1024, std=4.0)
+    y = lref.silu_mul(gu)
+    gs = torch.nn.functional.silu(gu[:, :1024].double()).to(torch.bfloat16)
+    want = (gs.double() * gu[:, 1024:].double()).to(torch.bfloat16)
+    d = _ulps(y, want)
+    assert y.shape == (32, 1024) and d.max() <= 1 and (d == 0).float().mean() >= 0.995
+
+
+def test_layer_linear_against_float64(lref):
+    g = torch.Generator().manual_seed(63)
+    x, w = randn_bf16(g, 16, 896), randn_bf16(g, 1152, 896)
+    want = (x.double() @ w.double().t()).to(torch.bfloat16)
+    d = _ulps(lref.linear(x, w), want)
+    assert d.max() <= 1 and (d == 0).float().mean() >= 0.99
+
+
+def test_layer_slow_stack_against_float64_unrolled(ref, lref):
+    """One decode layer of the stack against a float64 evaluation written out step by step (textbook RMSNorm,
+    GEMMs, RoPE on the rotate_half layout, softmax attention over the cache with the new key, SwiGLU, two
+    residual adds, the final norm): agreement to bf16 rounding noise, and a dropped residual is caught."""
+    g = torch.Generator().manual_seed(64)
+    nq, nkv, hd, hidden, inter, S, b = 14, 2, 64, 896, 256, 64, 3
+    W = (nq + 2 * nkv) * hd
+
+    def lin(n, k):
+        return (torch.randn(n, k, generator=g) / k ** 0.5).to(torch.bfloat16)
+
+    L = dict(wqkv=lin(W, hidden), bqkv=randn_bf16(g, W, std=0.02), wo=lin(hidden, nq * hd), w13=lin(2 * inter, hidden),
+             w2=lin(hidden, inter), ln1=(1 + 0.05 * torch.randn(hidden, generator=g)).to(torch.bfloat16),
+             ln2=(1 + 0.05 * torch.randn(hidden, generator=g)).to(torch.bfloat16))
+    norm = (1 + 0.05 * torch.randn(hidden, generator=g)).to(torch.bfloat16)
+    x = randn_bf16(g, b, hidden)
+    kc, vc = randn_bf16(g, b, nkv, S, hd), randn_bf16(g, b, nkv, S, hd)
+    pos = torch.tensor([5, 40, 63], dtype=torch.int32)
+    slot = torch.arange(b, dtype=torch.int32)
+    lens = pos + 1
+    cos, sin = ref.rope_tables(10000.0, hd, S)
+    got = lref.slow_stack(x.clone(), pos, slot, lens, [L], norm, nq, nkv, hd, 1e-6, cos, sin, [kc.clone()],
+                          [vc.clone()])
+
+    def rms(v, w):
+        return torch.nn.functional.rms_norm(v, (hidden,), eps=1e-6) * w.double()
+
+    def rope(t, p):                      # rotate_half on [heads, hd] at position p
+        c, s_ = cos[p].double(), sin[p].double()
+        rot = torch.cat([-t[:, hd // 2:], t[:, :hd // 2]], -1)
+        return t * c + rot * s_
+
+    out = torch.empty(b, hidden, dtype=torch.float64)
+    for r in range(b):
+        p = int(pos[r])
+        h0 = rms(x[r].double(), L["ln1"])
+        qkv = L["wqkv"].double() @ h0 + L["bqkv"].double()
+        q = rope(qkv[:nq * hd].view(nq, hd), p)
+        k_new = rope(qkv[nq * hd:(nq + nkv) * hd].view(nkv, hd), p)
+        v_new = qkv[(nq + nkv) * hd:].view(nkv, hd)
+        K, V = kc[r].double().clone(), vc[r].double().clone()
+        K[:, p], V[:, p] = k_new, v_new
+        o = torch.empty(nq, hd, dtype=torch.float64)
+        for hq in range(nq):
+            kh = hq // (nq // nkv)
+            s_ = K[kh, :p + 1] @ q[hq] / hd ** 0.5
+            o[hq] = torch.softmax(s_, 0) @ V[kh, :p + 1]
+        res1 = x[r].double() + L["wo"].double() @ o.reshape(-1)
+        h1 = rms(res1, L["ln2"])
+        gu = L["w13"].double() @ h1
+        m = L["w2"].double() @ (torch.nn.functional.silu(gu[:inter]) * gu[inter:])
+        out[r] = rms(res1 + m, norm)
+    err = (got.double() - out).abs().max().item()
+    assert err <= 0.02 * out.abs().max().item(), err   # measured 0.6 % (bf16 roundings of the stack)
+    wrong = torch.stack([rms(out[r] * 0 + x[r].double(), norm) for r in range(b)])   # residual stream not updated
+    assert (got.double() - wrong).abs().max().item() > 10 * err
