@@ -212,6 +212,31 @@ def per_config(a8, torch, dev, steps):
     del g, st, qkvs, outs
     torch.cuda.empty_cache()
 
+    # The whole slow-AR decode step (beside configs C1-C5): 24 layers x (rmsnorm, qkv GEMM, fused store + decode,
+    # o GEMM, residual + rmsnorm, w13 GEMM, silu_mul, w2 GEMM, residual + rmsnorm) over 192 slots at KV 2048,
+    # one graph. Synthetic weights of the slow AR's shapes (width 896; the MLP width 4864 is an assumption:
+    # the checkpoint is absent offline); GEMMs are hipBLASLt through torch.matmul.
+    from importlib import import_module
+    ss = import_module(a8.__name__ + ".slow_stack")
+    b, S, layers, hidden, inter = 192, 2048, LAYERS, 896, 4864
+    wts, norm = ss.random_weights(layers, hidden, NQ, NKV, HD, inter, dev, seed=11)
+    st = a8.SlowStack(wts, norm, NQ, NKV, HD, 1e-6, 10000.0, max_rows=max(16 * b, 8192), cache_rows=b + 1,
+                      cache_len=S, max_pos=S, dev=dev)
+    st.kc_all.normal_(generator=gen)
+    st.vc_all.normal_(generator=gen)
+    x0 = randn(b, hidden)
+    xbuf = x0.clone()
+    lens_d = torch.full((b,), S, dtype=torch.int32, device=dev)
+    pos, slot = lens_d - 1, torch.arange(b, dtype=torch.int32, device=dev)
+    g = capture(torch, lambda: st.forward(xbuf, pos, slot, lens_d, rowmap=False, fuse=True))
+    us = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
+    wbytes = layers * 2 * (hidden * (NQ + 2 * NKV) * HD + hidden * NQ * HD + hidden * 2 * inter + inter * hidden)
+    res["slow_ar_step"] = {"us_per_step": round(us, 1), "us_per_layer": round(us / layers, 2), "rows": b, "kv_len": S,
+                           "hidden": hidden, "inter": inter, "weight_bytes": wbytes,
+                           "note": "the full slow-AR decode step around the attention path; synthetic weights"}
+    del g, st, wts, xbuf
+    torch.cuda.empty_cache()
+
     # Codec window transformer (beside configs C1-C5): the same kernels on a 128-position
     # ring with caches that are views into a per-row byte arena (fast_engine.py:337-341, 368-387, 470-477),
     # 192 rows with a full window (lens 128, positions past the wrap). The codec's own head shape needs the
