@@ -476,3 +476,68 @@ def silu_mul(gu, out=None):
                                  _lib.stream_of(g2))
     _lib.check(st, "silu_mul")
     return y
+
+
+_F16 = torch.float16
+
+
+def conv_cl(xin, w, bias, TR, taps, dil, ph, out, res=None, f16acc=True, cfg=None, snake=None):
+    """Channels-last causal / transposed conv as an implicit GEMM (fast_kernels.py:600-623, kernel 551-597):
+    xin [B, Tin, Cin] fp16; w [ph, taps, Cin, Cout_pad] fp16; out [B, TR*ph, >=Cout] with Cout =
+    out.shape[-1]: out[b, t*ph + p] = bias + sum_j xin[b, t + j*dil] @ w[p, j] (+ res[b, t*ph + p]).
+    snake = (alpha, 1/(alpha+eps)) fp32 [Cin] applies x + ib sin(alpha x)^2 to xin on the load. Accumulation
+    is fp32 (f16acc, the reference's fp16 slice sums, and cfg, its Triton tile choice, are accepted and
+    unused)."""
+    for name, t, d in (("xin", xin, 3), ("w", w, 4), ("out", out, 3)):
+        _need(isinstance(t, torch.Tensor) and t.dtype == _F16, f"{name} must be a float16 tensor", TypeError)
+        _need(t.dim() == d and t.stride(-1) == 1, f"{name} must have {d} dims with a contiguous last dim")
+    B, Tin, Cin = xin.shape
+    Cout = out.shape[-1]
+    _need(w.shape[0] == ph and w.shape[1] == taps and w.shape[2] == Cin and w.shape[3] >= Cout,
+          f"w {tuple(w.shape)} does not match [{ph}, {taps}, {Cin}, >={Cout}]")
+    _need(out.shape[0] == B and out.shape[1] >= TR * ph, f"out {tuple(out.shape)} does not hold [{B}, {TR * ph}, ...]")
+    if bias is not None:
+        _need(bias.dtype == _F16 and bias.dim() == 1 and bias.shape[0] >= Cout and bias.is_contiguous(),
+              "bias must be a contiguous float16 vector of >= Cout entries")
+    if res is not None:
+        _need(res.dtype == _F16 and res.dim() == 3 and res.stride(-1) == 1 and res.shape[0] == B and
+              res.shape[1] >= TR * ph and res.shape[2] >= Cout, "res must be float16 like out")
+    sa = sib = None
+    if snake is not None:
+        sa, sib = snake
+        _need(sa.dtype == torch.float32 and sib.dtype == torch.float32 and sa.is_contiguous() and sib.is_contiguous()
+              and sa.numel() >= Cin and sib.numel() >= Cin, "snake must be two contiguous float32 [Cin] vectors")
+    _check_device(xin=xin, w=w, out=out, bias=bias, res=res, snake_a=sa, snake_ib=sib)
+    st = _lib.load().a8_conv_cl(
+        xin.data_ptr(), xin.stride(0), xin.stride(1), w.data_ptr(), w.stride(0), w.stride(1), w.stride(2),
+        w.shape[3], bias.data_ptr() if bias is not None else None, res.data_ptr() if res is not None else None,
+        res.stride(0) if res is not None else 0, res.stride(1) if res is not None else 0, out.data_ptr(),
+        out.stride(0), out.stride(1), sa.data_ptr() if sa is not None else None,
+        sib.data_ptr() if sib is not None else None, B, Tin, TR, Cin, Cout, taps, dil, ph, _lib.stream_of(xin))
+    _lib.check(st, "conv_cl")
+    return out
+
+
+def snake_cat(x, state, a, ib, out):
+    """x [B, T, C] (raw) and state [>=B, CTX, C] (activated context, or None) -> out [B, CTX+T, C] =
+    concat(state, snake(x)) along time (fast_kernels.py:718-729, kernel 695-715); a / ib None: no snake."""
+    _need(isinstance(x, torch.Tensor) and x.dim() == 3 and x.stride(-1) == 1, "x must be [B, T, C], last dim contiguous")
+    B, T, C = x.shape
+    CTX = state.shape[1] if state is not None else 0
+    _need(out.dim() == 3 and out.shape[0] == B and out.shape[1] >= CTX + T and out.shape[2] == C and
+          out.stride(-1) == 1 and out.dtype == x.dtype, "out must be [B, CTX+T, C] like x")
+    if state is not None:
+        _need(state.dtype == x.dtype and state.shape[0] >= B and state.shape[2] == C and state.stride(-1) == 1,
+              "state must be [>=B, CTX, C] like x")
+    if a is not None:
+        _need(a.dtype == torch.float32 and ib.dtype == torch.float32 and a.is_contiguous() and ib.is_contiguous()
+              and a.numel() >= C and ib.numel() >= C, "a / ib must be contiguous float32 [C] vectors")
+    _need(x.dtype == _F16, "x must be float16", TypeError)
+    _check_device(x=x, state=state, out=out, a=a, ib=ib)
+    st = _lib.load().a8_snake_cat(
+        x.data_ptr(), x.stride(0), x.stride(1), state.data_ptr() if state is not None else None,
+        state.stride(0) if state is not None else 0, state.stride(1) if state is not None else 0,
+        a.data_ptr() if a is not None else None, ib.data_ptr() if ib is not None else None, out.data_ptr(),
+        out.stride(0), out.stride(1), B, T, CTX, C, _lib.stream_of(out))
+    _lib.check(st, "snake_cat")
+    return out

@@ -1,0 +1,148 @@
+"""The streaming codec decoder's convolution stack (reference serve/fast_engine.py:178-310: _CLConv, _CLDecoder)
+on this package's conv kernels: channels-last fp16, one frame of work per frame, per-row causal state.
+
+CLConv packs one causal Conv1d [Cout, Cin, K] (stride 1, dilation d) or one causal ConvTranspose1d
+[Cin, Cout, 2s] (stride s, right crop s) into the weight layout conv_cl reads, [phases, taps, Cin, Cout_pad]
+with Cout_pad = max(16, Cout) (fast_engine.py:183-206):
+    Conv1d:           one phase, taps j = 0..K-1 at input rows t + j*d, ctx = (K-1)*d rows of state;
+    ConvTranspose1d:  s phases, two taps: tap 0 reads the previous input frame with w[:, :, p + s], tap 1 the
+                      current one with w[:, :, p]; ctx = 1 row of state.
+Its call (fast_engine.py:218-233): without state the snake runs on the conv's loads; with state, snake_cat
+builds [state, snake(x)] and conv_cl reads it, and the state keeps the last ctx activated rows.
+
+CLDecoder (fast_engine.py:276-310): conv_in, then per block [snake + transposed conv, 3 residual units
+(snake, dilated conv k, snake, 1x1 conv, + input)], snake + conv_out (one channel), tanh. The reference's
+opt-in fused residual unit (_FusedRU, off unless TTS_VOC_FUSED_RU names a width) computes the same unit; here a
+residual unit is always the two convs, the reference's default.
+
+The checkpoint's decoder (its modeling file and weights) is absent offline: `decoder_weights` draws a synthetic
+decoder of a stated shape (default: a DAC-style 44.1 kHz decoder, 1024 -> 1536 channels, strides 8, 8, 4, 2,
+kernel 7, dilations 1, 3, 9), with the reference's tensor layouts."""
+from __future__ import annotations
+
+import torch
+
+from .fast_kernels import conv_cl, snake_cat
+
+F16 = torch.float16
+
+
+def pack_conv(w, trans=False, stride=1):
+    """(W [ph, taps, Cin, max(16, Cout)] fp16, taps, ph) from a Conv1d weight [Cout, Cin, K] or a
+    ConvTranspose1d weight [Cin, Cout, 2*stride] (fast_engine.py:186-206)."""
+    w = w.detach().float()
+    if trans:
+        Cin, Cout, K = w.shape
+        if K != 2 * stride:
+            raise ValueError(f"transposed conv kernel {K} must be twice its stride {stride}")
+        W = torch.stack([torch.stack([w[:, :, p + stride], w[:, :, p]]) for p in range(stride)])
+        taps, ph = 2, stride
+    else:
+        Cout, Cin, K = w.shape
+        W = w.permute(2, 1, 0).unsqueeze(0)
+        taps, ph = K, 1
+    Wp = torch.zeros(*W.shape[:-1], max(16, Cout), device=w.device)
+    Wp[..., :Cout] = W
+    return Wp.to(F16).contiguous(), taps, ph
+
+
+class CLConv:
+    """One conv of the decoder with its packed weights, bias, snake vectors and per-row state
+    (_CLConv, fast_engine.py:178-233). weight / bias are the module's tensors; alpha the snake's [Cin] (or
+    None); dilation for a Conv1d, stride for a ConvTranspose1d (trans=True)."""
+
+    def __init__(self, weight, bias, Bmax, dev, states, alpha=None, trans=False, stride=1, dilation=1):
+        self.W, self.taps, self.ph = pack_conv(weight.to(dev), trans, stride)
+        self.dil = 1 if trans else int(dilation)
+        self.ctx = 1 if trans else (self.taps - 1) * self.dil
+        self.Cin, self.Cout = (weight.shape[0], weight.shape[1]) if trans else (weight.shape[1], weight.shape[0])
+        self.bias = bias.detach().to(dev, F16).contiguous() if bias is not None else None
+        self.a = self.ib = None
+        if alpha is not None:
+            al = alpha.detach().to(dev, torch.float32).reshape(-1)
+            self.a = al.contiguous()
+            self.ib = (1.0 / (al + 1e-9)).contiguous()
+        self.state = None
+        if self.ctx > 0:
+            self.state = torch.zeros(Bmax, self.ctx, self.Cin, dtype=F16, device=dev)
+            states.append(self.state)
+
+    def __call__(self, x, b, res=None):
+        """x [b, T, Cin] fp16 (pre-activation) -> [b, T*ph, Cout] fp16."""
+        T = x.shape[1]
+        y = torch.empty(b, T * self.ph, self.Cout, dtype=F16, device=x.device)
+        if self.state is None:
+            snake = (self.a, self.ib) if self.a is not None else None
+            conv_cl(x.contiguous(), self.W, self.bias, T, self.taps, self.dil, self.ph, y, res=res, snake=snake)
+            return y
+        xin = torch.empty(b, self.ctx + T, self.Cin, dtype=F16, device=x.device)
+        snake_cat(x, self.state[:b], self.a, self.ib, xin)
+        conv_cl(xin, self.W, self.bias, T, self.taps, self.dil, self.ph, y, res=res)
+        self.state[:b].copy_(xin[:, T:])
+        return y
+
+
+def decoder_weights(cin=1024, ch=1536, rates=(8, 8, 4, 2), k=7, dils=(1, 3, 9), dev="cpu", seed=0):
+    """A synthetic decoder in the modules' own layouts: conv_in (w [ch, cin, k], b), blocks of (alpha, transposed
+    w [C, C/2, 2s], b, stride, units of (alpha1, w1 [C/2, C/2, k], b1, dil, alpha2, w2 [C/2, C/2, 1], b2)),
+    final (alpha, w [1, C_last, k], b). Weights ~ N(0, 1/fan_in), snake alphas ~ U[0.5, 1.5]."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+
+    def conv(co, ci, kk, fan):
+        return (torch.randn(co, ci, kk, generator=g) / fan ** 0.5).to(dev), (0.02 * torch.randn(co, generator=g)).to(dev)
+
+    def alpha(c):
+        return (0.5 + torch.rand(c, generator=g)).to(dev)
+
+    wts = {"conv_in": conv(ch, cin, k, cin * k), "blocks": []}
+    C = ch
+    for s in rates:
+        tw = (torch.randn(C, C // 2, 2 * s, generator=g) / (C * 2) ** 0.5).to(dev)
+        tb = (0.02 * torch.randn(C // 2, generator=g)).to(dev)
+        a0 = alpha(C)
+        C //= 2
+        units = []
+        for d in dils:
+            w1, b1 = conv(C, C, k, C * k)
+            w2, b2 = conv(C, C, 1, C)
+            units.append((alpha(C), w1, b1, d, alpha(C), w2, b2))
+        wts["blocks"].append((a0, tw, tb, s, units))
+    wf, bf = conv(1, C, k, C * k)
+    wts["final"] = (alpha(C), wf, bf)
+    return wts
+
+
+class CLDecoder:
+    """The stateful channels-last decoder (_CLDecoder, fast_engine.py:276-310) over `decoder_weights`-shaped
+    weights; every conv's state is registered in `states` (per row, for snapshots / row resets)."""
+
+    def __init__(self, wts, Bmax, dev, states=None):
+        self.states = states if states is not None else []
+        S = self.states
+        w, b = wts["conv_in"]
+        self.dec_in = CLConv(w, b, Bmax, dev, S, dilation=1)
+        self.blocks = []
+        for a0, tw, tb, s, units in wts["blocks"]:
+            tc = CLConv(tw, tb, Bmax, dev, S, alpha=a0, trans=True, stride=s)
+            us = [(CLConv(w1, b1, Bmax, dev, S, alpha=a1, dilation=d), CLConv(w2, b2, Bmax, dev, S, alpha=a2))
+                  for a1, w1, b1, d, a2, w2, b2 in units]
+            self.blocks.append((tc, us))
+        af, wf, bf = wts["final"]
+        self.final = CLConv(wf, bf, Bmax, dev, S, alpha=af)
+        self.up = 1
+        for _, _, _, s, _ in wts["blocks"]:
+            self.up *= s
+
+    def reset_rows(self, rows):
+        """Zero the state of the given rows (a new utterance starts from silence)."""
+        for st in self.states:
+            st[rows] = 0
+
+    def __call__(self, x, b):
+        """x [b, T, cin] -> wav [b, T * up] float32 (tanh)."""
+        x = self.dec_in(x.to(F16).contiguous(), b)
+        for tc, units in self.blocks:
+            x = tc(x, b)
+            for c1, c2 in units:
+                x = c2(c1(x, b), b, res=x)
+        return self.final(x, b)[..., 0].float().tanh()

@@ -270,6 +270,39 @@ def per_config(a8, torch, dev, steps):
     del g, st, qkv, outs, arena
     torch.cuda.empty_cache()
 
+    # Streaming codec decoder (beside configs C1-C5): one codec frame (4 decoder input rows after the x4
+    # upsample) for 192 rows through the channels-last conv stack, one graph. The checkpoint's decoder is absent
+    # offline: a synthetic DAC-style decoder (1024 -> 1536 channels, strides 8, 8, 4, 2, kernel 7, dilations
+    # 1, 3, 9) stands in. FLOPs count each conv's multiply-adds (2 B T_out Cout taps Cin).
+    voc = import_module(a8.__name__ + ".vocoder")
+    b, T = 192, 4
+    wts = voc.decoder_weights(dev=dev, seed=21)
+    dec = voc.CLDecoder(wts, b, dev)
+    xf = torch.randn(b, T, 1024, generator=gen, device=dev).to(torch.float16)
+    g = capture(torch, lambda: dec(xf, b))
+    us = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
+    flops, t, C = 2 * b * T * 1536 * 7 * 1024, T, 1536
+    for _, _, _, s, units in wts["blocks"]:
+        flops += 2 * b * t * s * (C // 2) * 2 * C
+        t, C = t * s, C // 2
+        flops += len(units) * 2 * b * t * C * C * 8
+    flops += 2 * b * t * 1 * 7 * C
+    del g
+    # the dominant launch: a residual unit's k=7 conv at the 192-channel block (1024 output rows per row)
+    c1 = dec.blocks[2][1][0][0]
+    xr = torch.randn(b, 1024, 192, generator=gen, device=dev).to(torch.float16)
+    g = capture(torch, lambda: c1(xr, b))
+    us_c = time_median(torch, g, steps, 10) * 1e3
+    fl_c = 2 * b * 1024 * 192 * 7 * 192
+    res["vocoder_frame"] = {"us_per_frame": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
+                            "frac_fp16_mfma": round(flops / us / 1e6 / 2500.0, 4), "rows": b, "flops": flops,
+                            "conv_k7_c192": {"us": round(us_c, 1), "TFLOP/s": round(fl_c / us_c / 1e6, 1),
+                                             "note": "snake_cat + conv_cl + state copy, M = 196608, N = 192, "
+                                                     "K = 1344"},
+                            "note": "one frame of the streaming decoder; synthetic DAC-style weights"}
+    del g, dec, wts, xf, xr
+    torch.cuda.empty_cache()
+
     # C4: 64 requests, n ~ U[40, 400], after a 300-position voice prefix; store + packed prefill per layer
     ns = torch.randint(40, 401, (64,), generator=torch.Generator().manual_seed(0)).tolist()
     p0, nreq, layers = 300, 64, LAYERS

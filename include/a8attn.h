@@ -287,6 +287,25 @@ int a8_rmsnorm(const void *x, int64_t sx, const void *residual, int64_t sr, cons
                void *res_out, int64_t sro, int rows, int N, float eps, void *stream);
 int a8_silu_mul(const void *gu, int64_t s_gu, void *y, int64_t s_y, int rows, int I, void *stream);
 
+/*
+ * The streaming vocoder's channels-last convolutions (the codec decoder's default conv path,
+ * serve/fast_engine.py:218-233), fp16 storage:
+ * a8_conv_cl replaces serve/fast_kernels.py:600-623 (conv_cl, kernel 551-597): for rows (b, t), t < TR,
+ *   y[b, t*ph + p, n] = bias[n] + sum_{j < taps} sum_k x[b, t + j*dil, k] w[p, j, k, n] (+ res[b, t*ph + p, n]),
+ *   n < Cout; x [B, Tin, Cin] (Tin >= TR + (taps-1) dil, Cin a multiple of 8), w [ph, taps, Cin, cout_w]
+ *   (cout_w >= Cout, a multiple of 8; last dim contiguous), bias [Cout] or NULL, res like y or NULL.
+ *   snake_a / snake_ib (fp32 [Cin]) or NULL: x -> x + ib sin(a x)^2 (fp16) on the load. fp32 accumulation.
+ * a8_snake_cat replaces serve/fast_kernels.py:718-729 (snake_cat, kernel 695-715):
+ *   y[b] = concat(state[b] (CTX rows), snake(x[b]) (T rows)), C a multiple of 8; a / ib NULL: no snake.
+ */
+int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void *w, int64_t s_wp, int64_t s_wt, int64_t s_wc,
+               int cout_w, const void *bias, const void *res, int64_t s_rb, int64_t s_rt, void *y, int64_t s_yb,
+               int64_t s_yt, const float *snake_a, const float *snake_ib, int B, int Tin, int TR, int Cin, int Cout,
+               int taps, int dil, int ph, void *stream);
+int a8_snake_cat(const void *x, int64_t s_xb, int64_t s_xt, const void *state, int64_t s_sb, int64_t s_st,
+                 const float *a, const float *ib, void *y, int64_t s_yb, int64_t s_yt, int B, int T, int CTX, int C,
+                 void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,90 @@
+"""The streaming vocoder's channels-last convolutions on the GPU (conv_cl, snake_cat) against the oracle
+(oracle/conv_ref.py, pinned to torch's conv1d / conv_transpose1d): the codec decoder's conv shapes (input
+conv, the stride-s transposed convs as phases, residual units' dilated k=7 conv and 1x1 conv with the snake on
+the load and the residual, the one-channel output conv), ragged sizes, and the decoder's call pattern
+(snake_cat into the conv, the state refreshed from the concatenated input)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+F16 = torch.float16
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def cref():
+    from oracle import conv_ref
+    return conv_ref
+
+
+def _close(got, want):
+    """fp16 results: within one fp16 ulp of the oracle (fp32 sums in another order), or 1e-3 of the output
+    scale where a sum cancels."""
+    g, w = got.cpu().float(), want.float()
+    ulp = (w.abs() * 2 ** -10).clamp(min=2 ** -24)
+    scale = w.abs().max().item()
+    return bool((((g - w).abs() <= ulp * 1.01) | ((g - w).abs() <= 1e-3 * scale)).all())
+
+
+@pytest.mark.parametrize("B,T,Cin,Cout,cw,taps,dil,ph,bias,res,snake", [
+    (8, 4, 1024, 768, 768, 7, 1, 1, True, False, False),      # input conv
+    (8, 4, 768, 384, 384, 2, 1, 8, True, False, False),       # stride-8 transposed conv as 8 phases
+    (8, 64, 96, 96, 96, 7, 9, 1, True, False, False),         # residual unit's dilated conv (after snake_cat)
+    (8, 64, 96, 96, 96, 1, 1, 1, True, True, True),           # residual unit's 1x1 conv, snake on load, + input
+    (8, 128, 96, 1, 16, 7, 1, 1, True, False, False),         # one-channel output conv (padded weights)
+    (3, 5, 8, 24, 32, 3, 2, 3, False, True, True),            # ragged: one k chunk, Cout 24, 15 rows
+])
+def test_conv_cl_shapes(a8, cref, dev, B, T, Cin, Cout, cw, taps, dil, ph, bias, res, snake):
+    say(f"case: conv_cl B={B} T={T} Cin={Cin} Cout={Cout} taps={taps} dil={dil} ph={ph} bias={bias} res={res} "
+        f"snake={snake}")
+    g = torch.Generator().manual_seed(B + T + Cin + Cout + taps)
+    Tin = T + (taps - 1) * dil
+    x = torch.randn(B, Tin, Cin, generator=g).to(F16)
+    w = (torch.randn(ph, taps, Cin, cw, generator=g) / (taps * Cin) ** 0.5).to(F16)
+    bv = torch.randn(cw, generator=g).to(F16) if bias else None
+    rv = torch.randn(B, T * ph, Cout, generator=g).to(F16) if res else None
+    ab = None
+    if snake:
+        a = (torch.rand(Cin, generator=g) + 0.5)
+        ab = (a, 1.0 / (a + 1e-9))
+    want = cref.conv_cl(x, w, bv, T, taps, dil, ph, Cout, res=rv, snake_ab=ab)
+    out = torch.full((B, T * ph, Cout), 7.0, dtype=F16, device=dev)
+    a8.conv_cl(x.to(dev), w.to(dev), bv.to(dev) if bias else None, T, taps, dil, ph, out,
+               res=rv.to(dev) if res else None, snake=(ab[0].to(dev), ab[1].to(dev)) if snake else None)
+    torch.cuda.synchronize()
+    assert _close(out, want)
+
+
+def test_snake_cat_and_decoder_call_pattern(a8, cref, dev):
+    """_CLConv.__call__ (fast_engine.py:218-233) for a context conv, frame after frame: snake_cat(x, state) into
+    the conv's input, conv_cl over it, the state refreshed from the input's last ctx rows; against the oracle
+    doing the same."""
+    say("case: snake_cat + conv_cl streaming over 5 chunks")
+    g = torch.Generator().manual_seed(91)
+    B, C, Cout, taps, dil = 4, 96, 96, 7, 3
+    ctx = (taps - 1) * dil
+    w = (torch.randn(1, taps, C, Cout, generator=g) / (taps * C) ** 0.5).to(F16)
+    bias = torch.randn(Cout, generator=g).to(F16)
+    a = torch.rand(C, generator=g) + 0.5
+    ib = 1.0 / (a + 1e-9)
+    st_d = torch.zeros(B, ctx, C, dtype=F16, device=dev)
+    wd, bd, ad, ibd = w.to(dev), bias.to(dev), a.to(dev), ib.to(dev)
+    for T in (1, 5, 32, 2, 64):
+        x = torch.randn(B, T, C, generator=g).to(F16)
+        st_h = st_d.cpu()                   # the oracle continues from the device's state (snake rows may differ
+        xin = torch.empty(B, ctx + T, C, dtype=F16, device=dev)   # from the oracle's by one fp16 ulp)
+        a8.snake_cat(x.to(dev), st_d, ad, ibd, xin)
+        y = torch.empty(B, T, Cout, dtype=F16, device=dev)
+        a8.conv_cl(xin, wd, bd, T, taps, dil, 1, y)
+        st_d.copy_(xin[:, T:])
+        xin_h = cref.snake_cat(x, st_h, a, ib)
+        torch.cuda.synchronize()
+        assert torch.equal(xin.cpu()[:, :ctx], st_h)                          # the state rows move verbatim
+        assert _close(xin[:, ctx:], xin_h[:, ctx:])                           # the snake: <= 1 fp16 ulp
+        assert _close(y, cref.conv_cl(xin.cpu(), w, bias, T, taps, dil, 1, Cout))
+        assert _close(y, cref.conv_cl(xin_h, w, bias, T, taps, dil, 1, Cout))

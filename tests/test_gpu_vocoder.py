@@ -1,0 +1,69 @@
+"""The streaming channels-last decoder (vocoder.CLDecoder on conv_cl / snake_cat) against the oracle's
+whole-utterance decode (oracle/conv_ref.decoder: torch conv1d / conv_transpose1d, float64): streaming frame
+chunks from zero state reproduce the whole-utterance decode (fast_engine.py:24-25), and rows are independent:
+resetting one row's state restarts that row alone (work/voc_check.py's row independence)."""
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def _small(dev):
+    voc = importlib.import_module("audio8-turbo-engine_amd.vocoder")
+    return voc, voc.decoder_weights(cin=64, ch=128, rates=(4, 2), k=7, dils=(1, 3, 9), dev="cpu", seed=3)
+
+
+def test_streaming_decoder_matches_whole_utterance(dev):
+    from oracle import conv_ref
+    say("case: CLDecoder 64->128 ch, rates 4,2, chunks 1,2,3,1 x 3 rows")
+    voc, wts = _small(dev)
+    wd = {"conv_in": tuple(t.to(dev) for t in wts["conv_in"]),
+          "blocks": [(a.to(dev), w.to(dev), b.to(dev), s, [tuple(t.to(dev) if torch.is_tensor(t) else t for t in u)
+                                                          for u in us]) for a, w, b, s, us in wts["blocks"]],
+          "final": tuple(t.to(dev) for t in wts["final"])}
+    dec = voc.CLDecoder(wd, 4, dev)
+    g = torch.Generator().manual_seed(8)
+    B, chunks = 3, (1, 2, 3, 1)
+    x = torch.randn(B, sum(chunks), 64, generator=g)
+    outs, t0 = [], 0
+    for T in chunks:
+        outs.append(dec(x[:, t0:t0 + T].to(dev), B))
+        t0 += T
+    got = torch.cat(outs, 1).cpu().double()
+    want = conv_ref.decoder(wts, x)
+    torch.cuda.synchronize()
+    assert got.shape == want.shape == (B, sum(chunks) * 8)
+    err = (got - want).abs()
+    say(f"max err {err.max().item():.2e} mean {err.mean().item():.2e} scale {want.abs().max().item():.3f}")
+    assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
+
+
+def test_rows_are_independent(dev):
+    say("case: CLDecoder row reset, 3 rows")
+    voc, wts = _small(dev)
+    wd = {"conv_in": tuple(t.to(dev) for t in wts["conv_in"]),
+          "blocks": [(a.to(dev), w.to(dev), b.to(dev), s, [tuple(t.to(dev) if torch.is_tensor(t) else t for t in u)
+                                                          for u in us]) for a, w, b, s, us in wts["blocks"]],
+          "final": tuple(t.to(dev) for t in wts["final"])}
+    g = torch.Generator().manual_seed(9)
+    x1, x2 = torch.randn(3, 3, 64, generator=g).to(dev), torch.randn(3, 2, 64, generator=g).to(dev)
+    dec = voc.CLDecoder(wd, 3, dev)
+    dec(x1, 3)
+    dec.reset_rows(torch.tensor([1], device=dev))
+    y = dec(x2, 3)
+    fresh = voc.CLDecoder(wd, 3, dev)(x2, 3)                  # every row from zero state
+    cont = voc.CLDecoder(wd, 3, dev)
+    cont(x1, 3)
+    yc = cont(x2, 3)                                            # every row continuing
+    torch.cuda.synchronize()
+    assert torch.equal(y[1], fresh[1])
+    assert torch.equal(y[0], yc[0]) and torch.equal(y[2], yc[2])
+    assert not torch.equal(y[0], fresh[0])

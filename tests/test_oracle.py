@@ -423,3 +423,102 @@ def test_layer_slow_stack_against_float64_unrolled(ref, lref):
     assert err <= 0.02 * out.abs().max().item(), err   # measured 0.6 % (bf16 roundings of the stack)
     wrong = torch.stack([rms(out[r] * 0 + x[r].double(), norm) for r in range(b)])   # residual stream not updated
     assert (got.double() - wrong).abs().max().item() > 10 * err
+
+
+# ---- the vocoder's channels-last convolutions (oracle/conv_ref.py) ----
+
+@pytest.fixture(scope="module")
+def cref():
+    from oracle import conv_ref
+    return conv_ref
+
+
+def test_conv_cl_against_conv1d(cref):
+    """ph = 1: the causal dilated conv over a context-padded input equals torch's conv1d (cross-correlation)
+    in float64 up to the one fp16 rounding; with bias, residual and the snake on the load."""
+    g = torch.Generator().manual_seed(71)
+    B, T, Cin, Cout, taps, dil = 3, 11, 32, 24, 7, 3
+    Tin = T + (taps - 1) * dil
+    x = (torch.randn(B, Tin, Cin, generator=g)).to(torch.float16)
+    w = (torch.randn(1, taps, Cin, 32, generator=g) / 10).to(torch.float16)
+    bias = torch.randn(Cout, generator=g).to(torch.float16)
+    res = torch.randn(B, T, Cout, generator=g).to(torch.float16)
+    a = torch.rand(Cin, generator=g) + 0.5
+    ib = 1.0 / (a + 1e-9)
+    got = cref.conv_cl(x, w, bias, T, taps, dil, 1, Cout, res=res, snake_ab=(a, ib))
+    xs = cref.snake(x, a, ib)
+    want = torch.nn.functional.conv1d(xs.double().transpose(1, 2), w[0, :, :, :Cout].double().permute(2, 1, 0),
+                                      bias.double(), dilation=dil).transpose(1, 2)[:, :T] + res.double()
+    assert (got.double() - want).abs().max().item() <= 2 ** -10 * want.abs().max().item()
+    # a planted slip (taps read at stride 1 instead of dil) is caught
+    slip = torch.nn.functional.conv1d(xs.double().transpose(1, 2), w[0, :, :, :Cout].double().permute(2, 1, 0),
+                                      bias.double(), dilation=1).transpose(1, 2)[:, :T] + res.double()
+    assert (got.double() - slip).abs().max().item() > 0.1
+
+
+def test_conv_cl_phases_against_conv_transpose1d(cref):
+    """ph = s: the phase split of a stride-s transposed conv (kernel 2s, right crop s: tap 0 = w[:, :, p+s]
+    on the previous frame, tap 1 = w[:, :, p] on the current one, fast_engine.py:186-194) equals torch's
+    conv_transpose1d cropped to the new frames."""
+    g = torch.Generator().manual_seed(72)
+    B, T, Cin, Cout, s = 2, 6, 16, 8, 4
+    wt = (torch.randn(Cin, Cout, 2 * s, generator=g) / 4).to(torch.float16)
+    W = torch.zeros(s, 2, Cin, Cout, dtype=torch.float16)
+    for p in range(s):
+        W[p, 0] = wt[:, :, p + s]
+        W[p, 1] = wt[:, :, p]
+    x = torch.randn(B, T + 1, Cin, generator=g).to(torch.float16)        # row 0: the previous frame
+    got = cref.conv_cl(x, W, None, T, 2, 1, s, Cout)
+    full = torch.nn.functional.conv_transpose1d(x.double().transpose(1, 2), wt.double(), stride=s)
+    want = full[:, :, s:s + T * s].transpose(1, 2)
+    assert (got.double() - want).abs().max().item() <= 2 ** -10 * want.abs().max().item()
+
+
+def test_conv_cl_brute_force_tiny(cref):
+    g = torch.Generator().manual_seed(73)
+    B, T, Cin, Cout, taps, dil, ph = 2, 3, 8, 5, 2, 2, 3
+    x = torch.randn(B, T + (taps - 1) * dil, Cin, generator=g).to(torch.float16)
+    w = torch.randn(ph, taps, Cin, 8, generator=g).to(torch.float16)
+    got = cref.conv_cl(x, w, None, T, taps, dil, ph, Cout)
+    for b in range(B):
+        for t in range(T):
+            for p in range(ph):
+                for n in range(Cout):
+                    v = sum(float(x[b, t + j * dil, k]) * float(w[p, j, k, n]) for j in range(taps) for k in range(Cin))
+                    assert abs(float(got[b, t * ph + p, n]) - v) <= 2 ** -10 * max(1.0, abs(v))
+
+
+def test_snake_cat_layout(cref):
+    g = torch.Generator().manual_seed(74)
+    x = torch.randn(2, 5, 16, generator=g).to(torch.float16)
+    st = torch.randn(2, 3, 16, generator=g).to(torch.float16)
+    a = torch.rand(16, generator=g) + 0.5
+    y = cref.snake_cat(x, st, a, 1 / a)
+    assert y.shape == (2, 8, 16) and torch.equal(y[:, :3], st)
+    want = (x.double() + (1 / a).double() * torch.sin(x.double() * a.double()) ** 2).to(torch.float16)
+    assert ((y[:, 3:].double() - want.double()).abs() <= 2 ** -10 * want.double().abs().clamp(min=1)).all()
+    assert torch.equal(cref.snake_cat(x, None, None, None), x)
+
+
+def test_vocoder_pack_conv_against_torch_conv():
+    """The product's weight packing (vocoder.pack_conv, fast_engine.py:186-206) under the oracle's conv_cl
+    equals torch's conv1d / conv_transpose1d of the module weights (conv_ref._conv_fc: causal zero context,
+    right-cropped transposed conv) -- a wrong tap order, phase or transpose fails it."""
+    import importlib
+    voc = importlib.import_module("audio8-turbo-engine_amd.vocoder")
+    from oracle import conv_ref
+    g = torch.Generator().manual_seed(5)
+    B, T, Cin, Cout = 2, 6, 16, 24
+    x = torch.randn(B, T, Cin, generator=g).to(torch.float16)
+    for trans, s, K, dil in ((False, 1, 7, 3), (False, 1, 1, 1), (True, 4, 8, 1), (True, 2, 4, 1)):
+        w = torch.randn(Cin, Cout, K, generator=g) if trans else torch.randn(Cout, Cin, K, generator=g)
+        b = torch.randn(Cout, generator=g)
+        W, taps, ph = voc.pack_conv(w, trans, s)
+        assert W.shape == (ph, taps, Cin, max(16, Cout))
+        ctx = 1 if trans else (K - 1) * dil
+        xin = torch.cat([torch.zeros(B, ctx, Cin, dtype=torch.float16), x], 1)
+        got = conv_ref.conv_cl(xin, W, b.to(torch.float16), T, taps, dil if not trans else 1, ph, Cout)
+        want = conv_ref._conv_fc(x.transpose(1, 2).double(), w, b, dil=dil, trans=trans, stride=s).transpose(1, 2)
+        assert got.shape == want.shape
+        err = (got.double() - want).abs()
+        assert (err <= want.abs() * 2 ** -10 + 1e-3).all(), (trans, K, err.max())
