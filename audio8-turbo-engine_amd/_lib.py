@@ -44,7 +44,8 @@ SIGNATURES = {
     "a8_rmsnorm": (_I, [_P, _L, _P, _L, _P, _P, _L, _P, _L, _I, _I, _F, _P]),
     "a8_silu_mul": (_I, [_P, _L, _P, _L, _I, _I, _P]),
     "a8_conv_cl": (_I, [_P, _L, _L, _P, _L, _L, _L, _I, _P, _P, _L, _L, _P, _L, _L, _P, _P,
-                        _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+                        _I, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
+    "a8_conv_cl_ws_bytes": (_L, [_I, _I, _I, _I, _I, _I]),
     "a8_snake_cat": (_I, [_P, _L, _L, _P, _L, _L, _P, _P, _P, _L, _L, _I, _I, _I, _I, _P]),
     "a8_prefix_copy": (_I, [_P, _P, _L, _L, _L, _P, _P, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "a8_decode_choose_flat": (_I, [_I, _I, _I, _L, _I, _IP]),

@@ -11,13 +11,23 @@
 //              32-wide k slice in fp16 first; this is the more exact of the two).
 //   snake_cat: Y[b] = concat(ST[b] (CTX rows), snake(X[b]) (T rows)) along time; no snake when a is null.
 //
-// MI355X design (an implicit GEMM: M = B*TR rows, N = Cout, K = TAPS*Cin): a workgroup computes a 64 x 64
-// output tile of one phase with 4 waves (16 rows each) on v_mfma_f32_16x16x32_f16, as Y^T = W^T . X^T:
-//   * X rows are the B operand straight from global memory (lane l: 16 contiguous bytes of row l % 16 at
+// MI355X design (an implicit GEMM: M = B*TR rows, N = Cout, K = TAPS*Cin): a workgroup computes a BM x BN
+// output tile of one phase (BM = 64 WM rows, BN = 16 NT channels, up to 128 x 256) with 4 waves, each wave
+// WM row tiles of 16 x BN on v_mfma_f32_16x16x32_f16, as Y^T = W^T . X^T:
+//   * X rows are the B operands straight from global memory (lane l: 16 contiguous bytes of row l % 16 at
 //     channel offset 8 (l / 16)), with the snake applied in registers;
-//   * each 32 x 64 weight slice [k][n] is staged once in LDS (one 16-byte load per thread) and read as the
-//     A operand with ds_read_b64_tr_b16 (the LDS unit transposes 4 x 16 blocks), so W^T needs no copy;
-//   * the next slice's loads are issued before the current slice's MFMAs; two barriers a slice.
+//   * each KS x BN weight slice [k][n] (KS = 64 channels, or 32 when Cin is not a multiple of 64) is staged
+//     once in LDS (KS NT / 128 16-byte loads per thread) and read as the A operand with ds_read_b64_tr_b16
+//     (the LDS unit transposes 4 x 16 blocks), so W^T needs no copy;
+//     one A operand feeds WM MFMAs;
+//   * two LDS slices: the next slice's loads are issued before the current slice's MFMAs and written to the
+//     idle slice after them; one barrier a slice;
+//   * the tile shape is chosen per launch (conv_plan): the fewest padded output channels, then, among shapes
+//     that give >= 512 workgroups, two row tiles per wave and the widest tile; narrow tiles for short inputs;
+//   * short inputs with long K (the decoder's first blocks: a few hundred rows x 5-7 K channels) split K
+//     over workgroups into an fp32 workspace the caller provides (a8_conv_cl_ws_bytes), summed in a fixed
+//     order by a finishing kernel, so results do not depend on timing.
+// The snake's sine runs on the hardware sine unit after an exact reduction to one period.
 // snake_cat: one lane per 8 channels of one output row, 16-byte loads and stores.
 #include "a8_common.h"
 
@@ -36,50 +46,80 @@ __device__ __forceinline__ float h_hi(uint32_t w) { return (float)__builtin_bit_
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, f16x2{(_Float16)lo, (_Float16)hi});
 }
+// sin(x) on the hardware sine (v_sin_f32 takes revolutions): x / 2 pi reduced to [-1/2, 1/2] by its nearest
+// integer, so the unit sees its most accurate range; absolute error ~1e-6 for the snake's |a x| < 100, far
+// below the fp16 rounding of the result
+__device__ __forceinline__ float sin_hw(float x) {
+  float r = x * 0.15915494309189535f;
+  r -= __builtin_rintf(r);
+  return __builtin_amdgcn_sinf(r);
+}
+__device__ __forceinline__ u32x2 ld8(const void *p) { return *reinterpret_cast<const u32x2 *>(p); }
 // the snake x + ib sin(a x)^2 on 8 channels (fp32, one rounding to fp16)
 __device__ __forceinline__ u32x4 snake8(u32x4 v, const float *a, const float *ib) {
   u32x4 o;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const float x0 = h_lo(v[j]), x1 = h_hi(v[j]);
-    const float s0 = sinf(x0 * a[2 * j]), s1 = sinf(x1 * a[2 * j + 1]);
+    const float s0 = sin_hw(x0 * a[2 * j]), s1 = sin_hw(x1 * a[2 * j + 1]);
     o[j] = pack_f16x2(x0 + ib[2 * j] * s0 * s0, x1 + ib[2 * j + 1] * s1 * s1);
   }
   return o;
 }
 
-template <bool SNAKE>
+template <int WM, int NT, int KSUB, bool SNAKE>
 __global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x, int64_t s_xb, int64_t s_xt,
                                                  const uint16_t *__restrict__ w, int64_t s_wp, int64_t s_wt,
                                                  int64_t s_wc, const uint16_t *__restrict__ bias,
                                                  const uint16_t *__restrict__ res, int64_t s_rb, int64_t s_rt,
                                                  uint16_t *__restrict__ y, int64_t s_yb, int64_t s_yt,
                                                  const float *__restrict__ sa, const float *__restrict__ sib, int M,
-                                                 int TR, int Cin, int Cout, int CoutW, int taps, int dil, int PH) {
-  warm_kernargs<160>();  // the explicit arguments above span 0x00-0x9f
-  __shared__ __attribute__((aligned(16))) uint16_t wl[32 * 64];  // weight slice [k][n], 128 bytes a k row
-  const int p = blockIdx.z, m0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
+                                                 int TR, int Cin, int Cout, int CoutW, int taps, int dil, int PH,
+                                                 float *__restrict__ part, int ksplit) {
+  warm_kernargs<172>();  // the explicit arguments above span 0x00-0xab
+  constexpr int BN = 16 * NT, BM = 64 * WM, KS = 32 * KSUB, WCH = NT / 4 * KSUB, NCH = BN / 8;
+  // two weight slices [k][n] (KS x BN), BN * 2 bytes a k row: one is read while the next is written
+  __shared__ __attribute__((aligned(16))) uint16_t wl[2 * KS * BN];
+  const int p = blockIdx.z / ksplit, ks = blockIdx.z - p * ksplit, m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
-  // this lane's X row (the B operand's column r16) and channel chunk 8g
-  const int m = m0 + 16 * wv + r16;
-  const bool mvalid = m < M;
-  const int b = mvalid ? m / TR : 0, t = mvalid ? m - b * TR : 0;
-  const uint16_t *xrow = x + (int64_t)b * s_xb + (int64_t)t * s_xt + 8 * g;
-  // this thread's share of a weight slice: k row tid / 8, columns 8 (tid % 8) ..
-  const int wk = tid >> 3, wn = 8 * (tid & 7);
-  const uint16_t *wbase = w + (int64_t)p * s_wp + (int64_t)wk * s_wc + n0 + wn;
-  const bool wcol = n0 + wn < CoutW;
-  const int kchunks = (Cin + 31) / 32, steps = taps * kchunks;
+  // this lane's X rows (the B operands' column r16 of the wave's WM row tiles) and channel chunk 8g
+  const uint16_t *xrow[WM];
+  int mb[WM], mt[WM];
+  bool mv[WM];
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int m = m0 + (wv * WM + i) * 16 + r16;
+    mv[i] = m < M;
+    mb[i] = mv[i] ? m / TR : 0;
+    mt[i] = mv[i] ? m - mb[i] * TR : 0;
+    xrow[i] = x + (int64_t)mb[i] * s_xb + (int64_t)mt[i] * s_xt + 8 * g;
+  }
+  // this thread's share of a weight slice: 16-byte chunks c = tid + 256 q, at k row c / NCH, column 8 (c % NCH)
+  int wk[WCH], wn[WCH];
+  bool wcol[WCH];
+  const uint16_t *wb[WCH];
+#pragma unroll
+  for (int q = 0; q < WCH; ++q) {
+    const int c = tid + 256 * q;
+    wk[q] = c / NCH;
+    wn[q] = 8 * (c % NCH);
+    wcol[q] = n0 + wn[q] < CoutW;
+    wb[q] = w + (int64_t)p * s_wp + (int64_t)wk[q] * s_wc + n0 + wn[q];
+  }
+  // this workgroup's k slices: [sb, se) of taps * ceil(Cin / KS) (a 1 / ksplit share under split-K)
+  const int kchunks = (Cin + KS - 1) / KS, steps = taps * kchunks;
+  const int sb = (int)((int64_t)steps * ks / ksplit), se = (int)((int64_t)steps * (ks + 1) / ksplit);
 
-  auto load_w = [&](int s) __attribute__((always_inline)) -> u32x4 {
-    const int j = s / kchunks, k0 = (s - j * kchunks) * 32;
-    return (wcol && k0 + wk < Cin) ? ld16(wbase + (int64_t)j * s_wt + (int64_t)k0 * s_wc) : u32x4{0u, 0u, 0u, 0u};
+  auto load_w = [&](int s, int q) __attribute__((always_inline)) -> u32x4 {
+    const int j = s / kchunks, k0 = (s - j * kchunks) * KS;
+    return (wcol[q] && k0 + wk[q] < Cin) ? ld16(wb[q] + (int64_t)j * s_wt + (int64_t)k0 * s_wc)
+                                         : u32x4{0u, 0u, 0u, 0u};
   };
-  auto load_x = [&](int s) __attribute__((always_inline)) -> u32x4 {
-    const int j = s / kchunks, k0 = (s - j * kchunks) * 32;
-    if (!mvalid || k0 + 8 * g >= Cin) return u32x4{0u, 0u, 0u, 0u};
-    const u32x4 v = ld16(xrow + (int64_t)j * dil * s_xt + k0);
+  auto load_x = [&](int s, int i, int u) __attribute__((always_inline)) -> u32x4 {
+    const int j = s / kchunks, k0 = (s - j * kchunks) * KS + 32 * u;
+    if (!mv[i] || k0 + 8 * g >= Cin) return u32x4{0u, 0u, 0u, 0u};
+    const u32x4 v = ld16(xrow[i] + (int64_t)j * dil * s_xt + k0);
     if (!SNAKE) return v;
     float a[8], ib[8];
     const f32x4 a0 = *reinterpret_cast<const f32x4 *>(sa + k0 + 8 * g), a1 = *reinterpret_cast<const f32x4 *>(sa + k0 + 8 * g + 4);
@@ -94,53 +134,123 @@ __global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x,
     return snake8(v, a, ib);
   };
 
-  f32x4 acc[4];
+  f32x4 acc[WM][NT];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[i][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   // A-operand reads: rows (k) 8g + r16/4 (+4), columns (n) 16 nt + 4 (r16 % 4)
-  const uint16_t *ard = wl + (8 * g + (r16 >> 2)) * 64 + 4 * (r16 & 3);
-  u32x4 wcur = load_w(0), xcur = load_x(0);
-  for (int s = 0; s < steps; ++s) {
-    st16(wl + wk * 64 + wn, wcur);
-    __syncthreads();
-    u32x4 wnext{0u, 0u, 0u, 0u}, xnext{0u, 0u, 0u, 0u};
-    if (s + 1 < steps) {
-      wnext = load_w(s + 1);
-      xnext = load_x(s + 1);
-    }
+  const uint16_t *ard = wl + (8 * g + (r16 >> 2)) * BN + 4 * (r16 & 3);
+  u32x4 wreg[WCH], xcur[WM][KSUB], xnext[WM][KSUB];
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const u32x2 lo = lds_tr16(ard + 16 * nt), hi = lds_tr16(ard + 16 * nt + 4 * 64);
-      acc[nt] = mfma16x16x32_f16(u32x4{lo[0], lo[1], hi[0], hi[1]}, xcur, acc[nt]);
-    }
-    __syncthreads();
-    wcur = wnext;
-    xcur = xnext;
+  for (int q = 0; q < WCH; ++q) st16(wl + wk[q] * BN + wn[q], load_w(sb, q));
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int u = 0; u < KSUB; ++u) xcur[i][u] = load_x(sb, i, u);
+  for (int s = sb; s < se; ++s) {
+    const int cb = ((s - sb) & 1) * KS * BN, nb = KS * BN - cb;
+    // the next slice's loads (the last step reloads its own slice into the idle buffer: no branch)
+    const int s1 = s + 1 < se ? s + 1 : s;
+#pragma unroll
+    for (int q = 0; q < WCH; ++q) wreg[q] = load_w(s1, q);
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int u = 0; u < KSUB; ++u) xnext[i][u] = load_x(s1, i, u);
+    __syncthreads();  // slice s is in wl[cb]; every wave is done with wl[nb] (slice s - 1)
+#pragma unroll
+    for (int u = 0; u < KSUB; ++u)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const uint16_t *ap = ard + cb + 32 * u * BN + 16 * nt;
+        const u32x2 lo = lds_tr16(ap), hi = lds_tr16(ap + 4 * BN);
+        const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int i = 0; i < WM; ++i) acc[i][nt] = mfma16x16x32_f16(a, xcur[i][u], acc[i][nt]);
+      }
+#pragma unroll
+    for (int q = 0; q < WCH; ++q) st16(wl + nb + wk[q] * BN + wn[q], wreg[q]);
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int u = 0; u < KSUB; ++u) xcur[i][u] = xnext[i][u];
   }
-  // acc[nt]: lane (r16, g) holds Y[row m][n = n0 + 16 nt + 4g + i], i = 0..3
-  if (!mvalid) return;
-  const int64_t orow = (int64_t)t * PH + p;
-  uint16_t *yrow = y + (int64_t)b * s_yb + orow * s_yt;
-  const uint16_t *rrow = res ? res + (int64_t)b * s_rb + orow * s_rt : nullptr;
+  // acc[i][nt]: lane (r16, g) holds Y[row m0 + (wv WM + i) 16 + r16][n = n0 + 16 nt + 4g + e], e = 0..3
+  if (part) {  // split-K: raw fp32 sums to part[ks][p][m][n], row pitch gridDim.y BN; k_conv_fin finishes
+    const int64_t NP = (int64_t)gridDim.y * BN;
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int n = n0 + 16 * nt + 4 * g;
-    float v[4];
+    for (int i = 0; i < WM; ++i) {
+      if (!mv[i]) continue;
+      float *prow = part + ((int64_t)(ks * PH + p) * M + m0 + (wv * WM + i) * 16 + r16) * NP + n0 + 4 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = acc[nt][i];
-      if (n + i < Cout) {
-        if (bias) v[i] += h_lo(bias[n + i]);
-        if (rrow) v[i] += h_lo(rrow[n + i]);
+      for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<f32x4 *>(prow + 16 * nt) = acc[i][nt];
+    }
+    return;
+  }
+  // bias and residual by 8-byte loads where four channels share them (uniform)
+  const bool vec = (Cout & 3) == 0 && (reinterpret_cast<uintptr_t>(bias) & 7u) == 0 &&
+                   (!res || ((reinterpret_cast<uintptr_t>(res) & 7u) == 0 && ((s_rb | s_rt) & 3) == 0));
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    if (!mv[i]) continue;
+    const int64_t orow = (int64_t)mt[i] * PH + p;
+    uint16_t *yrow = y + (int64_t)mb[i] * s_yb + orow * s_yt;
+    const uint16_t *rrow = res ? res + (int64_t)mb[i] * s_rb + orow * s_rt : nullptr;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = n0 + 16 * nt + 4 * g;
+      if (n >= Cout) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = acc[i][nt][e];
+      if (vec) {  // n + 3 < Cout
+        if (bias) {
+          const u32x2 bv = ld8(bias + n);
+          v[0] += h_lo(bv[0]), v[1] += h_hi(bv[0]), v[2] += h_lo(bv[1]), v[3] += h_hi(bv[1]);
+        }
+        if (rrow) {
+          const u32x2 rv = ld8(rrow + n);
+          v[0] += h_lo(rv[0]), v[1] += h_hi(rv[0]), v[2] += h_lo(rv[1]), v[3] += h_hi(rv[1]);
+        }
+        st8(yrow + n, u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])});
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (n + e >= Cout) continue;
+          if (bias) v[e] += h_lo(bias[n + e]);
+          if (rrow) v[e] += h_lo(rrow[n + e]);
+          yrow[n + e] = (uint16_t)(pack_f16x2(v[e], 0.f) & 0xffffu);
+        }
       }
     }
-    if (n + 3 < Cout && (Cout & 3) == 0) {
-      st8(yrow + n, u32x2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])});
-    } else {
+  }
+}
+
+// Split-K finish: Y = sum over ks of part[ks] (in ks order) + bias (+ res), one rounding to fp16; one thread per
+// 4 channels of one output row.
+__global__ __launch_bounds__(256) void k_conv_fin(const float *__restrict__ part, int64_t NP, int ksplit,
+                                                  const uint16_t *__restrict__ bias, const uint16_t *__restrict__ res,
+                                                  int64_t s_rb, int64_t s_rt, uint16_t *__restrict__ y, int64_t s_yb,
+                                                  int64_t s_yt, int M, int TR, int Cout, int PH) {
+  warm_kernargs<92>();  // the explicit arguments above span 0x00-0x5b
+  const int nq = (Cout + 3) >> 2;
+  const uint32_t id = blockIdx.x * 256u + threadIdx.x;
+  if (id >= (uint32_t)PH * (uint32_t)M * (uint32_t)nq) return;
+  const int c = (int)(id % (uint32_t)nq);
+  const uint32_t pm = id / (uint32_t)nq;
+  const int m = (int)(pm % (uint32_t)M), p = (int)(pm / (uint32_t)M), n = 4 * c;
+  f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < ksplit; ++k) v += *reinterpret_cast<const f32x4 *>(part + ((int64_t)(k * PH + p) * M + m) * NP + n);
+  const int b = m / TR, t = m - b * TR;
+  const int64_t orow = (int64_t)t * PH + p;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (n + i < Cout) yrow[n + i] = (uint16_t)(pack_f16x2(v[i], 0.f) & 0xffffu);
-    }
+  for (int e = 0; e < 4; ++e) {
+    if (n + e >= Cout) continue;
+    float o = v[e];
+    if (bias) o += h_lo(bias[n + e]);
+    if (res) o += h_lo(res[(int64_t)b * s_rb + orow * s_rt + n + e]);
+    y[(int64_t)b * s_yb + orow * s_yt + n + e] = (uint16_t)(pack_f16x2(o, 0.f) & 0xffffu);
   }
 }
 
@@ -177,12 +287,55 @@ __global__ __launch_bounds__(256) void k_snake_cat(const uint16_t *__restrict__ 
 
 static inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
+// The launch shape of one conv: BN = 16 NT output channels and BM = 64 WM rows (NT in 4, 8, 12, 16; WM in
+// 1, 2) as conv_plan ranks them (four row tiles per wave measured slower: fewer waves per SIMD); k slices of
+// 64 channels when Cin allows, else 32; when fewer than 512 workgroups remain over a K of >= 16 slices (the decoder's early, short blocks), K is split into up to 16
+// shares of >= 8 slices, summed in fixed order by k_conv_fin from an fp32 workspace.
+struct ConvPlan {
+  int NT, WM, KSUB, ksplit;
+  int64_t ntiles, ws_bytes;
+};
+static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph) {
+  ConvPlan pl{16, 1, Cin % 64 == 0 ? 2 : 1, 1, 0, 0};
+  // (NT, WM) candidates: the fewest padded columns; then, among shapes that fill the chip (>= 512
+  // workgroups), the most row tiles per wave (each LDS weight read feeds WM MFMAs), then the widest tile;
+  // when none fills it, the most workgroups
+  static const int cand[][2] = {{16, 2}, {16, 1}, {12, 2}, {12, 1}, {8, 2}, {8, 1}, {4, 2}, {4, 1}};
+  int64_t best_cols = INT64_MAX, best_wgs = 0;
+  int best_wm = 0;
+  for (const auto &c : cand) {
+    const int nt = c[0], wm = c[1];
+    const int64_t nti = (Cout + 16 * nt - 1) / (16 * nt), cols = nti * 16 * nt;
+    const int64_t wgs = ((M + 64 * wm - 1) / (64 * wm)) * nti * ph;
+    bool better;
+    if (cols != best_cols) better = cols < best_cols;
+    else if ((wgs >= 512) != (best_wgs >= 512)) better = wgs >= 512;
+    else if (wgs >= 512) better = wm > best_wm;  // candidates come widest first
+    else better = wgs > best_wgs;
+    if (better) best_cols = cols, best_wgs = wgs, best_wm = wm, pl.NT = nt, pl.WM = wm;
+  }
+  pl.ntiles = (Cout + 16 * pl.NT - 1) / (16 * pl.NT);
+  const int64_t wgs = best_wgs;
+  const int steps = taps * ((Cin + 32 * pl.KSUB - 1) / (32 * pl.KSUB));
+  if (wgs < 512 && steps >= 16 && (int64_t)ph * M * ((Cout + 3) / 4) < ((int64_t)1 << 31)) {
+    int64_t k = (1024 + wgs - 1) / wgs;
+    k = k < steps / 8 ? k : steps / 8;
+    k = k < 16 ? k : 16;
+    if (k > 1) {
+      pl.ksplit = (int)k;
+      pl.ws_bytes = k * ph * M * pl.ntiles * 16 * pl.NT * 4;
+    }
+  }
+  return pl;
+}
+
 }  // namespace a8
 
 extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void *w, int64_t s_wp, int64_t s_wt,
                           int64_t s_wc, int cout_w, const void *bias, const void *res, int64_t s_rb, int64_t s_rt,
                           void *y, int64_t s_yb, int64_t s_yt, const float *snake_a, const float *snake_ib, int B,
-                          int Tin, int TR, int Cin, int Cout, int taps, int dil, int ph, void *stream) {
+                          int Tin, int TR, int Cin, int Cout, int taps, int dil, int ph, void *ws, int64_t ws_bytes,
+                          void *stream) {
   using namespace a8;
   if (B < 0 || TR < 0 || Cin <= 0 || Cout <= 0 || taps <= 0 || dil <= 0 || ph <= 0 || cout_w < Cout)
     return set_error(A8_EINVAL, "conv_cl: bad sizes B=%d TR=%d Cin=%d Cout=%d taps=%d dil=%d ph=%d cout_w=%d", B, TR,
@@ -199,16 +352,62 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
     return set_error(A8_EALIGN, "conv_cl: x / w / snake 16-byte aligned, strides multiples of 8, y 8-byte");
   const int64_t M = (int64_t)B * TR;
   if (M > INT32_MAX / 2) return set_error(A8_EUNSUP, "conv_cl: %lld rows too many", (long long)M);
-  const dim3 grid((unsigned)((M + 63) / 64), (unsigned)((Cout + 63) / 64), (unsigned)ph);
+  ConvPlan pl = conv_plan(M, Cin, Cout, taps, ph);
+  if (pl.ksplit > 1 && (!ws || ws_bytes < pl.ws_bytes)) pl.ksplit = 1;  // no workspace: one pass over K
+  if (pl.ksplit > 1 && !al16(ws)) return set_error(A8_EALIGN, "conv_cl: workspace must be 16-byte aligned");
+  const int NT = pl.NT, WM = pl.WM;
+  float *part = pl.ksplit > 1 ? (float *)ws : nullptr;
+  const dim3 grid((unsigned)((M + 64 * WM - 1) / (64 * WM)), (unsigned)pl.ntiles, (unsigned)(ph * pl.ksplit));
 #define A8_CONV_ARGS (const uint16_t *)x, s_xb, s_xt, (const uint16_t *)w, s_wp, s_wt, s_wc, (const uint16_t *)bias, \
                      (const uint16_t *)res, s_rb, s_rt, (uint16_t *)y, s_yb, s_yt, snake_a, snake_ib, (int)M, TR, Cin, \
-                     Cout, cout_w, taps, dil, ph
-  if (snake_a)
-    hipLaunchKernelGGL(k_conv_cl<true>, grid, dim3(256), 0, (hipStream_t)stream, A8_CONV_ARGS);
-  else
-    hipLaunchKernelGGL(k_conv_cl<false>, grid, dim3(256), 0, (hipStream_t)stream, A8_CONV_ARGS);
+                     Cout, cout_w, taps, dil, ph, part, pl.ksplit
+#define A8_CONV_L(wm, nt, ksub, sn) \
+  hipLaunchKernelGGL((k_conv_cl<wm, nt, ksub, sn>), grid, dim3(256), 0, (hipStream_t)stream, A8_CONV_ARGS)
+#define A8_CONV_NT(wm, ksub, sn)                 \
+  switch (NT) {                                  \
+    case 4: A8_CONV_L(wm, 4, ksub, sn); break;   \
+    case 8: A8_CONV_L(wm, 8, ksub, sn); break;   \
+    case 12: A8_CONV_L(wm, 12, ksub, sn); break; \
+    default: A8_CONV_L(wm, 16, ksub, sn); break; \
+  }
+#define A8_CONV_K(wm, sn)         \
+  if (pl.KSUB == 2) {             \
+    A8_CONV_NT(wm, 2, sn)         \
+  } else {                        \
+    A8_CONV_NT(wm, 1, sn)         \
+  }
+  if (WM == 2) {
+    if (snake_a) {
+      A8_CONV_K(2, true)
+    } else {
+      A8_CONV_K(2, false)
+    }
+  } else {
+    if (snake_a) {
+      A8_CONV_K(1, true)
+    } else {
+      A8_CONV_K(1, false)
+    }
+  }
+#undef A8_CONV_K
+#undef A8_CONV_L
+#undef A8_CONV_NT
 #undef A8_CONV_ARGS
+  if (part) {
+    const int64_t threads = (int64_t)ph * M * ((Cout + 3) / 4);
+    hipLaunchKernelGGL(k_conv_fin, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const float *)part, pl.ntiles * 16 * NT, pl.ksplit, (const uint16_t *)bias,
+                       (const uint16_t *)res, s_rb, s_rt, (uint16_t *)y, s_yb, s_yt, (int)M, TR, Cout, ph);
+  }
   return (int)hipGetLastError();
+}
+
+extern "C" int64_t a8_conv_cl_ws_bytes(int B, int TR, int Cin, int Cout, int taps, int ph) {
+  using namespace a8;
+  if (B <= 0 || TR <= 0 || Cin <= 0 || Cout <= 0 || taps <= 0 || ph <= 0) return 0;
+  const int64_t M = (int64_t)B * TR;
+  if (M > INT32_MAX / 2) return 0;
+  return conv_plan(M, Cin, Cout, taps, ph).ws_bytes;
 }
 
 extern "C" int a8_snake_cat(const void *x, int64_t s_xb, int64_t s_xt, const void *state, int64_t s_sb, int64_t s_st,

@@ -508,12 +508,16 @@ def conv_cl(xin, w, bias, TR, taps, dil, ph, out, res=None, f16acc=True, cfg=Non
         _need(sa.dtype == torch.float32 and sib.dtype == torch.float32 and sa.is_contiguous() and sib.is_contiguous()
               and sa.numel() >= Cin and sib.numel() >= Cin, "snake must be two contiguous float32 [Cin] vectors")
     _check_device(xin=xin, w=w, out=out, bias=bias, res=res, snake_a=sa, snake_ib=sib)
-    st = _lib.load().a8_conv_cl(
+    lib = _lib.load()
+    nws = lib.a8_conv_cl_ws_bytes(B, TR, Cin, Cout, taps, ph)    # split-K workspace (short inputs), else 0
+    ws = torch.empty(nws, dtype=torch.uint8, device=xin.device) if nws > 0 else None
+    st = lib.a8_conv_cl(
         xin.data_ptr(), xin.stride(0), xin.stride(1), w.data_ptr(), w.stride(0), w.stride(1), w.stride(2),
         w.shape[3], bias.data_ptr() if bias is not None else None, res.data_ptr() if res is not None else None,
         res.stride(0) if res is not None else 0, res.stride(1) if res is not None else 0, out.data_ptr(),
         out.stride(0), out.stride(1), sa.data_ptr() if sa is not None else None,
-        sib.data_ptr() if sib is not None else None, B, Tin, TR, Cin, Cout, taps, dil, ph, _lib.stream_of(xin))
+        sib.data_ptr() if sib is not None else None, B, Tin, TR, Cin, Cout, taps, dil, ph,
+        ws.data_ptr() if ws is not None else None, nws, _lib.stream_of(xin))
     _lib.check(st, "conv_cl")
     return out
 

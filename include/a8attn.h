@@ -295,13 +295,18 @@ int a8_silu_mul(const void *gu, int64_t s_gu, void *y, int64_t s_y, int rows, in
  *   n < Cout; x [B, Tin, Cin] (Tin >= TR + (taps-1) dil, Cin a multiple of 8), w [ph, taps, Cin, cout_w]
  *   (cout_w >= Cout, a multiple of 8; last dim contiguous), bias [Cout] or NULL, res like y or NULL.
  *   snake_a / snake_ib (fp32 [Cin]) or NULL: x -> x + ib sin(a x)^2 (fp16) on the load. fp32 accumulation.
+ *   ws / ws_bytes: an optional 16-byte aligned device workspace; with a8_conv_cl_ws_bytes(...) bytes the
+ *   kernel may split K across workgroups (fixed-order fp32 sums: the same result with or without it).
+ * a8_conv_cl_ws_bytes: the workspace a8_conv_cl would use for these sizes (0: none). No counterpart in the
+ *   reference (its Triton conv splits nothing); lets the caller allocate from its own pool.
  * a8_snake_cat replaces serve/fast_kernels.py:718-729 (snake_cat, kernel 695-715):
  *   y[b] = concat(state[b] (CTX rows), snake(x[b]) (T rows)), C a multiple of 8; a / ib NULL: no snake.
  */
 int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void *w, int64_t s_wp, int64_t s_wt, int64_t s_wc,
                int cout_w, const void *bias, const void *res, int64_t s_rb, int64_t s_rt, void *y, int64_t s_yb,
                int64_t s_yt, const float *snake_a, const float *snake_ib, int B, int Tin, int TR, int Cin, int Cout,
-               int taps, int dil, int ph, void *stream);
+               int taps, int dil, int ph, void *ws, int64_t ws_bytes, void *stream);
+int64_t a8_conv_cl_ws_bytes(int B, int TR, int Cin, int Cout, int taps, int ph);
 int a8_snake_cat(const void *x, int64_t s_xb, int64_t s_xt, const void *state, int64_t s_sb, int64_t s_st,
                  const float *a, const float *ib, void *y, int64_t s_yb, int64_t s_yt, int B, int T, int CTX, int C,
                  void *stream);

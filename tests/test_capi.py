@@ -25,7 +25,7 @@ def test_header_declares_the_entry_points():
                                          "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn",
                                          "a8_decode_attn_flat", "a8_decode_choose_flat", "a8_store_decode_flat",
                                          "a8_store_decode_split", "a8_prefix_copy", "a8_rmsnorm", "a8_silu_mul",
-                                         "a8_conv_cl", "a8_snake_cat"}
+                                         "a8_conv_cl", "a8_conv_cl_ws_bytes", "a8_snake_cat"}
 
 
 def test_library_exports_every_declared_symbol(a8):
@@ -287,7 +287,7 @@ def test_conv_ops_reject_before_launch(a8):
     lib = a8.load_library()
     conv = dict(x=16, s_xb=10 * 64, s_xt=64, w=16, s_wp=7 * 64 * 64, s_wt=64 * 64, s_wc=64, cout_w=64, bias=None,
                 res=None, s_rb=0, s_rt=0, y=16, s_yb=4 * 64, s_yt=64, sa=None, sib=None, B=2, Tin=10, TR=4, Cin=64,
-                Cout=64, taps=7, dil=1, ph=1, stream=None)
+                Cout=64, taps=7, dil=1, ph=1, ws=None, nws=0, stream=None)
     assert lib.a8_conv_cl(*{**conv, "Tin": 9}.values()) == -1           # 4 + 6 context rows needed
     assert b"input rows" in lib.a8_last_error()
     assert lib.a8_conv_cl(*{**conv, "Cin": 60}.values()) == -3          # channels in 16-byte chunks
@@ -295,6 +295,10 @@ def test_conv_ops_reject_before_launch(a8):
     assert lib.a8_conv_cl(*{**conv, "sa": 16}.values()) == -1           # snake needs both vectors
     assert lib.a8_conv_cl(*{**conv, "x": 24}.values()) == -2
     assert lib.a8_conv_cl(*{**conv, "TR": 0, "Tin": 6}.values()) == 0
+    # split-K workspace: short inputs with long K get one, long inputs none
+    assert lib.a8_conv_cl_ws_bytes(192, 4, 1024, 1536, 7, 1) > 0
+    assert lib.a8_conv_cl_ws_bytes(192, 1024, 192, 192, 7, 1) == 0
+    assert lib.a8_conv_cl_ws_bytes(0, 4, 1024, 1536, 7, 1) == 0
     snake = dict(x=16, s_xb=5 * 64, s_xt=64, st=16, s_sb=3 * 64, s_st=64, a=None, ib=None, y=16, s_yb=8 * 64, s_yt=64,
                  B=2, T=5, CTX=3, C=64, stream=None)
     assert lib.a8_snake_cat(*{**snake, "C": 60}.values()) == -3

@@ -38,6 +38,7 @@ def _close(got, want):
     (8, 64, 96, 96, 96, 1, 1, 1, True, True, True),           # residual unit's 1x1 conv, snake on load, + input
     (8, 128, 96, 1, 16, 7, 1, 1, True, False, False),         # one-channel output conv (padded weights)
     (3, 5, 8, 24, 32, 3, 2, 3, False, True, True),            # ragged: one k chunk, Cout 24, 15 rows
+    (4, 8, 512, 30, 32, 7, 1, 1, True, True, True),           # split K with Cout 30 (no 4-channel vectors)
 ])
 def test_conv_cl_shapes(a8, cref, dev, B, T, Cin, Cout, cw, taps, dil, ph, bias, res, snake):
     say(f"case: conv_cl B={B} T={T} Cin={Cin} Cout={Cout} taps={taps} dil={dil} ph={ph} bias={bias} res={res} "
@@ -88,3 +89,32 @@ def test_snake_cat_and_decoder_call_pattern(a8, cref, dev):
         assert _close(xin[:, ctx:], xin_h[:, ctx:])                           # the snake: <= 1 fp16 ulp
         assert _close(y, cref.conv_cl(xin.cpu(), w, bias, T, taps, dil, 1, Cout))
         assert _close(y, cref.conv_cl(xin_h, w, bias, T, taps, dil, 1, Cout))
+
+
+def test_conv_cl_split_k_equals_one_pass(a8, dev):
+    """The split-K path (short input, long K: the decoder's input conv) gives the same bits as the one-pass
+    kernel the entry point runs without a workspace: both sum in fp32, the split sums its shares in a fixed
+    order, so only the association differs -- checked to one fp16 ulp, and run-to-run identical."""
+    say("case: conv_cl split-K vs one pass, B=8 T=4 Cin=1024 Cout=1536 taps=7")
+    lib = a8.load_library()
+    g = torch.Generator(device=dev).manual_seed(4)
+    B, T, Cin, Cout, taps = 8, 4, 1024, 1536, 7
+    x = torch.randn(B, T + taps - 1, Cin, generator=g, device=dev).to(F16)
+    w = (torch.randn(1, taps, Cin, Cout, generator=g, device=dev) / (taps * Cin) ** 0.5).to(F16)
+    bias = torch.randn(Cout, generator=g, device=dev).to(F16)
+    nws = lib.a8_conv_cl_ws_bytes(B, T, Cin, Cout, taps, 1)
+    assert nws > 0
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev)
+    outs = []
+    for use_ws in (True, True, False):
+        y = torch.empty(B, T, Cout, dtype=F16, device=dev)
+        st = lib.a8_conv_cl(x.data_ptr(), x.stride(0), x.stride(1), w.data_ptr(), w.stride(0), w.stride(1),
+                            w.stride(2), Cout, bias.data_ptr(), None, 0, 0, y.data_ptr(), y.stride(0), y.stride(1),
+                            None, None, B, x.shape[1], T, Cin, Cout, taps, 1, 1, ws.data_ptr() if use_ws else None,
+                            nws if use_ws else 0, torch.cuda.current_stream().cuda_stream)
+        assert st == 0
+        outs.append(y)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    d = (outs[0].float() - outs[2].float()).abs()
+    assert (d <= outs[2].float().abs() * 2 ** -10 + 1e-3).all()
