@@ -46,6 +46,8 @@ def parse():
                    help="only launch one layer's decode 4x and a 256 MiB copy (target of rocprofv3 --pmc passes)")
     p.add_argument("--prefill-probe", action="store_true",
                    help="only launch the C4 prefill 3x (target of rocprofv3 --pmc passes)")
+    p.add_argument("--vocoder-probe", action="store_true",
+                   help="only run the streaming decoder for 5 frames at 192 rows (target of rocprofv3)")
     return p.parse_args()
 
 
@@ -399,6 +401,21 @@ def traffic_probe(torch, st, w, nsplit_req):
     print("traffic probe: 4 tick-layer launches, 2 copies of 268435456 bytes", flush=True)
 
 
+def vocoder_probe(a8, torch, dev):
+    """Profile target for the vocoder convolutions: the synthetic DAC-style decoder (1024 -> 1536 channels,
+    strides 8, 8, 4, 2) run eagerly for 5 frames of 4 input rows at 192 rows."""
+    from importlib import import_module
+    voc = import_module(a8.__name__ + ".vocoder")
+    b = 192
+    dec = voc.CLDecoder(voc.decoder_weights(dev=dev, seed=21), b, dev)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    xf = torch.randn(b, 4, 1024, generator=gen, device=dev).to(torch.float16)
+    for _ in range(5):
+        dec(xf, b)
+    torch.cuda.synchronize()
+    print("vocoder probe: 5 frames done", flush=True)
+
+
 def prefill_probe(a8, torch, dev):
     """Counter target for the prefill: the C4 workload (64 requests, n ~ U[40, 400] after a 300-position
     prefix, 13,745 packed rows) launched 3 times. Run under rocprofv3 --pmc with one counter group a pass."""
@@ -435,6 +452,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.prefill_probe:
         prefill_probe(a8, torch, dev)
+        return
+    if args.vocoder_probe:
+        vocoder_probe(a8, torch, dev)
         return
     props = torch.cuda.get_device_properties(dev)
     w = build_workload(a8, torch, args.config, dev)
