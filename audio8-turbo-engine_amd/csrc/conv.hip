@@ -78,8 +78,11 @@ __global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x,
                                                  float *__restrict__ part, int ksplit) {
   warm_kernargs<172>();  // the explicit arguments above span 0x00-0xab
   constexpr int BN = 16 * NT, BM = 64 * WM, KS = 32 * KSUB, WCH = NT / 4 * KSUB, NCH = BN / 8;
-  // two weight slices [k][n] (KS x BN), BN * 2 bytes a k row: one is read while the next is written
-  __shared__ __attribute__((aligned(16))) uint16_t wl[2 * KS * BN];
+  // two weight slices [k][n] (KS x BN): one is read while the next is written. A k row is BN + 16 elements
+  // apart: the 16 rows one transposing read touches then fall on distinct bank groups (at a pitch of BN,
+  // a multiple of 64 elements, they all hit the same 8 banks: 4x the LDS cycles, measured as bank conflicts)
+  constexpr int BNP = BN + 16;
+  __shared__ __attribute__((aligned(16))) uint16_t wl[2 * KS * BNP];
   const int p = blockIdx.z / ksplit, ks = blockIdx.z - p * ksplit, m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
@@ -140,16 +143,16 @@ __global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x,
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[i][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   // A-operand reads: rows (k) 8g + r16/4 (+4), columns (n) 16 nt + 4 (r16 % 4)
-  const uint16_t *ard = wl + (8 * g + (r16 >> 2)) * BN + 4 * (r16 & 3);
+  const uint16_t *ard = wl + (8 * g + (r16 >> 2)) * BNP + 4 * (r16 & 3);
   u32x4 wreg[WCH], xcur[WM][KSUB], xnext[WM][KSUB];
 #pragma unroll
-  for (int q = 0; q < WCH; ++q) st16(wl + wk[q] * BN + wn[q], load_w(sb, q));
+  for (int q = 0; q < WCH; ++q) st16(wl + wk[q] * BNP + wn[q], load_w(sb, q));
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
     for (int u = 0; u < KSUB; ++u) xcur[i][u] = load_x(sb, i, u);
   for (int s = sb; s < se; ++s) {
-    const int cb = ((s - sb) & 1) * KS * BN, nb = KS * BN - cb;
+    const int cb = ((s - sb) & 1) * KS * BNP, nb = KS * BNP - cb;
     // the next slice's loads (the last step reloads its own slice into the idle buffer: no branch)
     const int s1 = s + 1 < se ? s + 1 : s;
 #pragma unroll
@@ -163,14 +166,14 @@ __global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x,
     for (int u = 0; u < KSUB; ++u)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const uint16_t *ap = ard + cb + 32 * u * BN + 16 * nt;
-        const u32x2 lo = lds_tr16(ap), hi = lds_tr16(ap + 4 * BN);
+        const uint16_t *ap = ard + cb + 32 * u * BNP + 16 * nt;
+        const u32x2 lo = lds_tr16(ap), hi = lds_tr16(ap + 4 * BNP);
         const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int i = 0; i < WM; ++i) acc[i][nt] = mfma16x16x32_f16(a, xcur[i][u], acc[i][nt]);
       }
 #pragma unroll
-    for (int q = 0; q < WCH; ++q) st16(wl + nb + wk[q] * BN + wn[q], wreg[q]);
+    for (int q = 0; q < WCH; ++q) st16(wl + nb + wk[q] * BNP + wn[q], wreg[q]);
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
