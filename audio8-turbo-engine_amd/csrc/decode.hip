@@ -63,6 +63,25 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   constexpr uint32_t row_bytes = kRow;  // s_ks == 64, checked by the entry point
   TileLane tl;
   tl.init(lane);
+  const int64_t cbase = (int64_t)(crow < 0 || crow >= cache_rows ? 0 : crow) * s_kb + (int64_t)kh * s_kh;
+  // K / V of this (row, kv head) as buffers ending at key hi: rows past the range read as zeros.
+  const rsrc_t kr = make_rsrc(kc + cbase, (uint32_t)hi * row_bytes);
+  const rsrc_t vr = make_rsrc(vc + cbase, (uint32_t)hi * row_bytes);
+  uint16_t *va = vbA + w * kVTile, *vb = vbB + w * kVTile;
+
+  // Software pipeline over the wave's tiles first + k * 64*NW, k = 0..n-1, two register buffers, the
+  // loads one tile ahead. The first tile is requested before the q / qkv prologue, so its latency and
+  // the prologue's overlap (in the fused case the position being stored is patched from registers, so
+  // the tile may be read before the store lands). The first step is peeled: the loop is entered with
+  // exactly one tile's loads pending on both edges, so the compiler's waits stay partial (a load pending
+  // only on the entry edge costs a full drain per iteration). Requests past the range read zeros
+  // without memory traffic.
+  constexpr int kStep = 64 * NW;
+  const int first = lo + 64 * __builtin_amdgcn_readfirstlane(w);
+  const int n = first < hi ? (hi - first + kStep - 1) / kStep : 0;
+  KTile A[1], B[1];
+  load_step<1>(A, va, kr, vr, (uint32_t)first, tl);
+
   // Q^T operand: column r16 = q head kh*group + r16 (zeros past the group).
   u32x4 qB0, qB1;
   KVPatch pt;
@@ -81,30 +100,15 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   SoftmaxState S;
   S.reset();
 
-  const int64_t cbase = (int64_t)(crow < 0 || crow >= cache_rows ? 0 : crow) * s_kb + (int64_t)kh * s_kh;
-  // K / V of this (row, kv head) as buffers ending at key hi: rows past the range read as zeros.
-  const rsrc_t kr = make_rsrc(kc + cbase, (uint32_t)hi * row_bytes);
-  const rsrc_t vr = make_rsrc(vc + cbase, (uint32_t)hi * row_bytes);
-  uint16_t *va = vbA + w * kVTile, *vb = vbB + w * kVTile;
-
-  // Software pipeline over the wave's tiles first + k * 64*NW, k = 0..n-1, two register buffers:
-  // each iteration requests tile k, consumes tile k-1 (loaded one step earlier), requests tile k+1 and
-  // consumes tile k. Nothing is in flight when the loop is entered, so the loop header sees the same
-  // pending loads on both edges and the compiler's waits stay partial (vmcnt(16+)); a prologue load
-  // in front of the loop lands in other registers and costs a full drain (vmcnt(0)) per iteration.
-  // Requests past the range read zeros without memory traffic.
-  constexpr int kStep = 64 * NW;
-  const int first = lo + 64 * __builtin_amdgcn_readfirstlane(w);
-  const int n = first < hi ? (hi - first + kStep - 1) / kStep : 0;
   if (n > 0) {
-    KTile A[1], B[1];
-    for (int k = 0;; k += 2) {
-      load_step<1>(A, va, kr, vr, (uint32_t)(first + k * kStep), tl);
-      if (k > 0) compute_step<1, FUSED>(B, vb, first + (k - 1) * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
-      if (k >= n) break;
-      load_step<1>(B, vb, kr, vr, (uint32_t)(first + (k + 1) * kStep), tl);
-      compute_step<1, FUSED>(A, va, first + k * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
+    load_step<1>(B, vb, kr, vr, (uint32_t)(first + kStep), tl);
+    compute_step<1, FUSED>(A, va, first, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
+    for (int k = 1; k < n; k += 2) {
+      load_step<1>(A, va, kr, vr, (uint32_t)(first + (k + 1) * kStep), tl);
+      compute_step<1, FUSED>(B, vb, first + k * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
       if (k + 1 >= n) break;
+      load_step<1>(B, vb, kr, vr, (uint32_t)(first + (k + 2) * kStep), tl);
+      compute_step<1, FUSED>(A, va, first + (k + 1) * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
     }
   }
   // The last request past the range still writes (zeros) into LDS when it returns: let it land
