@@ -68,15 +68,16 @@ __device__ __forceinline__ u32x4 snake8(u32x4 v, const float *a, const float *ib
 }
 
 template <int WM, int NT, int KSUB, bool SNAKE>
-__global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x, int64_t s_xb, int64_t s_xt,
+__global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__ x, int64_t s_xb, int64_t s_xt,
                                                  const uint16_t *__restrict__ w, int64_t s_wp, int64_t s_wt,
                                                  int64_t s_wc, const uint16_t *__restrict__ bias,
                                                  const uint16_t *__restrict__ res, int64_t s_rb, int64_t s_rt,
                                                  uint16_t *__restrict__ y, int64_t s_yb, int64_t s_yt,
                                                  const float *__restrict__ sa, const float *__restrict__ sib, int M,
                                                  int TR, int Cin, int Cout, int CoutW, int taps, int dil, int PH,
-                                                 float *__restrict__ part, int ksplit) {
-  warm_kernargs<172>();  // the explicit arguments above span 0x00-0xab
+                                                 float *__restrict__ part, int ksplit, uint32_t x_span,
+                                                 uint32_t w_span) {
+  warm_kernargs<180>();  // the explicit arguments above span 0x00-0xb3
   constexpr int BN = 16 * NT, BM = 64 * WM, KS = 32 * KSUB, WCH = NT / 4 * KSUB, NCH = BN / 8;
   // two weight slices [k][n] (KS x BN): one is read while the next is written. A k row is BN + 16 elements
   // apart: the 16 rows one transposing read touches then fall on distinct bank groups (at a pitch of BN,
@@ -86,8 +87,13 @@ __global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x,
   const int p = blockIdx.z / ksplit, ks = blockIdx.z - p * ksplit, m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r16 = lane & 15, g = lane >> 4;
+  // Operand loads are buffer loads with the range check as the mask (an invalid lane asks for offset
+  // kOob and reads zeros): no branch around a load, so the compiler's wait before the MFMAs covers only
+  // the operands they use, not the next slice's loads in flight (conditional loads made it vmcnt(0)).
+  constexpr uint32_t kOob = 0x80000000u;  // the entry point checks both spans are below it
+  const rsrc_t xr = make_rsrc(x, x_span), wr = make_rsrc(w, w_span);
   // this lane's X rows (the B operands' column r16 of the wave's WM row tiles) and channel chunk 8g
-  const uint16_t *xrow[WM];
+  uint32_t xoff[WM];
   int mb[WM], mt[WM];
   bool mv[WM];
 #pragma unroll
@@ -96,19 +102,19 @@ __global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x,
     mv[i] = m < M;
     mb[i] = mv[i] ? m / TR : 0;
     mt[i] = mv[i] ? m - mb[i] * TR : 0;
-    xrow[i] = x + (int64_t)mb[i] * s_xb + (int64_t)mt[i] * s_xt + 8 * g;
+    xoff[i] = (uint32_t)(((int64_t)mb[i] * s_xb + (int64_t)mt[i] * s_xt + 8 * g) * 2);
   }
   // this thread's share of a weight slice: 16-byte chunks c = tid + 256 q, at k row c / NCH, column 8 (c % NCH)
   int wk[WCH], wn[WCH];
   bool wcol[WCH];
-  const uint16_t *wb[WCH];
+  uint32_t wb[WCH];
 #pragma unroll
   for (int q = 0; q < WCH; ++q) {
     const int c = tid + 256 * q;
     wk[q] = c / NCH;
     wn[q] = 8 * (c % NCH);
     wcol[q] = n0 + wn[q] < CoutW;
-    wb[q] = w + (int64_t)p * s_wp + (int64_t)wk[q] * s_wc + n0 + wn[q];
+    wb[q] = (uint32_t)(((int64_t)p * s_wp + (int64_t)wk[q] * s_wc + n0 + wn[q]) * 2);
   }
   // this workgroup's k slices: [sb, se) of taps * ceil(Cin / KS) (a 1 / ksplit share under split-K)
   const int kchunks = (Cin + KS - 1) / KS, steps = taps * kchunks;
@@ -116,17 +122,19 @@ __global__ __launch_bounds__(256) void k_conv_cl(const uint16_t *__restrict__ x,
 
   auto load_w = [&](int s, int q) __attribute__((always_inline)) -> u32x4 {
     const int j = s / kchunks, k0 = (s - j * kchunks) * KS;
-    return (wcol[q] && k0 + wk[q] < Cin) ? ld16(wb[q] + (int64_t)j * s_wt + (int64_t)k0 * s_wc)
-                                         : u32x4{0u, 0u, 0u, 0u};
+    const bool ok = wcol[q] && k0 + wk[q] < Cin;
+    return bld16(wr, ok ? wb[q] + (uint32_t)(((int64_t)j * s_wt + (int64_t)k0 * s_wc) * 2) : kOob);
   };
   auto load_x = [&](int s, int i, int u) __attribute__((always_inline)) -> u32x4 {
     const int j = s / kchunks, k0 = (s - j * kchunks) * KS + 32 * u;
-    if (!mv[i] || k0 + 8 * g >= Cin) return u32x4{0u, 0u, 0u, 0u};
-    const u32x4 v = ld16(xrow[i] + (int64_t)j * dil * s_xt + k0);
+    const bool ok = mv[i] && k0 + 8 * g < Cin;
+    const u32x4 v = bld16(xr, ok ? xoff[i] + (uint32_t)(((int64_t)j * dil * s_xt + k0) * 2) : kOob);
     if (!SNAKE) return v;
+    // snake(0) = 0: lanes that read zeros stay zero, so their snake vectors may be any in-range entries
+    const int kc = ok ? k0 + 8 * g : 0;
     float a[8], ib[8];
-    const f32x4 a0 = *reinterpret_cast<const f32x4 *>(sa + k0 + 8 * g), a1 = *reinterpret_cast<const f32x4 *>(sa + k0 + 8 * g + 4);
-    const f32x4 i0 = *reinterpret_cast<const f32x4 *>(sib + k0 + 8 * g), i1 = *reinterpret_cast<const f32x4 *>(sib + k0 + 8 * g + 4);
+    const f32x4 a0 = *reinterpret_cast<const f32x4 *>(sa + kc), a1 = *reinterpret_cast<const f32x4 *>(sa + kc + 4);
+    const f32x4 i0 = *reinterpret_cast<const f32x4 *>(sib + kc), i1 = *reinterpret_cast<const f32x4 *>(sib + kc + 4);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       a[q] = a0[q];
@@ -355,6 +363,13 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
     return set_error(A8_EALIGN, "conv_cl: x / w / snake 16-byte aligned, strides multiples of 8, y 8-byte");
   const int64_t M = (int64_t)B * TR;
   if (M > INT32_MAX / 2) return set_error(A8_EUNSUP, "conv_cl: %lld rows too many", (long long)M);
+  // bytes the kernel may read from x and w: both are addressed by 32-bit buffer offsets
+  const int64_t x_span = ((int64_t)(B - 1) * s_xb + (int64_t)(Tin - 1) * s_xt + Cin) * 2;
+  const int64_t w_span = ((int64_t)(ph - 1) * s_wp + (int64_t)(taps - 1) * s_wt + (int64_t)(Cin - 1) * s_wc + cout_w) * 2;
+  if (x_span >= ((int64_t)1 << 31) || w_span >= ((int64_t)1 << 31) || s_xb < 0 || s_xt < 0 || s_wp < 0 || s_wt < 0 ||
+      s_wc < 0)
+    return set_error(A8_EUNSUP, "conv_cl: x spans %lld bytes, w %lld (each must be below 2 GiB, strides >= 0)",
+                     (long long)x_span, (long long)w_span);
   ConvPlan pl = conv_plan(M, Cin, Cout, taps, ph);
   if (pl.ksplit > 1 && (!ws || ws_bytes < pl.ws_bytes)) pl.ksplit = 1;  // no workspace: one pass over K
   if (pl.ksplit > 1 && !al16(ws)) return set_error(A8_EALIGN, "conv_cl: workspace must be 16-byte aligned");
@@ -363,7 +378,7 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
   const dim3 grid((unsigned)((M + 64 * WM - 1) / (64 * WM)), (unsigned)pl.ntiles, (unsigned)(ph * pl.ksplit));
 #define A8_CONV_ARGS (const uint16_t *)x, s_xb, s_xt, (const uint16_t *)w, s_wp, s_wt, s_wc, (const uint16_t *)bias, \
                      (const uint16_t *)res, s_rb, s_rt, (uint16_t *)y, s_yb, s_yt, snake_a, snake_ib, (int)M, TR, Cin, \
-                     Cout, cout_w, taps, dil, ph, part, pl.ksplit
+                     Cout, cout_w, taps, dil, ph, part, pl.ksplit, (uint32_t)x_span, (uint32_t)w_span
 #define A8_CONV_L(wm, nt, ksub, sn) \
   hipLaunchKernelGGL((k_conv_cl<wm, nt, ksub, sn>), grid, dim3(256), 0, (hipStream_t)stream, A8_CONV_ARGS)
 #define A8_CONV_NT(wm, ksub, sn)                 \
