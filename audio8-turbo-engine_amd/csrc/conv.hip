@@ -67,6 +67,8 @@ __device__ __forceinline__ u32x4 snake8(u32x4 v, const float *a, const float *ib
   return o;
 }
 
+constexpr int kSnakeMaxC = 1024;  // input channels a conv with the snake on its loads may have
+
 template <int WM, int NT, int KSUB, bool SNAKE>
 __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__ x, int64_t s_xb, int64_t s_xt,
                                                  const uint16_t *__restrict__ w, int64_t s_wp, int64_t s_wt,
@@ -128,13 +130,26 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
   auto load_x = [&](int s, int i, int u) __attribute__((always_inline)) -> u32x4 {
     const int j = s / kchunks, k0 = (s - j * kchunks) * KS + 32 * u;
     const bool ok = mv[i] && k0 + 8 * g < Cin;
-    const u32x4 v = bld16(xr, ok ? xoff[i] + (uint32_t)(((int64_t)j * dil * s_xt + k0) * 2) : kOob);
+    return bld16(xr, ok ? xoff[i] + (uint32_t)(((int64_t)j * dil * s_xt + k0) * 2) : kOob);
+  };
+  // The snake runs where an operand is used, not where it is loaded (applied at the load it would wait
+  // for the load at once and undo the prefetch); its vectors are staged in LDS once per workgroup
+  // (visible after the first step's barrier).
+  __shared__ __attribute__((aligned(16))) float sabl[SNAKE ? 2 * kSnakeMaxC : 4];
+  if (SNAKE)
+    for (int c = tid; c < Cin; c += 256) {
+      sabl[c] = sa[c];
+      sabl[kSnakeMaxC + c] = sib[c];
+    }
+  auto operand = [&](u32x4 v, int s, int u) __attribute__((always_inline)) -> u32x4 {
     if (!SNAKE) return v;
+    const int j = s / kchunks, k0 = (s - j * kchunks) * KS + 32 * u;
     // snake(0) = 0: lanes that read zeros stay zero, so their snake vectors may be any in-range entries
-    const int kc = ok ? k0 + 8 * g : 0;
+    const int kc = k0 + 8 * g < Cin ? k0 + 8 * g : 0;
     float a[8], ib[8];
-    const f32x4 a0 = *reinterpret_cast<const f32x4 *>(sa + kc), a1 = *reinterpret_cast<const f32x4 *>(sa + kc + 4);
-    const f32x4 i0 = *reinterpret_cast<const f32x4 *>(sib + kc), i1 = *reinterpret_cast<const f32x4 *>(sib + kc + 4);
+    const f32x4 a0 = *reinterpret_cast<const f32x4 *>(sabl + kc), a1 = *reinterpret_cast<const f32x4 *>(sabl + kc + 4);
+    const f32x4 i0 = *reinterpret_cast<const f32x4 *>(sabl + kSnakeMaxC + kc);
+    const f32x4 i1 = *reinterpret_cast<const f32x4 *>(sabl + kSnakeMaxC + kc + 4);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       a[q] = a0[q];
@@ -171,15 +186,19 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
       for (int u = 0; u < KSUB; ++u) xnext[i][u] = load_x(s1, i, u);
     __syncthreads();  // slice s is in wl[cb]; every wave is done with wl[nb] (slice s - 1)
 #pragma unroll
-    for (int u = 0; u < KSUB; ++u)
+    for (int u = 0; u < KSUB; ++u) {
+      u32x4 xo[WM];
+#pragma unroll
+      for (int i = 0; i < WM; ++i) xo[i] = operand(xcur[i][u], s, u);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const uint16_t *ap = ard + cb + 32 * u * BNP + 16 * nt;
         const u32x2 lo = lds_tr16(ap), hi = lds_tr16(ap + 4 * BNP);
         const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int i = 0; i < WM; ++i) acc[i][nt] = mfma16x16x32_f16(a, xcur[i][u], acc[i][nt]);
+        for (int i = 0; i < WM; ++i) acc[i][nt] = mfma16x16x32_f16(a, xo[i], acc[i][nt]);
       }
+    }
 #pragma unroll
     for (int q = 0; q < WCH; ++q) st16(wl + nb + wk[q] * BNP + wn[q], wreg[q]);
 #pragma unroll
@@ -354,6 +373,8 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
   if ((int64_t)TR + (int64_t)(taps - 1) * dil > Tin)
     return set_error(A8_EINVAL, "conv_cl: %d input rows, %d needed", Tin, TR + (taps - 1) * dil);
   if (Cin % 8) return set_error(A8_EUNSUP, "conv_cl: Cin %d not a multiple of 8", Cin);
+  if (snake_a && Cin > kSnakeMaxC)
+    return set_error(A8_EUNSUP, "conv_cl: the snake on the load takes Cin <= %d (got %d; use snake_cat)", kSnakeMaxC, Cin);
   if (B == 0 || TR == 0) return 0;
   if (!x || !w || !y || (snake_a != nullptr) != (snake_ib != nullptr))
     return set_error(A8_EINVAL, "conv_cl: null pointer");

@@ -294,7 +294,8 @@ int a8_silu_mul(const void *gu, int64_t s_gu, void *y, int64_t s_y, int rows, in
  *   y[b, t*ph + p, n] = bias[n] + sum_{j < taps} sum_k x[b, t + j*dil, k] w[p, j, k, n] (+ res[b, t*ph + p, n]),
  *   n < Cout; x [B, Tin, Cin] (Tin >= TR + (taps-1) dil, Cin a multiple of 8), w [ph, taps, Cin, cout_w]
  *   (cout_w >= Cout, a multiple of 8; last dim contiguous), bias [Cout] or NULL, res like y or NULL.
- *   snake_a / snake_ib (fp32 [Cin]) or NULL: x -> x + ib sin(a x)^2 (fp16) on the load. fp32 accumulation.
+ *   snake_a / snake_ib (fp32 [Cin]) or NULL: x -> x + ib sin(a x)^2 (fp16) on the load (Cin <= 1024;
+ *   wider inputs take snake_cat first). fp32 accumulation.
  *   ws / ws_bytes: an optional 16-byte aligned device workspace; with a8_conv_cl_ws_bytes(...) bytes the
  *   kernel may split K across workgroups (fixed-order fp32 sums: the same result with or without it).
  * a8_conv_cl_ws_bytes: the workspace a8_conv_cl would use for these sizes (0: none). No counterpart in the
