@@ -17,11 +17,12 @@
 //   * X rows are the B operands straight from global memory (lane l: 16 contiguous bytes of row l % 16 at
 //     channel offset 8 (l / 16)), with the snake applied in registers;
 //   * each KS x BN weight slice [k][n] (KS = 64 channels, or 32 when Cin is not a multiple of 64) is staged
-//     once in LDS (KS NT / 128 16-byte loads per thread) and read as the A operand with ds_read_b64_tr_b16
+//     once in LDS and read as the A operand with ds_read_b64_tr_b16
 //     (the LDS unit transposes 4 x 16 blocks), so W^T needs no copy;
 //     one A operand feeds WM MFMAs;
-//   * two LDS slices: the next slice's loads are issued before the current slice's MFMAs and written to the
-//     idle slice after them; one barrier a slice;
+//   * two LDS slice areas filled by DMA (buffer_load ... lds), the next slice's DMA and X loads issued
+//     right after the barrier that frees its area, before the current slice's MFMAs; one barrier a slice
+//     and no register copies between steps;
 //   * the tile shape is chosen per launch (conv_plan): the fewest padded output channels, then, among shapes
 //     that give >= 512 workgroups, two row tiles per wave and the widest tile; narrow tiles for short inputs;
 //   * short inputs with long K (the decoder's first blocks: a few hundred rows x 5-7 K channels) split K
@@ -85,9 +86,16 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
   // apart: the 16 rows one transposing read touches then fall on distinct bank groups (at a pitch of BN,
   // a multiple of 64 elements, they all hit the same 8 banks: 4x the LDS cycles, measured as bank conflicts)
   constexpr int BNP = BN + 16;
-  __shared__ __attribute__((aligned(16))) uint16_t wl[2 * KS * BNP];
+  // A slice goes from memory into LDS by DMA (buffer_load ... lds: one instruction fills 64 consecutive
+  // 16-byte chunks): chunk c of a slice is k row c / RC, column chunk c % RC, the last two chunks of a row
+  // being the padding. Each wave issues R instructions a slice, so the slice area is rounded up to R * 256
+  // chunks (the chunks past the slice and the padding receive zeros). Two slice areas as two arrays: the
+  // compiler then tells their DMA completions apart.
+  constexpr int RC = NCH + 2, R = (KS * RC + 255) / 256, SL = R * 256 * 8;
+  __shared__ __attribute__((aligned(16))) uint16_t wlA[SL];
+  __shared__ __attribute__((aligned(16))) uint16_t wlB[SL];
   const int p = blockIdx.z / ksplit, ks = blockIdx.z - p * ksplit, m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g = lane >> 4;
   // Operand loads are buffer loads with the range check as the mask (an invalid lane asks for offset
   // kOob and reads zeros): no branch around a load, so the compiler's wait before the MFMAs covers only
@@ -106,26 +114,27 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
     mt[i] = mv[i] ? m - mb[i] * TR : 0;
     xoff[i] = (uint32_t)(((int64_t)mb[i] * s_xb + (int64_t)mt[i] * s_xt + 8 * g) * 2);
   }
-  // this thread's share of a weight slice: 16-byte chunks c = tid + 256 q, at k row c / NCH, column 8 (c % NCH)
-  int wk[WCH], wn[WCH];
-  bool wcol[WCH];
-  uint32_t wb[WCH];
+  // this lane's chunk of each of the wave's R DMA instructions: c = (4 r + wave) 64 + lane
+  int wk[R];
+  uint32_t wb[R];
 #pragma unroll
-  for (int q = 0; q < WCH; ++q) {
-    const int c = tid + 256 * q;
-    wk[q] = c / NCH;
-    wn[q] = 8 * (c % NCH);
-    wcol[q] = n0 + wn[q] < CoutW;
-    wb[q] = (uint32_t)(((int64_t)p * s_wp + (int64_t)wk[q] * s_wc + n0 + wn[q]) * 2);
+  for (int r = 0; r < R; ++r) {
+    const int c = (4 * r + wv) * 64 + lane, kr = c / RC, cc = c - kr * RC;
+    const bool ok = kr < KS && cc < NCH && n0 + 8 * cc < CoutW;
+    wk[r] = ok ? kr : Cin;  // a chunk that is never valid gets a k row past every slice
+    wb[r] = ok ? (uint32_t)(((int64_t)p * s_wp + (int64_t)kr * s_wc + n0 + 8 * cc) * 2) : 0u;
   }
   // this workgroup's k slices: [sb, se) of taps * ceil(Cin / KS) (a 1 / ksplit share under split-K)
   const int kchunks = (Cin + KS - 1) / KS, steps = taps * kchunks;
   const int sb = (int)((int64_t)steps * ks / ksplit), se = (int)((int64_t)steps * (ks + 1) / ksplit);
 
-  auto load_w = [&](int s, int q) __attribute__((always_inline)) -> u32x4 {
+  // slice s of the weights into LDS area dst (the slice's uniform offset goes in soffset)
+  auto issue_w = [&](int s, uint16_t *dst) __attribute__((always_inline)) {
     const int j = s / kchunks, k0 = (s - j * kchunks) * KS;
-    const bool ok = wcol[q] && k0 + wk[q] < Cin;
-    return bld16(wr, ok ? wb[q] + (uint32_t)(((int64_t)j * s_wt + (int64_t)k0 * s_wc) * 2) : kOob);
+    const uint32_t so = (uint32_t)(((int64_t)j * s_wt + (int64_t)k0 * s_wc) * 2);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      bld16_lds<0>(wr, dst + (4 * r + wv) * 512, k0 + wk[r] < Cin ? wb[r] : kOob, so);
   };
   auto load_x = [&](int s, int i, int u) __attribute__((always_inline)) -> u32x4 {
     const int j = s / kchunks, k0 = (s - j * kchunks) * KS + 32 * u;
@@ -166,46 +175,54 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[i][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
   // A-operand reads: rows (k) 8g + r16/4 (+4), columns (n) 16 nt + 4 (r16 % 4)
-  const uint16_t *ard = wl + (8 * g + (r16 >> 2)) * BNP + 4 * (r16 & 3);
-  u32x4 wreg[WCH], xcur[WM][KSUB], xnext[WM][KSUB];
-#pragma unroll
-  for (int q = 0; q < WCH; ++q) st16(wl + wk[q] * BNP + wn[q], load_w(sb, q));
+  const int aoff = (8 * g + (r16 >> 2)) * BNP + 4 * (r16 & 3);
+  u32x4 xa[WM][KSUB], xb[WM][KSUB];
+  issue_w(sb, wlA);
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int u = 0; u < KSUB; ++u) xcur[i][u] = load_x(sb, i, u);
-  for (int s = sb; s < se; ++s) {
-    const int cb = ((s - sb) & 1) * KS * BNP, nb = KS * BNP - cb;
-    // the next slice's loads (the last step reloads its own slice into the idle buffer: no branch)
+    for (int u = 0; u < KSUB; ++u) xa[i][u] = load_x(sb, i, u);
+  // One k slice s, its weights in `cur` (DMA issued one step earlier) and its X operands in xc (loaded one
+  // step earlier): wait for this wave's DMA of the slice (the X loads issued after it may still fly), the
+  // barrier (every wave's DMA landed; every wave is done with `nxt`, slice s - 1), the DMA of slice s + 1
+  // into `nxt` and its X loads into xn (the last step reloads its own slice: no branch), then the MFMAs.
+  // No register copies between steps: loads stay in flight until their first use.
+  auto step = [&](int s, u32x4(&xc)[WM][KSUB], u32x4(&xn)[WM][KSUB], const uint16_t *cur,
+                  uint16_t *nxt) __attribute__((always_inline)) {
+    constexpr int nx = WM * KSUB;  // X loads issued after a slice's DMA
+    static_assert(nx < 16, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | nx);  // s_waitcnt vmcnt(nx)
+    __syncthreads();
     const int s1 = s + 1 < se ? s + 1 : s;
-#pragma unroll
-    for (int q = 0; q < WCH; ++q) wreg[q] = load_w(s1, q);
+    issue_w(s1, nxt);
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
-      for (int u = 0; u < KSUB; ++u) xnext[i][u] = load_x(s1, i, u);
-    __syncthreads();  // slice s is in wl[cb]; every wave is done with wl[nb] (slice s - 1)
+      for (int u = 0; u < KSUB; ++u) xn[i][u] = load_x(s1, i, u);
 #pragma unroll
     for (int u = 0; u < KSUB; ++u) {
       u32x4 xo[WM];
 #pragma unroll
-      for (int i = 0; i < WM; ++i) xo[i] = operand(xcur[i][u], s, u);
+      for (int i = 0; i < WM; ++i) xo[i] = operand(xc[i][u], s, u);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        const uint16_t *ap = ard + cb + 32 * u * BNP + 16 * nt;
+        const uint16_t *ap = cur + aoff + 32 * u * BNP + 16 * nt;
         const u32x2 lo = lds_tr16(ap), hi = lds_tr16(ap + 4 * BNP);
         const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int i = 0; i < WM; ++i) acc[i][nt] = mfma16x16x32_f16(a, xo[i], acc[i][nt]);
       }
     }
-#pragma unroll
-    for (int q = 0; q < WCH; ++q) st16(wl + nb + wk[q] * BNP + wn[q], wreg[q]);
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-      for (int u = 0; u < KSUB; ++u) xcur[i][u] = xnext[i][u];
+  };
+  int s = sb;
+  for (; s + 1 < se; s += 2) {
+    step(s, xa, xb, wlA, wlB);
+    step(s + 1, xb, xa, wlB, wlA);
   }
+  if (s < se) step(s, xa, xb, wlA, wlB);
+  // the DMA issued by the last step (its own slice again) still writes LDS: let it land before the
+  // workgroup ends. s_waitcnt vmcnt(0).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   // acc[i][nt]: lane (r16, g) holds Y[row m0 + (wv WM + i) 16 + r16][n = n0 + 16 nt + 4g + e], e = 0..3
   if (part) {  // split-K: raw fp32 sums to part[ks][p][m][n], row pitch gridDim.y BN; k_conv_fin finishes
     const int64_t NP = (int64_t)gridDim.y * BN;
