@@ -16,7 +16,7 @@
 // WM row tiles of 16 x BN on v_mfma_f32_16x16x32_f16, as Y^T = W^T . X^T:
 //   * X rows are the B operands straight from global memory (lane l: 16 contiguous bytes of row l % 16 at
 //     channel offset 8 (l / 16)), with the snake applied in registers;
-//   * each KS x BN weight slice [k][n] (KS = 64 channels, or 32 when Cin is not a multiple of 64) is staged
+//   * each KS x BN weight slice [k][n] (KS = 64 channels, else 96, else 32, whichever divides Cin) is staged
 //     once in LDS and read as the A operand with ds_read_b64_tr_b16
 //     (the LDS unit transposes 4 x 16 blocks), so W^T needs no copy;
 //     one A operand feeds WM MFMAs;
@@ -334,20 +334,23 @@ __global__ __launch_bounds__(256) void k_snake_cat(const uint16_t *__restrict__ 
 
 static inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
-// The launch shape of one conv: BN = 16 NT output channels and BM = 64 WM rows (NT in 4, 8, 12, 16; WM in
+// The launch shape of one conv: BN = 16 NT output channels and BM = 64 WM rows (NT in 4, 6, 8, 12, 16; WM in
 // 1, 2) as conv_plan ranks them (four row tiles per wave measured slower: fewer waves per SIMD); k slices of
-// 64 channels when Cin allows, else 32; when fewer than 512 workgroups remain over a K of >= 16 slices (the decoder's early, short blocks), K is split into up to 16
-// shares of >= 8 slices, summed in fixed order by k_conv_fin from an fp32 workspace.
+// 64 channels when Cin allows, else 96, else 32; when fewer than 512 workgroups remain over a K of >= 16
+// slices (the decoder's early, short blocks), K is split into up to 16 shares of >= 8 slices, summed in fixed
+// order by k_conv_fin from an fp32 workspace.
 struct ConvPlan {
   int NT, WM, KSUB, ksplit;
   int64_t ntiles, ws_bytes;
 };
 static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph) {
-  ConvPlan pl{16, 1, Cin % 64 == 0 ? 2 : 1, 1, 0, 0};
+  // 96-channel slices only where K has several of them (a 1x1 conv of 96 channels would be one step with
+  // nothing to overlap: measured slower than three 32-channel steps)
+  ConvPlan pl{16, 1, Cin % 64 == 0 ? 2 : (Cin % 96 == 0 && taps > 1) ? 3 : 1, 1, 0, 0};
   // (NT, WM) candidates: the fewest padded columns; then, among shapes that fill the chip (>= 512
   // workgroups), the most row tiles per wave (each LDS weight read feeds WM MFMAs), then the widest tile;
   // when none fills it, the most workgroups
-  static const int cand[][2] = {{16, 2}, {16, 1}, {12, 2}, {12, 1}, {8, 2}, {8, 1}, {4, 2}, {4, 1}};
+  static const int cand[][2] = {{16, 2}, {16, 1}, {12, 2}, {12, 1}, {8, 2}, {8, 1}, {6, 2}, {6, 1}, {4, 2}, {4, 1}};
   int64_t best_cols = INT64_MAX, best_wgs = 0;
   int best_wm = 0;
   for (const auto &c : cand) {
@@ -422,6 +425,7 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
 #define A8_CONV_NT(wm, ksub, sn)                 \
   switch (NT) {                                  \
     case 4: A8_CONV_L(wm, 4, ksub, sn); break;   \
+    case 6: A8_CONV_L(wm, 6, ksub, sn); break;   \
     case 8: A8_CONV_L(wm, 8, ksub, sn); break;   \
     case 12: A8_CONV_L(wm, 12, ksub, sn); break; \
     default: A8_CONV_L(wm, 16, ksub, sn); break; \
@@ -429,6 +433,8 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
 #define A8_CONV_K(wm, sn)         \
   if (pl.KSUB == 2) {             \
     A8_CONV_NT(wm, 2, sn)         \
+  } else if (pl.KSUB == 3) {      \
+    A8_CONV_NT(wm, 3, sn)         \
   } else {                        \
     A8_CONV_NT(wm, 1, sn)         \
   }
