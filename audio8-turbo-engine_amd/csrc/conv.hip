@@ -364,6 +364,19 @@ static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph) {
     else better = wgs > best_wgs;
     if (better) best_cols = cols, best_wgs = wgs, best_wm = wm, pl.NT = nt, pl.WM = wm;
   }
+  // multi-tap convs on short inputs (the decoder's input conv and first block): a wide two-row-tile shape
+  // with K split across workgroups beat the narrow tile that fills the chip by itself (block 0's k=7
+  // convs 138 -> 97 us); the two-tap transposed convs did not gain (87 -> 96 us) and keep the narrow tile
+  if (taps > 2 && pl.NT * pl.WM < 16 && best_wgs < 1024) {
+    for (int nt : {12, 8, 16}) {
+      const int64_t nti = (Cout + 16 * nt - 1) / (16 * nt);
+      if (nti * 16 * nt != best_cols) continue;
+      pl.NT = nt;
+      pl.WM = 2;
+      best_wgs = ((M + 127) / 128) * nti * ph;
+      break;
+    }
+  }
   pl.ntiles = (Cout + 16 * pl.NT - 1) / (16 * pl.NT);
   const int64_t wgs = best_wgs;
   const int steps = taps * ((Cin + 32 * pl.KSUB - 1) / (32 * pl.KSUB));
