@@ -293,6 +293,9 @@ def test_conv_ops_reject_before_launch(a8):
     assert lib.a8_conv_cl(*{**conv, "Cin": 60}.values()) == -3          # channels in 16-byte chunks
     assert lib.a8_conv_cl(*{**conv, "cout_w": 32}.values()) == -1       # the weights hold fewer columns
     assert lib.a8_conv_cl(*{**conv, "sa": 16}.values()) == -1           # snake needs both vectors
+    assert lib.a8_conv_cl(*{**conv, "sa": 16, "sib": 16, "Cin": 1032, "s_xt": 1032, "s_wt": 1032 * 64,
+                            "s_xb": 10 * 1032}.values()) == -3               # snake on the load: Cin <= 1024
+    assert b"snake" in lib.a8_last_error()
     assert lib.a8_conv_cl(*{**conv, "x": 24}.values()) == -2
     assert lib.a8_conv_cl(*{**conv, "TR": 0, "Tin": 6}.values()) == 0
     # split-K workspace: short inputs with long K get one, long inputs none
