@@ -39,6 +39,10 @@ def _close(got, want):
     (8, 128, 96, 1, 16, 7, 1, 1, True, False, False),         # one-channel output conv (padded weights)
     (3, 5, 8, 24, 32, 3, 2, 3, False, True, True),            # ragged: one k chunk, Cout 24, 15 rows
     (4, 8, 512, 30, 32, 7, 1, 1, True, True, True),           # split K with Cout 30 (no 4-channel vectors)
+    (64, 1024, 192, 192, 192, 1, 1, 1, True, True, True),     # long pointwise convs (block 2's shape)
+    (65, 1009, 96, 96, 96, 1, 1, 1, True, True, True),        #   (ragged last tile)
+    (64, 1100, 96, 24, 32, 1, 1, 1, False, True, False),      #   (Cout 24, no bias, no snake)
+    (64, 1030, 192, 70, 80, 1, 1, 1, True, False, True),      #   (Cout 70: element stores)
 ])
 def test_conv_cl_shapes(a8, cref, dev, B, T, Cin, Cout, cw, taps, dil, ph, bias, res, snake):
     say(f"case: conv_cl B={B} T={T} Cin={Cin} Cout={Cout} taps={taps} dil={dil} ph={ph} bias={bias} res={res} "
