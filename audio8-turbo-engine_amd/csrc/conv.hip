@@ -337,8 +337,9 @@ static inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) 
 // The launch shape of one conv: BN = 16 NT output channels and BM = 64 WM rows (NT in 4, 6, 8, 12, 16; WM in
 // 1, 2) as conv_plan ranks them (four row tiles per wave measured slower: fewer waves per SIMD); k slices of
 // 64 channels when Cin allows, else 96, else 32; when fewer than 512 workgroups remain over a K of >= 16
-// slices (the decoder's early, short blocks), K is split into up to 16 shares of >= 8 slices, summed in fixed
-// order by k_conv_fin from an fp32 workspace.
+// slices (the decoder's early, short blocks), K is split into enough shares for ~512 workgroups (at most 16,
+// each >= 8 slices; fewer shares than 1024 workgroups' worth measured faster: less workspace to finish),
+// summed in fixed order by k_conv_fin from an fp32 workspace.
 struct ConvPlan {
   int NT, WM, KSUB, ksplit;
   int64_t ntiles, ws_bytes;
@@ -381,7 +382,7 @@ static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph) {
   const int64_t wgs = best_wgs;
   const int steps = taps * ((Cin + 32 * pl.KSUB - 1) / (32 * pl.KSUB));
   if (wgs < 512 && steps >= 16 && (int64_t)ph * M * ((Cout + 3) / 4) < ((int64_t)1 << 31)) {
-    int64_t k = (1024 + wgs - 1) / wgs;
+    int64_t k = (512 + wgs - 1) / wgs;
     k = k < steps / 8 ? k : steps / 8;
     k = k < 16 ? k : 16;
     if (k > 1) {
