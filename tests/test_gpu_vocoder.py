@@ -67,3 +67,39 @@ def test_rows_are_independent(dev):
     assert torch.equal(y[1], fresh[1])
     assert torch.equal(y[0], yc[0]) and torch.equal(y[2], yc[2])
     assert not torch.equal(y[0], fresh[0])
+
+
+def test_decoder_graph_replay_equals_eager(dev):
+    """The decoder captured once as a graph (its split-K workspaces and activations from the graph's pool) and
+    replayed frame after frame, with the program's own eager work between replays, gives the same bits as
+    the eager decoder fed the same frames (fast_engine.py:744-768 captures the vocoder step in the tick)."""
+    say("case: CLDecoder graph capture (256 channels: the input conv splits K), 4 replays vs eager")
+    voc = importlib.import_module("audio8-turbo-engine_amd.vocoder")
+    wts = voc.decoder_weights(cin=256, ch=256, rates=(2, 2), k=7, dils=(1, 3, 9), dev="cpu", seed=4)
+    lib = importlib.import_module("audio8-turbo-engine_amd").load_library()
+    assert lib.a8_conv_cl_ws_bytes(3, 2, 256, 256, 7, 1) > 0          # the input conv takes the split-K path
+    wd = {"conv_in": tuple(t.to(dev) for t in wts["conv_in"]),
+          "blocks": [(a.to(dev), w.to(dev), b.to(dev), s, [tuple(t.to(dev) if torch.is_tensor(t) else t for t in u)
+                                                          for u in us]) for a, w, b, s, us in wts["blocks"]],
+          "final": tuple(t.to(dev) for t in wts["final"])}
+    B = 3
+    dec_g, dec_e = voc.CLDecoder(wd, B, dev), voc.CLDecoder(wd, B, dev)
+    xs = torch.zeros(B, 2, 256, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        dec_g(xs, B)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        yg = dec_g(xs, B)
+    rows = torch.arange(B, device=dev)
+    dec_g.reset_rows(rows)
+    gen = torch.Generator(device=dev).manual_seed(12)
+    for f in range(4):
+        x = torch.randn(B, 2, 256, generator=gen, device=dev)
+        xs.copy_(x)
+        graph.replay()
+        ye = dec_e(x, B)
+        torch.cuda.synchronize()
+        assert torch.equal(yg, ye), f"frame {f}"
