@@ -1,4 +1,5 @@
-"""Benchmark of the MI355X attention hot path: BASELINE.json's metric on its peak-load config.
+"""Benchmark of the MI355X attention hot path: the headline metric (decode-attention µs per layer and achieved HBM
+GB/s) on its peak-load config.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu-baseline]
 
@@ -138,7 +139,7 @@ def cpu_baseline(w, budget_s):
 
 
 def per_config(a8, torch, dev, steps):
-    """µs per layer (per pass at C5), achieved GB/s or TFLOP/s and the roofline fraction of the other BASELINE
+    """µs per layer (per pass at C5), achieved GB/s or TFLOP/s and the roofline fraction of the other benchmark
     configs, each timed as a captured graph (median of 5 runs). Decode configs: store + decode per layer, the
     engine's calls (fused where the schedule allows). C4: store + packed prefill per layer, and the prefill
     launch alone against the bf16 MFMA peak."""

@@ -1,5 +1,5 @@
 """GPU parity of split-K decode attention (DecodeAttention -> a8_decode_attn) against the golden vectors and
-the CPU oracle at every BASELINE config's shape, over launch shapes, row maps, strides and edge lengths.
+the CPU oracle at every benchmark config's shape (C1-C5), over launch shapes, row maps, strides and edge lengths.
 Bar: max-abs <= 2e-2 on the bf16 outputs (fp32 softmax / accumulate, bf16 out)."""
 from __future__ import annotations
 
@@ -45,7 +45,7 @@ def test_decode_golden(a8, dev):
 
 
 def _cfg(name, g):
-    """(q, kc, vc, lens, rowmap, nsplit_max) at a BASELINE config's shape (one layer)."""
+    """(q, kc, vc, lens, rowmap, nsplit_max) at a benchmark config's shape (one layer)."""
     if name == "C1":
         b, rows, S = 1, 1, 512
         lens = torch.tensor([385])
