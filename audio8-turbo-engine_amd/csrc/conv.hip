@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
                                                  float *__restrict__ part, int ksplit, uint32_t x_span,
                                                  uint32_t w_span) {
   warm_kernargs<180>();  // the explicit arguments above span 0x00-0xb3
-  constexpr int BN = 16 * NT, BM = 64 * WM, KS = 32 * KSUB, WCH = NT / 4 * KSUB, NCH = BN / 8;
+  constexpr int BN = 16 * NT, BM = 64 * WM, KS = 32 * KSUB, NCH = BN / 8;
   // two weight slices [k][n] (KS x BN): one is read while the next is written. A k row is BN + 16 elements
   // apart: the 16 rows one transposing read touches then fall on distinct bank groups (at a pitch of BN,
   // a multiple of 64 elements, they all hit the same 8 banks: 4x the LDS cycles, measured as bank conflicts)
