@@ -337,8 +337,8 @@ static inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) 
 // The launch shape of one conv: BN = 16 NT output channels and BM = 64 WM rows (NT in 4, 6, 8, 12, 16; WM in
 // 1, 2) as conv_plan ranks them (four row tiles per wave measured slower: fewer waves per SIMD); k slices of
 // 64 channels when Cin allows, else 96, else 32; when fewer than 512 workgroups remain over a K of >= 16
-// slices (the decoder's early, short blocks), K is split into enough shares for ~512 workgroups (at most 16,
-// each >= 8 slices; fewer shares than 1024 workgroups' worth measured faster: less workspace to finish),
+// slices (the decoder's early, short blocks), K is split into enough shares for ~512 workgroups (at most 6,
+// each >= 8 slices; fewer shares measured faster: less workspace to finish),
 // summed in fixed order by k_conv_fin from an fp32 workspace.
 struct ConvPlan {
   int NT, WM, KSUB, ksplit;
@@ -365,10 +365,10 @@ static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph) {
     else better = wgs > best_wgs;
     if (better) best_cols = cols, best_wgs = wgs, best_wm = wm, pl.NT = nt, pl.WM = wm;
   }
-  // multi-tap convs on short inputs (the decoder's input conv and first block): a wide two-row-tile shape
-  // with K split across workgroups beat the narrow tile that fills the chip by itself (block 0's k=7
-  // convs 138 -> 97 us); the two-tap transposed convs did not gain (87 -> 96 us) and keep the narrow tile
-  if (taps > 2 && pl.NT * pl.WM < 16 && best_wgs < 1024) {
+  // multi-tap convs and many-phase transposed convs on short inputs (the decoder's input conv and first
+  // block): a wide two-row-tile shape with K split across workgroups beat the narrow tile that fills the
+  // chip by itself (block 0's k=7 convs 138 -> 93 us, its stride-8 transposed conv 87 -> 77 us)
+  if ((taps > 2 || ph >= 8) && pl.NT * pl.WM < 16 && best_wgs < 1024) {
     for (int nt : {12, 8, 16}) {
       const int64_t nti = (Cout + 16 * nt - 1) / (16 * nt);
       if (nti * 16 * nt != best_cols) continue;
@@ -384,7 +384,7 @@ static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph) {
   if (wgs < 512 && steps >= 16 && (int64_t)ph * M * ((Cout + 3) / 4) < ((int64_t)1 << 31)) {
     int64_t k = (512 + wgs - 1) / wgs;
     k = k < steps / 8 ? k : steps / 8;
-    k = k < 16 ? k : 16;
+    k = k < 6 ? k : 6;  // more shares measured slower (the input conv: 11 shares 58 us, 6 shares 51 us)
     if (k > 1) {
       pl.ksplit = (int)k;
       pl.ws_bytes = k * ph * M * pl.ntiles * 16 * pl.NT * 4;
