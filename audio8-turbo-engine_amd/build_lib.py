@@ -1,7 +1,7 @@
 """Builds the gfx950 HIP library behind the C ABI (include/a8attn.h) into this package, in-tree.
 
 `python build_lib.py` (or `__graft_entry__.build()`) compiles every source in csrc/ with hipcc for
-gfx950 only and links one shared library, `liba8attn.so`, next to this file. The library links the
+gfx950 only (objects in _build/, one compiler process per source) and links one shared library, `liba8attn.so`, next to this file. The library links the
 HIP runtime by soname (libamdhip64.so.7), so inside a process that has imported torch it binds to
 the runtime torch already loaded and shares its streams and graphs.
 """
@@ -14,7 +14,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liba8attn.so")
-SOURCES = ["capi.hip", "store.hip", "decode.hip", "decode_stream.hip", "decode_flat.hip", "prefill.hip",
+SOURCES = ["capi.hip", "store.hip", "decode.hip", "decode_stream.hip", "decode_rows.hip", "decode_flat.hip", "prefill.hip",
            "prefix_copy.hip", "layer_ops.hip", "conv.hip"]
 
 HIPCC_FLAGS = [
@@ -37,21 +37,46 @@ def hipcc() -> str:
     return path if os.path.exists(path) else "hipcc"
 
 
-def build(verbose: bool = False, extra_flags=None) -> str:
-    """Compile csrc/*.hip for gfx950 into liba8attn.so (always rebuilds). Returns the library path."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, *(extra_flags or []), *srcs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
+def _run(cmd):
     res = subprocess.run(cmd, capture_output=True, text=True)
     # the host pass warns about the device-only feature flag; anything else is worth showing
     noise = "'-packed-fp32-ops' is not a recognized feature for this target (ignoring feature)"
     msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln and ln.strip()]
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
-    if msgs and verbose:
-        print("\n".join(msgs))
+    return res.returncode, msgs
+
+
+def build(verbose: bool = False, extra_flags=None, jobs=None) -> str:
+    """Compile csrc/*.hip for gfx950 (one hipcc per source, in parallel) and link liba8attn.so (always
+    rebuilds). Returns the library path."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"] + list(extra_flags or [])
+    jobs = jobs or max(1, min(len(SOURCES), os.cpu_count() or 1, 16))
+
+    def compile_one(src):
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        cmd = [hipcc(), *flags, "-c", os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        return obj, _run(cmd)
+
+    with ThreadPoolExecutor(jobs) as ex:
+        results = list(ex.map(compile_one, SOURCES))
+    objs, errs = [], []
+    for obj, (rc, msgs) in results:
+        objs.append(obj)
+        if rc != 0:
+            errs += msgs
+        elif msgs and verbose:
+            print("\n".join(msgs))
+    if errs:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(errs))
+    tmp = LIB + ".tmp"
+    rc, msgs = _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
+    if rc != 0:
+        raise RuntimeError("link failed:\n" + "\n".join(msgs))
     os.replace(tmp, LIB)
     return LIB
 

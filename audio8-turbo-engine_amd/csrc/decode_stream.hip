@@ -420,6 +420,12 @@ static void launch_stream(int grid, hipStream_t st, const uint16_t *q, int64_t s
 
 static inline bool al16s(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// decode_rows.hip
+bool rows_launch(int grid, hipStream_t st, const uint16_t *q, int64_t s_qb, int64_t s_qh, uint16_t *kc, uint16_t *vc,
+                 int64_t s_kb, int64_t s_kh, int cache_rows, int cache_len, const int32_t *lens, const int32_t *rowmap,
+                 uint16_t *out, int64_t s_ob, int64_t s_oh, int b, int nq, int nkv, int group, float sl2,
+                 const StoreIn &si);
+
 // Body of a8_decode_attn_stream and a8_store_decode_stream (fused = si.qkv != nullptr: q is unused, the
 // store's inputs are in si). Checks the decode arguments, launches the streaming kernel and,
 // for rows longer than a chunk, the merge kernel.
@@ -462,6 +468,12 @@ static int stream_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_q
   auto *kk = (uint16_t *)kc;
   auto *vv = (uint16_t *)vc;
   auto *oo = (uint16_t *)out;
+  // whole rows per workgroup at 4 waves x one tile per step (the peak-load shape): k_decode_rows, same
+  // results bit for bit; phases bit 2 keeps k_decode_stream (for timing the two apart)
+  const bool rows = (phases & 1) && P == 1 && waves == 4 && !(phases & 4) &&
+                    rows_launch(grid, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, cache_rows, cache_len, lens, rowmap, oo,
+                                s_ob, s_oh, b, nq, nkv, group, sl2, si);
+  if (rows) return (int)hipGetLastError();
   if (phases & 1) {
 #define A8_STREAM_ARGS grid, st, qq, s_qb, s_qh, kk, vv, s_kb, s_kh, s_ks, cache_rows, cache_len, lens, rowmap, oo, \
                        s_ob, s_oh, acc_ws, ml_ws, b, nq, nkv, group, tiles_per_wave, P, sl2, si
