@@ -110,13 +110,29 @@ def time_graph(torch, g, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def host_cpu():
+    """(model name, logical CPUs the OS reports) of this host, from /proc/cpuinfo (lscpu's source)."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model, os.cpu_count()
+
+
 def cpu_baseline(w, budget_s):
     """The CPU oracle (torch on the host cores) on one layer of the same workload: store + decode for all
-    slots, repeated until the budget is spent (at least 3 reps); median per layer."""
+    slots, repeated until the budget is spent (at least 3 reps); median per layer. Threads: torch's intra-op
+    pool as the process starts it (OMP_NUM_THREADS when set: on the GPU boxes that is the share of cores a
+    one-GPU job gets, which may be fewer than os.cpu_count() reports); both counts are recorded."""
     import torch
     from oracle import attn_ref as ref
 
-    torch.set_num_threads(torch.get_num_threads())
+    threads = torch.get_num_threads()
     st = w["st"]
     b, S = w["b"], w["S"]
     kc, vc = st.kc[0].cpu(), st.vc[0].cpu()
@@ -133,8 +149,10 @@ def cpu_baseline(w, budget_s):
         times.append(time.perf_counter() - t0)
     per_layer = statistics.median(times)
     nbytes = ref.decode_bytes(w["lens_h"].tolist(), NQ, NKV, HD)
-    return {"value": round(nbytes / per_layer / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port", "us_per_layer": round(per_layer * 1e6, 1),
+    model, ncpu = host_cpu()
+    return {"value": round(nbytes / per_layer / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "us_per_layer": round(per_layer * 1e6, 1), "cpu_model": model, "os_cpu_count": ncpu,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
             "sample": f"1 of {LAYERS} layers (store + decode, {b} slots, same inputs), {len(times)} reps, median"}
 
 
@@ -470,7 +488,8 @@ def main():
     if kind == "stream":
         nw, tpw, grid = shape
         chunks = -(-w["S"] // (nw * tpw * 64))
-        launch = {"kernel": "k_decode_stream" + (" (store fused)" if fused else "") +
+        rows = chunks == 1 and nw == 4  # whole rows per workgroup: the whole-row kernel
+        launch = {"kernel": ("k_decode_rows" if rows else "k_decode_stream") + (" (store fused)" if fused else "") +
                   (" + k_decode_stream_combine" if chunks > 1 else ""), "waves": nw,
                   "tiles_per_wave": tpw, "grid": grid, "chunk_keys": nw * tpw * 64, "chunks_per_row": chunks}
     else:
