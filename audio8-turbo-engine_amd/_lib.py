@@ -29,6 +29,8 @@ SIGNATURES = {
                                 _P, _P, _L, _L, _L, _I, _I, _I, _I, _I, _I, _P]),
     "a8_decode_attn": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _I, _P, _P, _P, _L, _L,
                             _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _F, _I, _P]),
+    "a8_decode_attn_noalloc": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _I, _P, _P, _P, _L, _L,
+                                    _I, _I, _I, _I, _I, _I, _F, _P]),
     "a8_decode_choose": (_I, [_I, _I, _I, _I, _I, _L, _I, _IP, _IP]),
     "a8_decode_attn_stream": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _I, _P, _P, _P, _L, _L,
                                    _P, _P, _L, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P]),

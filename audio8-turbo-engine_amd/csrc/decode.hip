@@ -29,6 +29,8 @@
 // FUSED (a8_store_decode_split): q and the new k / v come from qkv + bias + RoPE (fused_qkv.h, the
 // store kernel's arithmetic) in every workgroup, split 0's first wave writes them to the cache (and q
 // to qo) like k_bias_rope_store, and the tile holding the new key takes it from registers.
+#include <mutex>
+
 #include "decode_tile.h"
 #include "fused_qkv.h"
 
@@ -449,4 +451,80 @@ extern "C" int a8_decode_choose(int b, int nkv, int cache_len, int nsplit_req, i
   *nsplit_out = (int)ns;
   *waves_out = nw_out;
   return 0;
+}
+
+// ---- a8_decode_attn_noalloc: the split + combine launch with its partials in a fixed device array ----
+namespace a8 {
+
+// The split partials (acc [b, nq, nsplit, 64] then ml [b, nq, nsplit, 2], fp32) of a8_decode_attn_noalloc.
+// Every GPU the library runs on holds its own copy from module load until the process ends. Host code never
+// uses the name (on the host it is only a stand-in for the symbol): it uses the address that
+// hipGetSymbolAddress returns for the current device, kept per device in g_scratch_dev.
+constexpr int64_t kScratchFloats = A8_NOALLOC_SCRATCH_BYTES / 4;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+static float *g_scratch_dev[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch` (looked up once per device), or nullptr with the error recorded.
+static float *scratch_on_current_device(const char *fn) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error(A8_EINVAL, "%s: hipGetDevice failed (%d)", fn, (int)e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error(A8_EUNSUP, "%s: device %d beyond the %d supported", fn, dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error(A8_EINVAL, "%s: hipGetSymbolAddress(scratch) failed on device %d (%d)", fn, dev, (int)e);
+      return nullptr;
+    }
+    g_scratch_dev[dev] = static_cast<float *>(p);
+  }
+  return g_scratch_dev[dev];
+}
+
+}  // namespace a8
+
+extern "C" int a8_decode_attn_noalloc(const void *q, int64_t s_qb, int64_t s_qh,
+                                      const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                                      int cache_rows, int cache_len,
+                                      const int32_t *lens, const int32_t *rowmap,
+                                      void *out, int64_t s_ob, int64_t s_oh,
+                                      int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
+                                      void *stream) {
+  using namespace a8;
+  const char *fn = "decode_attn_noalloc";
+  if (b < 0 || nq <= 0 || hd <= 0 || nsplit < 1)
+    return set_error(A8_EINVAL, "%s: bad sizes b=%d nq=%d hd=%d nsplit=%d", fn, b, nq, hd, nsplit);
+  if (b == 0) return 0;
+  float *acc = nullptr, *ml = nullptr;
+  int64_t row_splits = 0;
+  if (nsplit > 1) {
+    // every (row, head, split) partial the combine reads is written by the split kernel first: nothing in
+    // the array has to start at zero
+    const int64_t parts = (int64_t)b * nq * nsplit;
+    const int64_t need = parts * ((int64_t)hd + 2);
+    if (need > kScratchFloats)
+      return set_error(A8_EWSPACE, "%s: b*nq*nsplit*(hd+2) = %lld floats exceed the fixed %lld-float scratch "
+                       "(8 MiB); use a8_decode_attn with a caller workspace", fn, (long long)need,
+                       (long long)kScratchFloats);
+    float *base = scratch_on_current_device(fn);
+    if (!base) return A8_EINVAL;
+    acc = base;
+    ml = base + parts * hd;  // parts * hd floats in: a multiple of 64 floats, 256-byte aligned
+    row_splits = (int64_t)b * nsplit;
+  }
+  const StoreIn none{};
+  return split_entry(fn, q, s_qb, s_qh, const_cast<void *>(kc), const_cast<void *>(vc), s_kb, s_kh, s_ks,
+                     cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc, ml, row_splits, nullptr, 0, b, nq,
+                     nkv, hd, nsplit, waves, scale, 3, none, stream);
 }

@@ -113,6 +113,26 @@ int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
                    int phases, void *stream);
 
 /*
+ * a8_decode_attn without a caller workspace, for callers that cannot allocate device memory (code
+ * being captured into a HIP graph, tight serving loops, harnesses that forbid hipMalloc). No counterpart
+ * in the reference: its DecodeAttention always owns a workspace (fast_kernels.py:256-269).
+ * Same arguments, kernels and results (bit for bit) as a8_decode_attn with counters == NULL and
+ * phases == 3; the split partials go to a fixed device array of A8_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each GPU until the process ends. Allocates nothing. nsplit > 1 needs
+ * b * nq * nsplit * (hd + 2) * 4 <= A8_NOALLOC_SCRATCH_BYTES, else A8_EWSPACE. Every call on one GPU
+ * shares that GPU's array: calls that overlap in time on one GPU (two streams, two host threads) race;
+ * serialise them.
+ */
+#define A8_NOALLOC_SCRATCH_BYTES (8ll << 20)
+int a8_decode_attn_noalloc(const void *q, int64_t s_qb, int64_t s_qh,
+                           const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                           int cache_rows, int cache_len,
+                           const int32_t *lens, const int32_t *rowmap,
+                           void *out, int64_t s_ob, int64_t s_oh,
+                           int b, int nq, int nkv, int hd, int nsplit, int waves, float scale,
+                           void *stream);
+
+/*
  * Launch-shape policy for a8_decode_attn on this GPU: picks (nsplit, waves) so that
  * b * nkv * nsplit workgroups fill n_cu compute units for keys up to cache_len.
  * nsplit_req is the caller's request (the reference's per-bucket heuristic, fast_engine.py:776):

@@ -21,7 +21,7 @@ def declared_functions():
 
 def test_header_declares_the_entry_points():
     assert set(declared_functions()) == {"a8_version", "a8_last_error", "a8_hip_runtime_path", "a8_bias_rope_store",
-                                         "a8_decode_attn", "a8_decode_choose", "a8_decode_attn_stream",
+                                         "a8_decode_attn", "a8_decode_attn_noalloc", "a8_decode_choose", "a8_decode_attn_stream",
                                          "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn",
                                          "a8_decode_attn_flat", "a8_decode_choose_flat", "a8_store_decode_flat",
                                          "a8_store_decode_split", "a8_prefix_copy", "a8_rmsnorm", "a8_silu_mul",
