@@ -31,6 +31,20 @@ HIPCC_FLAGS = [
 ]
 
 
+def source_hash() -> str:
+    """A short hash of every source the library is built from (csrc/ and include/a8attn.h); the build bakes it
+    into a8_version(), so a library older than its sources can be told apart."""
+    import hashlib
+    h = hashlib.sha1()
+    inc = os.path.join(os.path.dirname(HERE), "include", "a8attn.h")
+    for p in sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC)) + [inc]:
+        if os.path.isfile(p):
+            h.update(os.path.basename(p).encode())
+            with open(p, "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:12]
+
+
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     path = os.path.join(rocm, "bin", "hipcc")
@@ -52,7 +66,7 @@ def build(verbose: bool = False, extra_flags=None, jobs=None) -> str:
 
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    flags = [f for f in HIPCC_FLAGS if f != "-shared"] + list(extra_flags or [])
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"] + list(extra_flags or []) + [f'-DA8_SRC_HASH="{source_hash()}"']
     jobs = jobs or max(1, min(len(SOURCES), os.cpu_count() or 1, 16))
 
     def compile_one(src):

@@ -19,7 +19,11 @@ int set_error(int code, const char *fmt, ...) {
 
 }  // namespace a8
 
-extern "C" const char *a8_version(void) { return "a8attn 0.1.0 gfx950"; }
+#ifndef A8_SRC_HASH
+#define A8_SRC_HASH "unknown"
+#endif
+// "a8attn <version> gfx950 src:<hash of the sources it was built from>"
+extern "C" const char *a8_version(void) { return "a8attn 0.2.0 gfx950 src:" A8_SRC_HASH; }
 
 extern "C" const char *a8_last_error(void) { return a8::g_err; }
 

@@ -237,6 +237,7 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
   }
   // bias and residual by 8-byte loads where four channels share them (uniform)
   const bool vec = (Cout & 3) == 0 && (reinterpret_cast<uintptr_t>(bias) & 7u) == 0 &&
+                   (reinterpret_cast<uintptr_t>(y) & 7u) == 0 && ((s_yb | s_yt) & 3) == 0 &&
                    (!res || ((reinterpret_cast<uintptr_t>(res) & 7u) == 0 && ((s_rb | s_rt) & 3) == 0));
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
@@ -344,7 +345,8 @@ struct ConvPlan {
   int NT, WM, KSUB, ksplit;
   int64_t ntiles, ws_bytes;
 };
-static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph) {
+// allow_split = false: the caller has no workspace (one pass over K, and the narrow shape that goes with it).
+static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph, bool allow_split = true) {
   // 96-channel slices only where K has several of them (a 1x1 conv of 96 channels would be one step with
   // nothing to overlap: measured slower than three 32-channel steps)
   ConvPlan pl{16, 1, Cin % 64 == 0 ? 2 : (Cin % 96 == 0 && taps > 1) ? 3 : 1, 1, 0, 0};
@@ -365,23 +367,27 @@ static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph) {
     else better = wgs > best_wgs;
     if (better) best_cols = cols, best_wgs = wgs, best_wm = wm, pl.NT = nt, pl.WM = wm;
   }
+  const int steps = taps * ((Cin + 32 * pl.KSUB - 1) / (32 * pl.KSUB));
+  const bool fin_fits = (int64_t)ph * M * ((Cout + 3) / 4) < ((int64_t)1 << 31);
   // multi-tap convs and many-phase transposed convs on short inputs (the decoder's input conv and first
   // block): a wide two-row-tile shape with K split across workgroups beat the narrow tile that fills the
-  // chip by itself (block 0's k=7 convs 138 -> 93 us, its stride-8 transposed conv 87 -> 77 us)
-  if ((taps > 2 || ph >= 8) && pl.NT * pl.WM < 16 && best_wgs < 1024) {
+  // chip by itself (block 0's k=7 convs 138 -> 93 us, its stride-8 transposed conv 87 -> 77 us). Only with
+  // the split: alone, the wide tile leaves most of the chip idle.
+  if ((taps > 2 || ph >= 8) && pl.NT * pl.WM < 16 && best_wgs < 1024 && allow_split && steps >= 16 && fin_fits) {
     for (int nt : {12, 8, 16}) {
       const int64_t nti = (Cout + 16 * nt - 1) / (16 * nt);
       if (nti * 16 * nt != best_cols) continue;
+      const int64_t wide_wgs = ((M + 127) / 128) * nti * ph;
+      if (wide_wgs >= 512) break;  // K would not be split: keep the narrow tile
       pl.NT = nt;
       pl.WM = 2;
-      best_wgs = ((M + 127) / 128) * nti * ph;
+      best_wgs = wide_wgs;
       break;
     }
   }
   pl.ntiles = (Cout + 16 * pl.NT - 1) / (16 * pl.NT);
   const int64_t wgs = best_wgs;
-  const int steps = taps * ((Cin + 32 * pl.KSUB - 1) / (32 * pl.KSUB));
-  if (wgs < 512 && steps >= 16 && (int64_t)ph * M * ((Cout + 3) / 4) < ((int64_t)1 << 31)) {
+  if (allow_split && wgs < 512 && steps >= 16 && fin_fits) {
     int64_t k = (512 + wgs - 1) / wgs;
     k = k < steps / 8 ? k : steps / 8;
     k = k < 6 ? k : 6;  // more shares measured slower (the input conv: 11 shares 58 us, 6 shares 51 us)
@@ -412,10 +418,14 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
   if (B == 0 || TR == 0) return 0;
   if (!x || !w || !y || (snake_a != nullptr) != (snake_ib != nullptr))
     return set_error(A8_EINVAL, "conv_cl: null pointer");
+  // y (and res) may be any 2-byte-aligned view: the epilogue stores element by element unless 8-byte stores of
+  // four channels are aligned. The weight rows are read 16 bytes at a time: cout_w (its padded width) must be a
+  // multiple of 8.
   if (!al16(x) || !al16(w) || (s_xb | s_xt | s_wp | s_wt | s_wc) & 7 || (cout_w & 7) ||
-      (snake_a && (!al16(snake_a) || !al16(snake_ib))) || (reinterpret_cast<uintptr_t>(y) & 7u) ||
-      ((Cout & 3) == 0 && (s_yb | s_yt) & 3))
-    return set_error(A8_EALIGN, "conv_cl: x / w / snake 16-byte aligned, strides multiples of 8, y 8-byte");
+      (snake_a && (!al16(snake_a) || !al16(snake_ib))) || (reinterpret_cast<uintptr_t>(y) & 1u) ||
+      (res && (reinterpret_cast<uintptr_t>(res) & 1u)))
+    return set_error(A8_EALIGN, "conv_cl: x / w / snake 16-byte aligned, their strides and the weight's padded "
+                     "width (%d) multiples of 8", cout_w);
   const int64_t M = (int64_t)B * TR;
   if (M > INT32_MAX / 2) return set_error(A8_EUNSUP, "conv_cl: %lld rows too many", (long long)M);
   // bytes the kernel may read from x and w: both are addressed by 32-bit buffer offsets
@@ -426,7 +436,7 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
     return set_error(A8_EUNSUP, "conv_cl: x spans %lld bytes, w %lld (each must be below 2 GiB, strides >= 0)",
                      (long long)x_span, (long long)w_span);
   ConvPlan pl = conv_plan(M, Cin, Cout, taps, ph);
-  if (pl.ksplit > 1 && (!ws || ws_bytes < pl.ws_bytes)) pl.ksplit = 1;  // no workspace: one pass over K
+  if (pl.ksplit > 1 && (!ws || ws_bytes < pl.ws_bytes)) pl = conv_plan(M, Cin, Cout, taps, ph, false);  // one pass
   if (pl.ksplit > 1 && !al16(ws)) return set_error(A8_EALIGN, "conv_cl: workspace must be 16-byte aligned");
   const int NT = pl.NT, WM = pl.WM;
   float *part = pl.ksplit > 1 ? (float *)ws : nullptr;
@@ -470,6 +480,8 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
 #undef A8_CONV_NT
 #undef A8_CONV_ARGS
   if (part) {
+    const hipError_t e = hipGetLastError();  // the finish would sum a workspace the main launch never wrote
+    if (e != hipSuccess) return (int)e;
     const int64_t threads = (int64_t)ph * M * ((Cout + 3) / 4);
     hipLaunchKernelGGL(k_conv_fin, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        (const float *)part, pl.ntiles * 16 * NT, pl.ksplit, (const uint16_t *)bias,

@@ -481,13 +481,15 @@ def silu_mul(gu, out=None):
 _F16 = torch.float16
 
 
-def conv_cl(xin, w, bias, TR, taps, dil, ph, out, res=None, f16acc=True, cfg=None, snake=None):
+def conv_cl(xin, w, bias, TR, taps, dil, ph, out, res=None, f16acc=True, cfg=None, snake=None, ws=None):
     """Channels-last causal / transposed conv as an implicit GEMM (fast_kernels.py:600-623, kernel 551-597):
-    xin [B, Tin, Cin] fp16; w [ph, taps, Cin, Cout_pad] fp16; out [B, TR*ph, >=Cout] with Cout =
-    out.shape[-1]: out[b, t*ph + p] = bias + sum_j xin[b, t + j*dil] @ w[p, j] (+ res[b, t*ph + p]).
+    xin [B, Tin, Cin] fp16; w [ph, taps, Cin, Cout_pad] fp16 with Cout_pad a multiple of 8 (its rows are read
+    16 bytes at a time; the reference pads to max(16, Cout)); out [B, TR*ph, >=Cout] with Cout =
+    out.shape[-1], any view: out[b, t*ph + p] = bias + sum_j xin[b, t + j*dil] @ w[p, j] (+ res[b, t*ph + p]).
     snake = (alpha, 1/(alpha+eps)) fp32 [Cin] applies x + ib sin(alpha x)^2 to xin on the load. Accumulation
     is fp32 (f16acc, the reference's fp16 slice sums, and cfg, its Triton tile choice, are accepted and
-    unused)."""
+    unused). ws: an optional device byte buffer the launch may use to split K on short inputs (its size:
+    conv_cl_ws_bytes); without one, or when it is too small, K is not split. Nothing is allocated here."""
     for name, t, d in (("xin", xin, 3), ("w", w, 4), ("out", out, 3)):
         _need(isinstance(t, torch.Tensor) and t.dtype == _F16, f"{name} must be a float16 tensor", TypeError)
         _need(t.dim() == d and t.stride(-1) == 1, f"{name} must have {d} dims with a contiguous last dim")
@@ -508,18 +510,25 @@ def conv_cl(xin, w, bias, TR, taps, dil, ph, out, res=None, f16acc=True, cfg=Non
         _need(sa.dtype == torch.float32 and sib.dtype == torch.float32 and sa.is_contiguous() and sib.is_contiguous()
               and sa.numel() >= Cin and sib.numel() >= Cin, "snake must be two contiguous float32 [Cin] vectors")
     _check_device(xin=xin, w=w, out=out, bias=bias, res=res, snake_a=sa, snake_ib=sib)
+    if ws is not None:
+        _need(isinstance(ws, torch.Tensor) and ws.is_contiguous() and ws.device == xin.device,
+              "ws must be a contiguous device tensor on xin's device")
     lib = _lib.load()
-    nws = lib.a8_conv_cl_ws_bytes(B, TR, Cin, Cout, taps, ph)    # split-K workspace (short inputs), else 0
-    ws = torch.empty(nws, dtype=torch.uint8, device=xin.device) if nws > 0 else None
     st = lib.a8_conv_cl(
         xin.data_ptr(), xin.stride(0), xin.stride(1), w.data_ptr(), w.stride(0), w.stride(1), w.stride(2),
         w.shape[3], bias.data_ptr() if bias is not None else None, res.data_ptr() if res is not None else None,
         res.stride(0) if res is not None else 0, res.stride(1) if res is not None else 0, out.data_ptr(),
         out.stride(0), out.stride(1), sa.data_ptr() if sa is not None else None,
         sib.data_ptr() if sib is not None else None, B, Tin, TR, Cin, Cout, taps, dil, ph,
-        ws.data_ptr() if ws is not None else None, nws, _lib.stream_of(xin))
+        ws.data_ptr() if ws is not None else None, ws.numel() * ws.element_size() if ws is not None else 0,
+        _lib.stream_of(xin))
     _lib.check(st, "conv_cl")
     return out
+
+
+def conv_cl_ws_bytes(B, TR, Cin, Cout, taps, ph):
+    """Bytes of the split-K workspace conv_cl uses for this shape (0: K is not split)."""
+    return int(_lib.load().a8_conv_cl_ws_bytes(B, TR, Cin, Cout, taps, ph))
 
 
 def snake_cat(x, state, a, ib, out):

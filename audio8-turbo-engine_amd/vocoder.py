@@ -22,14 +22,15 @@ from __future__ import annotations
 
 import torch
 
-from .fast_kernels import conv_cl, snake_cat
+from .fast_kernels import conv_cl, conv_cl_ws_bytes, snake_cat
 
 F16 = torch.float16
 
 
 def pack_conv(w, trans=False, stride=1):
-    """(W [ph, taps, Cin, max(16, Cout)] fp16, taps, ph) from a Conv1d weight [Cout, Cin, K] or a
-    ConvTranspose1d weight [Cin, Cout, 2*stride] (fast_engine.py:186-206)."""
+    """(W [ph, taps, Cin, Cout_pad] fp16, taps, ph) from a Conv1d weight [Cout, Cin, K] or a ConvTranspose1d
+    weight [Cin, Cout, 2*stride] (fast_engine.py:186-206). Cout_pad = max(16, Cout) as in the reference,
+    rounded up to a multiple of 8 (conv_cl reads weight rows 16 bytes at a time)."""
     w = w.detach().float()
     if trans:
         Cin, Cout, K = w.shape
@@ -41,7 +42,7 @@ def pack_conv(w, trans=False, stride=1):
         Cout, Cin, K = w.shape
         W = w.permute(2, 1, 0).unsqueeze(0)
         taps, ph = K, 1
-    Wp = torch.zeros(*W.shape[:-1], max(16, Cout), device=w.device)
+    Wp = torch.zeros(*W.shape[:-1], max(16, -(-Cout // 8) * 8), device=w.device)
     Wp[..., :Cout] = W
     return Wp.to(F16).contiguous(), taps, ph
 
@@ -49,9 +50,12 @@ def pack_conv(w, trans=False, stride=1):
 class CLConv:
     """One conv of the decoder with its packed weights, bias, snake vectors and per-row state
     (_CLConv, fast_engine.py:178-233). weight / bias are the module's tensors; alpha the snake's [Cin] (or
-    None); dilation for a Conv1d, stride for a ConvTranspose1d (trans=True)."""
+    None); dilation for a Conv1d, stride for a ConvTranspose1d (trans=True). tmax: the most input rows a call
+    takes (a frame's length at this conv); the split-K workspace is sized once for every row count up to Bmax
+    at tmax rows. A call with more rows or a shape needing more runs K unsplit (nothing is allocated in a
+    call)."""
 
-    def __init__(self, weight, bias, Bmax, dev, states, alpha=None, trans=False, stride=1, dilation=1):
+    def __init__(self, weight, bias, Bmax, dev, states, alpha=None, trans=False, stride=1, dilation=1, tmax=None):
         self.W, self.taps, self.ph = pack_conv(weight.to(dev), trans, stride)
         self.dil = 1 if trans else int(dilation)
         self.ctx = 1 if trans else (self.taps - 1) * self.dil
@@ -66,6 +70,12 @@ class CLConv:
         if self.ctx > 0:
             self.state = torch.zeros(Bmax, self.ctx, self.Cin, dtype=F16, device=dev)
             states.append(self.state)
+        self.ws = None
+        if tmax and torch.device(dev).type == "cuda":
+            need = max(conv_cl_ws_bytes(b, int(tmax), self.Cin, self.Cout, self.taps, self.ph)
+                       for b in range(1, Bmax + 1))
+            if need > 0:
+                self.ws = torch.empty(need, dtype=torch.uint8, device=dev)
 
     def __call__(self, x, b, res=None):
         """x [b, T, Cin] fp16 (pre-activation) -> [b, T*ph, Cout] fp16."""
@@ -73,11 +83,12 @@ class CLConv:
         y = torch.empty(b, T * self.ph, self.Cout, dtype=F16, device=x.device)
         if self.state is None:
             snake = (self.a, self.ib) if self.a is not None else None
-            conv_cl(x.contiguous(), self.W, self.bias, T, self.taps, self.dil, self.ph, y, res=res, snake=snake)
+            conv_cl(x.contiguous(), self.W, self.bias, T, self.taps, self.dil, self.ph, y, res=res, snake=snake,
+                    ws=self.ws)
             return y
         xin = torch.empty(b, self.ctx + T, self.Cin, dtype=F16, device=x.device)
         snake_cat(x, self.state[:b], self.a, self.ib, xin)
-        conv_cl(xin, self.W, self.bias, T, self.taps, self.dil, self.ph, y, res=res)
+        conv_cl(xin, self.W, self.bias, T, self.taps, self.dil, self.ph, y, res=res, ws=self.ws)
         self.state[:b].copy_(xin[:, T:])
         return y
 
@@ -114,21 +125,24 @@ def decoder_weights(cin=1024, ch=1536, rates=(8, 8, 4, 2), k=7, dils=(1, 3, 9), 
 
 class CLDecoder:
     """The stateful channels-last decoder (_CLDecoder, fast_engine.py:276-310) over `decoder_weights`-shaped
-    weights; every conv's state is registered in `states` (per row, for snapshots / row resets)."""
+    weights; every conv's state is registered in `states` (per row, for snapshots / row resets). frame: the
+    input rows a call takes (sizes each conv's split-K workspace once; the streaming decoder's frame is 4)."""
 
-    def __init__(self, wts, Bmax, dev, states=None):
+    def __init__(self, wts, Bmax, dev, states=None, frame=4):
         self.states = states if states is not None else []
         S = self.states
         w, b = wts["conv_in"]
-        self.dec_in = CLConv(w, b, Bmax, dev, S, dilation=1)
+        t = int(frame)
+        self.dec_in = CLConv(w, b, Bmax, dev, S, dilation=1, tmax=t)
         self.blocks = []
         for a0, tw, tb, s, units in wts["blocks"]:
-            tc = CLConv(tw, tb, Bmax, dev, S, alpha=a0, trans=True, stride=s)
-            us = [(CLConv(w1, b1, Bmax, dev, S, alpha=a1, dilation=d), CLConv(w2, b2, Bmax, dev, S, alpha=a2))
-                  for a1, w1, b1, d, a2, w2, b2 in units]
+            tc = CLConv(tw, tb, Bmax, dev, S, alpha=a0, trans=True, stride=s, tmax=t)
+            t *= s
+            us = [(CLConv(w1, b1, Bmax, dev, S, alpha=a1, dilation=d, tmax=t),
+                   CLConv(w2, b2, Bmax, dev, S, alpha=a2, tmax=t)) for a1, w1, b1, d, a2, w2, b2 in units]
             self.blocks.append((tc, us))
         af, wf, bf = wts["final"]
-        self.final = CLConv(wf, bf, Bmax, dev, S, alpha=af)
+        self.final = CLConv(wf, bf, Bmax, dev, S, alpha=af, tmax=t)
         self.up = 1
         for _, _, _, s, _ in wts["blocks"]:
             self.up *= s

@@ -43,7 +43,8 @@ extern "C" {
 #define A8_EUNSUP  (-3) /* configuration this build does not implement (e.g. head_dim != 64) */
 #define A8_EWSPACE (-4) /* decode workspace too small for b * nsplit row-splits */
 
-/* Library version string, e.g. "a8attn 0.1.0 gfx950". No reference counterpart. */
+/* Library version string, "a8attn <version> gfx950 src:<hash>", the hash being that of the sources the library
+ * was built from (so a stale build can be detected). No reference counterpart. */
 const char *a8_version(void);
 
 /* Message for the last negative status returned on the calling thread ("" if none). */

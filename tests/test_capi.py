@@ -28,6 +28,17 @@ def test_header_declares_the_entry_points():
                                          "a8_conv_cl", "a8_conv_cl_ws_bytes", "a8_snake_cat"}
 
 
+def test_library_is_built_from_these_sources(a8):
+    """The library in the tree carries the hash of the sources it was built from: a build older than an edit
+    to csrc/ or include/ fails here (rebuild with `python __graft_entry__.py build`)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("_a8_bl", os.path.join(ROOT, "audio8-turbo-engine_amd", "build_lib.py"))
+    bl = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bl)
+    ver = a8.load_library().a8_version().decode()
+    assert ver.endswith("src:" + bl.source_hash()), (ver, bl.source_hash())
+
+
 def test_library_exports_every_declared_symbol(a8):
     lib = a8.load_library()
     raw = ctypes.CDLL(a8.LIB_PATH)

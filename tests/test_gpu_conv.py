@@ -59,10 +59,34 @@ def test_conv_cl_shapes(a8, cref, dev, B, T, Cin, Cout, cw, taps, dil, ph, bias,
         ab = (a, 1.0 / (a + 1e-9))
     want = cref.conv_cl(x, w, bv, T, taps, dil, ph, Cout, res=rv, snake_ab=ab)
     out = torch.full((B, T * ph, Cout), 7.0, dtype=F16, device=dev)
+    nws = a8.conv_cl_ws_bytes(B, T, Cin, Cout, taps, ph)      # the split-K shapes get a caller workspace
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev) if nws > 0 else None
     a8.conv_cl(x.to(dev), w.to(dev), bv.to(dev) if bias else None, T, taps, dil, ph, out,
-               res=rv.to(dev) if res else None, snake=(ab[0].to(dev), ab[1].to(dev)) if snake else None)
+               res=rv.to(dev) if res else None, snake=(ab[0].to(dev), ab[1].to(dev)) if snake else None, ws=ws)
     torch.cuda.synchronize()
     assert _close(out, want)
+
+
+@pytest.mark.parametrize("Cout,cw", [(30, 32), (1, 16), (96, 96)])
+def test_conv_cl_into_offset_view(a8, cref, dev, Cout, cw):
+    """out (and res) as time-offset views of a larger buffer, as the reference's conv_cl accepts: row 1
+    onwards, so the view starts 2 * Cout bytes in (not 8-byte aligned for odd Cout / 2); the rows around it
+    are left alone."""
+    say(f"case: conv_cl into out[:, 1:] with Cout={Cout}")
+    g = torch.Generator().manual_seed(40 + Cout)
+    B, T, Cin, taps = 3, 9, 64, 3
+    x = torch.randn(B, T + taps - 1, Cin, generator=g).to(F16)
+    w = (torch.randn(1, taps, Cin, cw, generator=g) / (taps * Cin) ** 0.5).to(F16)
+    bv = torch.randn(cw, generator=g).to(F16)
+    rbuf = torch.randn(B, T + 1, Cout, generator=g).to(F16)
+    want = cref.conv_cl(x, w, bv, T, taps, 1, 1, Cout, res=rbuf[:, 1:])
+    buf = torch.full((B, T + 2, Cout), 7.0, dtype=F16, device=dev)
+    rb_d = rbuf.to(dev)
+    a8.conv_cl(x.to(dev), w.to(dev), bv.to(dev), T, taps, 1, 1, buf[:, 1:T + 1], res=rb_d[:, 1:])
+    torch.cuda.synchronize()
+    got = buf.cpu()
+    assert _close(got[:, 1:T + 1], want)
+    assert (got[:, 0] == 7.0).all() and (got[:, T + 1] == 7.0).all()
 
 
 def test_snake_cat_and_decoder_call_pattern(a8, cref, dev):

@@ -83,7 +83,8 @@ def test_decoder_graph_replay_equals_eager(dev):
                                                           for u in us]) for a, w, b, s, us in wts["blocks"]],
           "final": tuple(t.to(dev) for t in wts["final"])}
     B = 3
-    dec_g, dec_e = voc.CLDecoder(wd, B, dev), voc.CLDecoder(wd, B, dev)
+    dec_g, dec_e = voc.CLDecoder(wd, B, dev, frame=2), voc.CLDecoder(wd, B, dev, frame=2)
+    assert dec_g.dec_in.ws is not None                                  # owned once, sized for the frame
     xs = torch.zeros(B, 2, 256, device=dev)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
