@@ -235,3 +235,48 @@ def test_prefill_rows_match_decode(a8, dev):
     att(q, kc, vc, lens, dec, nsplit=2, rowmap=rowmap)
     torch.cuda.synchronize()
     assert maxabs(out, dec) <= TOL
+
+
+@pytest.mark.parametrize("nq,nkv", [(14, 2), (10, 2), (12, 2), (16, 2), (16, 1), (8, 2), (4, 4)])
+def test_prefill_groups(a8, ref, dev, nq, nkv):
+    """Every head grouping through the workgroup shapes it takes (q heads per kv head split into shares of <= 4
+    waves: 7 -> 4 + 3, 5 -> 4 + 1, 6 -> 4 + 2, 16 -> 4 x 4; 1 and 2 in one workgroup) against the oracle: 200
+    short requests (one-tile blocks, last query groups empty), 24 long ones, and padding blocks (n = 0)
+    between them; rows past the packed tokens stay untouched."""
+    group = nq // nkv
+    say(f"case: prefill nq={nq} nkv={nkv} (group {group})")
+    g = torch.Generator().manual_seed(40 + group * 3 + nkv)
+    S = 704
+    ns = torch.randint(1, 65, (200,), generator=g).tolist() + torch.randint(100, 301, (24,), generator=g).tolist()
+    p0s = torch.randint(0, 101, (200,), generator=g).tolist() + torch.randint(0, 301, (24,), generator=g).tolist()
+    nreq = len(ns)
+    slots = torch.randperm(nreq, generator=g).tolist()
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    R = sum(ns)
+    kc, vc = randn_bf16(g, nreq + 1, nkv, S, HD), randn_bf16(g, nreq + 1, nkv, S, HD)
+    q = randn_bf16(g, R + 64, nq, HD)
+    want = torch.zeros(R, nq, HD, dtype=BF)
+    ref.prefill_attention(q[:R], kc, vc, *ref.prefill_plan(r0s, ns, slots, p0s), want, group)
+    # the plan's blocks with a padding block (n = 0, rows R..R+63 of the scratch slot) after every 16th
+    plan = a8.PrefillPlan(r0s, ns, slots, p0s, dev)
+    cols = [t.cpu().tolist() for t in (plan.q0, plan.n, plan.slot, plan.pos0)]
+    blocks = []
+    for i, b in enumerate(zip(*cols)):
+        blocks.append(b)
+        if i % 16 == 15:
+            blocks.append((R, 0, nreq, 0))
+    t = torch.tensor(blocks, dtype=torch.int32).T.contiguous().to(dev)
+
+    class Plan:
+        BM, nblk = 64, len(blocks)
+        q0, n, slot, pos0 = t[0], t[1], t[2], t[3]
+
+    out = torch.full((R + 64, nq, HD), 7.0, dtype=BF, device=dev)
+    a8.prefill_attention(q.to(dev), kc.to(dev), vc.to(dev), Plan, out, group)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    err = maxabs(got[:R], want)
+    say(f"  R={R} blocks={len(blocks)} max-abs {err:.3e}")
+    assert torch.isfinite(got[:R].float()).all()
+    assert err <= TOL
+    assert (got[R:].float() == 7.0).all()
