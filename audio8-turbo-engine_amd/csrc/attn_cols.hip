@@ -1,0 +1,253 @@
+// Attention for head dimensions other than 64 (head_dim 128): decode (a8_decode_attn*) and packed prefill
+// (a8_prefill_attn) through one kernel, for the reference's generic-HD kernels (serve/fast_kernels.py:190-290
+// decode, 296-358 prefill: HD is a compile-time constant there, any power of two).
+//
+// One wave computes up to 16 attention columns that share a cache row and a kv head; column j (lane r16 = j of
+// each 16-lane group) is one (query row, q head) with its own key count L_j: it attends keys [0, L_j) of the
+// cache row, online softmax in fp32 (exp2 with the scale folded in, the weights rounded to bf16 for P.V as in
+// the reference, the row sum of the fp32 weights), out = bf16(acc / l). Decode: the group's q heads of one
+// query row (L = lens); prefill: 16 consecutive rows of one block and q head (L = position + 1, causal).
+//
+// Per 64-key tile, with the MFMA layouts of the head_dim-64 kernels (v_mfma_f32_16x16x32_bf16):
+//   * S^T = K.Q^T: tile (c, t) rows 4g+i <-> key t0 + 32c + 8g + 4t + i; the K operand (lane (g, r16): key
+//     t0 + 32c + 8(r16/4) + 4t + r16%4, dims 32s + 8g..+7) comes straight from the cache with 16-byte buffer
+//     loads (keys past the wave's largest L read as zeros), HD/32 products per (c, t);
+//   * O^T += V^T.P^T: the S^T C layout is the P^T operand; V goes by DMA (buffer_load ... lds) into a
+//     wave-private LDS tile, row r's 16-byte chunks permuted by chunk ^= 2 (r & 3) (the permutation goes into
+//     the DMA's source offsets), so the transposing reads of four consecutive rows hit distinct banks; it is
+//     read as V^T by ds_read_b64_tr_b16, HD/16 row blocks of 16 dims.
+// Work is one wave per column group (four independent waves per workgroup); the kernel is not tuned like the
+// head_dim-64 paths: it is the generic-head fallback those entry points route to.
+#include "decode_tile.h"
+
+namespace a8 {
+namespace {
+
+constexpr int kColWaves = 4;  // independent waves per workgroup
+
+// The column group of one wave: its columns' query / output rows, q heads and key counts (per lane), the
+// cache row and kv head (uniform), and the wave's largest and smallest key counts over its valid columns.
+struct ColGroup {
+  bool ok;          // the wave has work
+  int64_t crow;     // cache row
+  int kh;           // kv head
+  int lmax, lmin;   // over valid columns (uniform)
+  bool valid;       // this lane's column exists
+  int64_t qrow;     // this lane's query row (and output row)
+  int head;         // this lane's q head
+  int L;            // this lane's key count
+};
+
+template <int HD>
+__global__ __launch_bounds__(64 * kColWaves) void k_attn_cols(
+    const uint16_t *__restrict__ q, int64_t s_qr, int64_t s_qh, int R,
+    const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh,
+    int cache_rows, int cache_len, uint16_t *__restrict__ out, int64_t s_or, int64_t s_oh,
+    // decode (prefill = false): lens [b], rowmap [b] or null; prefill: the block plan
+    const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap, const int32_t *__restrict__ bq0,
+    const int32_t *__restrict__ bn, const int32_t *__restrict__ bslot, const int32_t *__restrict__ bpos0,
+    int ngroups, int nq, int nkv, int group, bool prefill, float sl2) {
+  static_assert(HD % 32 == 0 && HD <= 128, "head dimension");
+  constexpr int KS = HD / 32;   // reduction slices of S^T
+  constexpr int DT = HD / 16;   // 16-dim row blocks of O^T
+  constexpr int PITCH = HD * 2;  // bytes per key row of the LDS V tile
+  constexpr int NCH = HD / 8;    // 16-byte chunks per key row
+  __shared__ __attribute__((aligned(16))) char vbuf[kColWaves][64 * PITCH];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int r16 = lane & 15, g = lane >> 4;
+  const int gw = blockIdx.x * kColWaves + w;
+  if (gw >= ngroups) return;  // whole wave (waves of a workgroup never meet at a barrier)
+  char *vt = vbuf[w];
+
+  ColGroup cg{};
+  if (!prefill) {
+    // decode: group gw = (row b, kv head kh); column j = q head kh * group + j of row b
+    const int b = gw / nkv;
+    cg.kh = gw - b * nkv;
+    const int crow = rowmap ? rowmap[b] : b;
+    const int L = min(max(lens[b], 0), cache_len);
+    cg.ok = crow >= 0 && crow < cache_rows;
+    cg.crow = crow;
+    cg.lmax = cg.lmin = L;
+    cg.valid = r16 < group;
+    cg.qrow = b;
+    cg.head = cg.kh * group + r16;
+    cg.L = L;
+  } else {
+    // prefill: group gw = (block, q head h, 16-row sub-block sb); column j = row 16 sb + j of the block
+    const int per = nq * 4;
+    const int blk = gw / per, rem = gw - blk * per;
+    const int h = rem >> 2, sb = rem & 3;
+    const int n = bn[blk], q0 = bq0[blk], p0 = bpos0[blk];
+    const int64_t sl = bslot[blk];
+    const int nv = min(min(n, 64), R - q0);
+    const int hi = min(p0 + n, cache_len);
+    cg.ok = n > 0 && sl >= 0 && sl < cache_rows && p0 >= 0 && q0 >= 0 && q0 < R && 16 * sb < nv && hi > 0;
+    cg.crow = sl;
+    cg.kh = h / group;
+    const int last = min(16 * sb + 15, nv - 1);
+    cg.lmax = min(p0 + last + 1, hi);
+    cg.lmin = min(p0 + 16 * sb + 1, hi);
+    const int row = 16 * sb + r16;
+    cg.valid = row < nv;
+    cg.qrow = (int64_t)q0 + row;
+    cg.head = h;
+    cg.L = cg.valid ? min(p0 + row + 1, hi) : 0;
+  }
+  if (!cg.ok) return;
+  if (!cg.valid) cg.L = 0;
+
+  // Q^T operands: column r16, dims 32s + 8g..+7 (zeros for a missing column)
+  u32x4 qb[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qb[s] = u32x4{0u, 0u, 0u, 0u};
+  if (cg.valid) {  // (a missing column's address may lie past q)
+    const uint16_t *qp = q + cg.qrow * s_qr + (int64_t)cg.head * s_qh + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qb[s] = ld16(qp + 32 * s);
+  }
+  // K / V of the cache row and kv head as buffers over keys [0, lmax): rows past it read as zeros
+  const int64_t cb = cg.crow * s_kb + (int64_t)cg.kh * s_kh;
+  constexpr uint32_t kRowB = HD * 2;
+  const rsrc_t kr = make_rsrc(kc + cb, (uint32_t)cg.lmax * kRowB);
+  const rsrc_t vr = make_rsrc(vc + cb, (uint32_t)cg.lmax * kRowB);
+  // K operand rows of this lane: key 32c + 8(r16/4) + 4t + r16%4 of the tile
+  const uint32_t krow = (uint32_t)(8 * (r16 >> 2) + (r16 & 3));
+  // V DMA: instruction i writes rows (16 i + lane) / NCH.., lane l's 16 bytes to LDS chunk l % NCH of its row,
+  // from source chunk (l % NCH) ^ 2 (row & 3)
+  constexpr int VDMA = 64 * NCH / 64;  // instructions per tile
+  static_assert(64 % NCH == 0, "whole rows per DMA instruction");
+  const uint32_t vrow = (uint32_t)(lane / NCH), vch = (uint32_t)(lane % NCH);
+  const uint32_t vsrc = vrow * PITCH + ((vch ^ (2u * (vrow & 3u))) << 4);
+  // V^T reads: lane i of a 16-lane group points at row r0 + i/4 (r0 = 32c + 8g, + 4), dims 16dt + 4(i%4),
+  // found in LDS chunk (2dt + (i%4)/2) ^ 2 ((i/4) & 3)
+  const uint32_t vrr = (uint32_t)(r16 >> 2), vperm = 2u * (vrr & 3u), vhalf = (uint32_t)(r16 & 1) * 8u;
+  const uint32_t vc0 = (uint32_t)((r16 & 3) >> 1);
+
+  float m = kNegInf, lsum = 0.f;
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int t0 = 0; t0 < cg.lmax; t0 += 64) {
+    // the V tile into LDS by DMA, K operands into registers
+#pragma unroll
+    for (int i = 0; i < VDMA; ++i)
+      bld16_lds<0>(vr, vt + i * 1024, (uint32_t)t0 * kRowB + (uint32_t)i * 1024u + vsrc, 0u);
+    u32x4 ka[2][2][KS];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          ka[c][t][s] = bld16(kr, ((uint32_t)t0 + 32u * c + krow + 4u * t) * kRowB + (uint32_t)(32 * s + 8 * g) * 2u);
+    // scores, masked per column where the tile reaches past some column's key count
+    f32x4 sc[2][2];
+    float mt = kNegInf;
+    const bool mask = t0 + 64 > cg.lmin || !cg.valid;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) a = mfma16x16x32(ka[c][t][s], qb[s], a);
+        if (mask) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (t0 + 32 * c + 8 * g + 4 * t + i >= cg.L) a[i] = kNegInf;
+        }
+        mt = fmaxf(mt, fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])));
+        sc[c][t] = a;
+      }
+    mt = max_over_groups(mt);
+    const float mn = fmaxf(m, mt);
+    const float mc = mn == kNegInf ? 0.f : mn * sl2;  // a column with no key yet stays inert
+    const float alpha = m == kNegInf ? 0.f : fast_exp2(__builtin_fmaf(m, sl2, -mc));
+    float ps = 0.f;
+    u32x4 pB[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = fast_exp2(__builtin_fmaf(sc[c][t][i], sl2, -mc));
+          ps += p[i];
+        }
+        pB[c][2 * t] = pack_bf16x2(p[0], p[1]);
+        pB[c][2 * t + 1] = pack_bf16x2(p[2], p[3]);
+      }
+    lsum = lsum * alpha + ps;
+    m = mn;
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const char *p = vt + (32 * c + 8 * g + vrr) * PITCH + ((((uint32_t)(2 * dt) + vc0) ^ vperm) << 4) + vhalf;
+        const u32x2 lo = lds_tr16(p), hi2 = lds_tr16(p + 4 * PITCH);
+        o[dt] = mfma16x16x32(u32x4{lo[0], lo[1], hi2[0], hi2[1]}, pB[c], o[dt]);
+      }
+    // every lane's reads of the tile are done before the next tile's DMA overwrites it
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  }
+
+  // l = 0 (no key, decode lens = 0) gives 0 * inf = NaN, like the reference's 0 / 0
+  const float rl = __builtin_amdgcn_rcpf(sum_over_groups(lsum));
+  if (!cg.valid) return;
+  uint16_t *op = out + cg.qrow * s_or + (int64_t)cg.head * s_oh + 4 * g;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    st8(op + 16 * dt, u32x2{pack_bf16x2(o[dt][0] * rl, o[dt][1] * rl), pack_bf16x2(o[dt][2] * rl, o[dt][3] * rl)});
+}
+
+}  // namespace
+
+// Decode of b rows (a8_decode_attn / _stream / _flat / _noalloc for head_dim 128): q [b, nq, HD] (strides
+// s_qb, s_qh), caches [rows, nkv, S, HD] with contiguous positions, lens / rowmap as the decode entry points.
+int attn_cols_decode(const char *fn, const void *q, int64_t s_qb, int64_t s_qh, const void *kc, const void *vc,
+                     int64_t s_kb, int64_t s_kh, int cache_rows, int cache_len, const int32_t *lens,
+                     const int32_t *rowmap, void *out, int64_t s_ob, int64_t s_oh, int b, int nq, int nkv, int hd,
+                     float scale, hipStream_t stream) {
+  if (hd != 128) return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64 or 128)", fn, hd);
+  const int group = nq / nkv;
+  if (group > 16) return set_error(A8_EUNSUP, "%s: GQA group %d > 16 not supported", fn, group);
+  const int64_t ngroups = (int64_t)b * nkv;
+  if (ngroups == 0) return 0;
+  if (ngroups > INT32_MAX / 2) return set_error(A8_EUNSUP, "%s: %d rows x %d kv heads too many", fn, b, nkv);
+  if ((int64_t)cache_len * hd * 2 >= ((int64_t)1 << 32))
+    return set_error(A8_EUNSUP, "%s: cache of %d positions too long for 32-bit offsets", fn, cache_len);
+  const unsigned grid = (unsigned)((ngroups + kColWaves - 1) / kColWaves);
+  hipLaunchKernelGGL(k_attn_cols<128>, dim3(grid), dim3(64 * kColWaves), 0, stream, (const uint16_t *)q, s_qb, s_qh,
+                     b, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, cache_rows, cache_len,
+                     (uint16_t *)out, s_ob, s_oh, lens, rowmap, nullptr, nullptr, nullptr, nullptr, (int)ngroups, nq,
+                     nkv, group, false, scale * kLog2e);
+  return (int)hipGetLastError();
+}
+
+// Packed prefill over a block plan (a8_prefill_attn for head_dim 128).
+int attn_cols_prefill(const void *q, int64_t s_qr, int64_t s_qh, int R, const void *kc, const void *vc, int64_t s_kb,
+                      int64_t s_kh, int cache_rows, int cache_len, void *out, int64_t s_or, int64_t s_oh,
+                      const int32_t *bq0, const int32_t *bn, const int32_t *bslot, const int32_t *bpos0, int nblk,
+                      int nq, int group, int hd, float scale, hipStream_t stream) {
+  if (hd != 128) return set_error(A8_EUNSUP, "prefill_attn: head_dim %d not supported (64 or 128)", hd);
+  const int64_t ngroups = (int64_t)nblk * nq * 4;
+  if (ngroups == 0) return 0;
+  if (ngroups > INT32_MAX / 2) return set_error(A8_EUNSUP, "prefill_attn: %d blocks x %d heads too many", nblk, nq);
+  if ((int64_t)cache_len * hd * 2 >= ((int64_t)1 << 32))
+    return set_error(A8_EUNSUP, "prefill_attn: cache of %d positions too long for 32-bit offsets", cache_len);
+  const unsigned grid = (unsigned)((ngroups + kColWaves - 1) / kColWaves);
+  hipLaunchKernelGGL(k_attn_cols<128>, dim3(grid), dim3(64 * kColWaves), 0, stream, (const uint16_t *)q, s_qr, s_qh,
+                     R, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, cache_rows, cache_len,
+                     (uint16_t *)out, s_or, s_oh, nullptr, nullptr, bq0, bn, bslot, bpos0, (int)ngroups, nq,
+                     nq / group, group, true, scale * kLog2e);
+  return (int)hipGetLastError();
+}
+
+}  // namespace a8

@@ -336,7 +336,8 @@ static int flat_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh,
                       int64_t ws_row_splits, int32_t *counters, int64_t n_counters, int b, int nq, int nkv, int hd,
                       int grid, float scale, const StoreIn &si, void *stream) {
   const bool fused = si.qkv != nullptr;
-  if (hd != 64) return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64 only)", fn, hd);
+  if (hd != 64 && (fused || hd != 128))
+    return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64; 128 through the unfused call)", fn, hd);
   if (b < 0 || nq <= 0 || nkv <= 0 || nq % nkv || cache_rows < 0 || cache_len < 0)
     return set_error(A8_EINVAL, "%s: bad sizes b=%d nq=%d nkv=%d", fn, b, nq, nkv);
   const int group = nq / nkv;
@@ -363,6 +364,9 @@ static int flat_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_qh,
   if ((!fused && !al16f(q)) || !al16f(kc) || !al16f(vc) || !al16f(out) || !al16f(acc_ws) ||
       ((fused ? 0 : (s_qb | s_qh)) | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
     return set_error(A8_EALIGN, "%s: pointers must be 16-byte aligned and strides multiples of 8", fn);
+  if (hd != 64)  // the generic-head kernel (one launch, no workspace)
+    return attn_cols_decode(fn, q, s_qb, s_qh, kc, vc, s_kb, s_kh, cache_rows, cache_len, lens, rowmap, out, s_ob,
+                            s_oh, b, nq, nkv, hd, scale, (hipStream_t)stream);
   const hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;
   auto kern = fused ? k_decode_flat<true> : k_decode_flat<false>;

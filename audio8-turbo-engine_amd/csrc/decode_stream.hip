@@ -436,7 +436,8 @@ static int stream_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_q
                         int waves, int tiles_per_wave, int grid, float scale, int phases, const StoreIn &si,
                         void *stream) {
   const bool fused = si.qkv != nullptr;
-  if (hd != 64) return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64 only)", fn, hd);
+  if (hd != 64 && (fused || hd != 128))
+    return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64; 128 through the unfused call)", fn, hd);
   if (b < 0 || nq <= 0 || nkv <= 0 || nq % nkv || cache_rows < 0 || cache_len < 0)
     return set_error(A8_EINVAL, "%s: bad sizes b=%d nq=%d nkv=%d", fn, b, nq, nkv);
   const int group = nq / nkv;
@@ -461,6 +462,9 @@ static int stream_entry(const char *fn, const void *q, int64_t s_qb, int64_t s_q
   if ((!fused && !al16s(q)) || !al16s(kc) || !al16s(vc) || !al16s(out) || (P > 1 && !al16s(acc_ws)) ||
       ((fused ? 0 : (s_qb | s_qh)) | s_kb | s_kh | s_ks | s_ob | s_oh) & 7)
     return set_error(A8_EALIGN, "%s: pointers must be 16-byte aligned and strides multiples of 8", fn);
+  if (hd != 64)  // the generic-head kernel (one launch, no workspace)
+    return attn_cols_decode(fn, q, s_qb, s_qh, kc, vc, s_kb, s_kh, cache_rows, cache_len, lens, rowmap, out, s_ob,
+                            s_oh, b, nq, nkv, hd, scale, (hipStream_t)stream);
   if (grid > NC) grid = (int)NC;
   const hipStream_t st = (hipStream_t)stream;
   const float sl2 = scale * kLog2e;

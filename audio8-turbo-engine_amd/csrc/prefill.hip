@@ -397,7 +397,8 @@ extern "C" int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
                                const int32_t *bpos0, int nblk, int bm,
                                int nq, int group, int hd, float scale, void *stream) {
   using namespace a8;
-  if (hd != 64) return set_error(A8_EUNSUP, "prefill_attn: head_dim %d not supported (64 only)", hd);
+  if (hd != 64 && hd != 128)
+    return set_error(A8_EUNSUP, "prefill_attn: head_dim %d not supported (64 or 128)", hd);
   if (bm != 64) return set_error(A8_EUNSUP, "prefill_attn: block size %d not supported (64 only)", bm);
   if (nblk < 0 || R < 0 || nq <= 0 || group <= 0 || nq % group || cache_rows < 0 || cache_len < 0)
     return set_error(A8_EINVAL, "prefill_attn: bad sizes nblk=%d R=%d nq=%d group=%d", nblk, R, nq, group);
@@ -409,6 +410,9 @@ extern "C" int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
   if (s_ks != hd)
     return set_error(A8_EUNSUP, "prefill_attn: cache positions must be contiguous rows (s_ks %lld)", (long long)s_ks);
   const int nkv = nq / group;
+  if (hd != 64)  // the generic-head kernel
+    return attn_cols_prefill(q, s_qr, s_qh, R, kc, vc, s_kb, s_kh, cache_rows, cache_len, out, s_or, s_oh, bq0, bn,
+                             bslot, bpos0, nblk, nq, group, hd, scale, (hipStream_t)stream);
   const int hpw = group < kPfMaxHW ? group : kPfMaxHW;  // q heads (waves) per workgroup
   const int hsplit = (group + hpw - 1) / hpw;
   const int nh = nkv * hsplit;

@@ -1,8 +1,9 @@
 // qkv bias + rotate_half RoPE arithmetic of serve/fast_kernels.py:139-187, per partner pair of 16-byte
-// chunks (dims 8c..8c+7 and 32+8c..32+8c+7 of one head), shared by the store kernel (store.hip) and the
-// fused store + decode path (decode_stream.hip), so both produce the same bits:
+// chunks (dims 8c..8c+7 and HD/2+8c..HD/2+8c+7 of one head, HD the head dimension), shared by the store
+// kernel (store.hip) and the fused store + decode paths (decode_stream.hip, decode_rows.hip), so both
+// produce the same bits:
 //   x = f32(qkv) + f32(bias)
-//   q/k: o[d] = bf16(x[d] * cos[d] + sign(d) * x[(d + 32) % 64] * sin[d]),  sign = -1 for d < 32
+//   q/k: o[d] = bf16(x[d] * cos[d] + sign(d) * x[(d + HD/2) % HD] * sin[d]),  sign = -1 for d < HD/2
 //   v:   o[d] = bf16(x[d])
 // with two roundings for the products and one for the sum (no contraction) and a torch-exact
 // round-to-nearest-even narrowing.
@@ -54,7 +55,7 @@ __device__ __forceinline__ void rope_rotate_f(const float (&xl)[8], const float 
       const int j = 2 * e + k;
       const float cl = k ? bf_hi(clo[e]) : bf_lo(clo[e]), ch = k ? bf_hi(chi[e]) : bf_lo(chi[e]);
       const float sn_l = k ? bf_hi(slo[e]) : bf_lo(slo[e]), sn_h = k ? bf_hi(shi[e]) : bf_lo(shi[e]);
-      // d < 32: partner x[d+32] with sign -1; d >= 32: partner x[d-32] with sign +1.
+      // low half: partner x[d + HD/2] with sign -1; high half: partner x[d - HD/2] with sign +1.
       ol[j] = xl[j] * cl + (-xh[j]) * sn_l;
       oh[j] = xh[j] * ch + xl[j] * sn_h;
     }

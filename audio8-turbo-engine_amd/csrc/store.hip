@@ -1,16 +1,17 @@
 // Fused qkv bias + rotate_half RoPE + K/V store (a8_bias_rope_store).
 //
-// Semantics follow serve/fast_kernels.py:139-187 (_bias_rope_store_kernel / bias_rope_store):
-// per token row r and head h of the fused [q | k | v] row,
-//   x  = f32(qkv[r, h*64 + d]) + f32(bias[h*64 + d])
-//   q/k: o[d] = bf16(x[d]*cos[pos, d] + sign(d) * x[(d+32) % 64] * sin[pos, d]),  sign = -1 for d < 32
+// Semantics follow serve/fast_kernels.py:139-187 (_bias_rope_store_kernel / bias_rope_store), for a head
+// dimension HD (a multiple of 16, <= 256; the reference's HD constexpr): per token row r and head h of the
+// fused [q | k | v] row,
+//   x  = f32(qkv[r, h*HD + d]) + f32(bias[h*HD + d])
+//   q/k: o[d] = bf16(x[d]*cos[pos, d] + sign(d) * x[(d+HD/2) % HD] * sin[pos, d]),  sign = -1 for d < HD/2
 //   v:   o[d] = bf16(x[d])
 // q goes to qo[r, h]; k / v go to kc / vc[slot[r], h', pos[r] % ring].
 //
-// MI355X layout: one thread owns the partner pair of 16-byte chunks (d = 8c..8c+7 and 32+8c..)
+// MI355X layout: one thread owns the partner pair of 16-byte chunks (d = 8c..8c+7 and HD/2+8c..)
 // of one head, so rotate_half needs no cross-lane traffic and every global access is a 128-bit
-// load/store; 4 consecutive lanes cover one 128-byte head row. The work is ~1 MB per layer at 192
-// slots: the kernel is launch-latency bound and sized as a single flat grid.
+// load/store; HD/16 consecutive lanes cover one head row (4 for the engine's HD = 64). The work is ~1 MB
+// per layer at 192 slots: the kernel is launch-latency bound and sized as a single flat grid.
 #include "rope.h"
 
 namespace a8 {
@@ -21,26 +22,28 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     const int32_t *__restrict__ pos, const int32_t *__restrict__ slot, int R,
     uint16_t *__restrict__ qo, int64_t s_qo_r, int64_t s_qo_h,
     uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
-    int cache_rows, int cache_len, int nq, int nkv, int ring) {
-  warm_kernargs<164>();  // the explicit arguments above span 0x00-0xa3
+    int cache_rows, int cache_len, int nq, int nkv, int ring, int hd) {
+  warm_kernargs<168>();  // the explicit arguments above span 0x00-0xa7
   const int H = nq + 2 * nkv;
-  const uint32_t per = 4u * (uint32_t)H;  // threads per row (the host keeps R * per below 2^31)
+  const int np = hd >> 4;                  // chunk pairs (threads) per head
+  const int half = hd >> 1;                // the partner chunk's offset
+  const uint32_t per = (uint32_t)np * (uint32_t)H;  // threads per row (the host keeps R * per below 2^31)
   const uint32_t t = blockIdx.x * 256u + threadIdx.x;
   if (t >= (uint32_t)R * per) return;
   const int r = (int)(t / per);
   const int rem = (int)(t - (uint32_t)r * per);
-  const int h = rem >> 2, c = rem & 3;
+  const int h = rem / np, c = rem - h * np;
 
   // Every load that does not depend on the position goes out before anything waits for it; the position
   // check only decides the stores (so the loads are not held behind it).
   const int p = pos[r];
   const int64_t sl = slot[r];
-  const uint16_t *src = qkv + (int64_t)r * s_qkv + h * 64;
-  const u32x4 wlo = ld16(src + 8 * c), whi = ld16(src + 32 + 8 * c);
+  const uint16_t *src = qkv + (int64_t)r * s_qkv + h * hd;
+  const u32x4 wlo = ld16(src + 8 * c), whi = ld16(src + half + 8 * c);
   u32x4 blo{0u, 0u, 0u, 0u}, bhi{0u, 0u, 0u, 0u};
   if (bias) {
-    blo = ld16(bias + h * 64 + 8 * c);
-    bhi = ld16(bias + h * 64 + 32 + 8 * c);
+    blo = ld16(bias + h * hd + 8 * c);
+    bhi = ld16(bias + h * hd + half + 8 * c);
   }
   const bool in_tab = p >= 0 && p < n_tab;  // a position outside the RoPE tables: the row writes nothing
   const int sidx = p % ring;
@@ -54,13 +57,13 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     rope_narrow(xl, xh, olo, ohi);
     uint16_t *dst = vc + sl * s_kb + (int64_t)(h - nq - nkv) * s_kh + (int64_t)sidx * s_ks;
     st16(dst + 8 * c, olo);
-    st16(dst + 32 + 8 * c, ohi);
+    st16(dst + half + 8 * c, ohi);
     return;
   }
 
   const int pc = in_tab ? p : 0;  // the host launches nothing when the tables are empty
   const uint16_t *crow = cos_tab + (int64_t)pc * s_cs, *srow = sin_tab + (int64_t)pc * s_cs;
-  rope_rotate(xl, xh, ld16(crow + 8 * c), ld16(crow + 32 + 8 * c), ld16(srow + 8 * c), ld16(srow + 32 + 8 * c),
+  rope_rotate(xl, xh, ld16(crow + 8 * c), ld16(crow + half + 8 * c), ld16(srow + 8 * c), ld16(srow + half + 8 * c),
               olo, ohi);
   if (!in_tab) return;
   uint16_t *dst;
@@ -71,7 +74,7 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     dst = kc + sl * s_kb + (int64_t)(h - nq) * s_kh + (int64_t)sidx * s_ks;
   }
   st16(dst + 8 * c, olo);
-  st16(dst + 32 + 8 * c, ohi);
+  st16(dst + half + 8 * c, ohi);
 }
 
 static inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -86,7 +89,8 @@ extern "C" int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bi
                                   int cache_rows, int cache_len,
                                   int nq, int nkv, int hd, int ring, void *stream) {
   using namespace a8;
-  if (hd != 64) return set_error(A8_EUNSUP, "bias_rope_store: head_dim %d not supported (64 only)", hd);
+  if (hd <= 0 || hd > 256 || hd % 16)
+    return set_error(A8_EUNSUP, "bias_rope_store: head_dim %d not supported (a multiple of 16 up to 256)", hd);
   if (R < 0 || nq <= 0 || nkv <= 0 || ring <= 0 || n_tab < 0 || cache_rows < 0 || cache_len < 0)
     return set_error(A8_EINVAL, "bias_rope_store: bad sizes R=%d nq=%d nkv=%d ring=%d n_tab=%d", R, nq, nkv,
                      ring, n_tab);
@@ -96,13 +100,13 @@ extern "C" int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bi
   if (!al16(qkv) || !al16(cos_tab) || !al16(sin_tab) || !al16(qo) || !al16(kc) || !al16(vc) ||
       (bias && !al16(bias)) || (s_qkv | s_cs | s_qo_r | s_qo_h | s_kb | s_kh | s_ks) & 7)
     return set_error(A8_EALIGN, "bias_rope_store: pointers must be 16-byte aligned and strides multiples of 8");
-  const int64_t threads = (int64_t)R * (nq + 2 * nkv) * 4;
+  const int64_t threads = (int64_t)R * (nq + 2 * nkv) * (hd / 16);
   if (threads >= (int64_t)1 << 31) return set_error(A8_EUNSUP, "bias_rope_store: %d rows x %d heads too many", R, nq + 2 * nkv);
   if (n_tab == 0) return 0;  // no position is inside the tables: nothing is written
   const unsigned grid = (unsigned)((threads + 255) / 256);
   hipLaunchKernelGGL(k_bias_rope_store, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t *)qkv, s_qkv, (const uint16_t *)bias, (const uint16_t *)cos_tab,
                      (const uint16_t *)sin_tab, s_cs, n_tab, pos, slot, R, (uint16_t *)qo, s_qo_r, s_qo_h,
-                     (uint16_t *)kc, (uint16_t *)vc, s_kb, s_kh, s_ks, cache_rows, cache_len, nq, nkv, ring);
+                     (uint16_t *)kc, (uint16_t *)vc, s_kb, s_kh, s_ks, cache_rows, cache_len, nq, nkv, ring, hd);
   return (int)hipGetLastError();
 }

@@ -258,7 +258,11 @@ class DecodeAttention:
         The rotated q is an intermediate of the pair that the engine never reads back: with write_q=False
         it is not written (a saving of ~1 us per layer at the peak load). One difference where the
         reference is undefined: a row whose position lies outside the RoPE tables attends with q = 0 here
-        (the two calls leave its q row unwritten)."""
+        (the two calls leave its q row unwritten). A head_dim other than 64 takes the two calls (its kernel
+        has no fused store)."""
+        if self.hd != 64:
+            bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd, ring=ring)
+            return self(q, kc, vc, lens, out, nsplit, rowmap=rowmap, phases=phases)
         R = _check_store(qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, self.nq, self.nkv, self.hd, ring)
         kind, shape = self.schedule(R, kc.shape[2], nsplit, fused=True)
         _check_i32("lens", lens, R)

@@ -40,7 +40,7 @@ extern "C" {
 
 #define A8_EINVAL  (-1) /* shape / count argument out of range */
 #define A8_EALIGN  (-2) /* pointer or stride not 16-byte aligned */
-#define A8_EUNSUP  (-3) /* configuration this build does not implement (e.g. head_dim != 64) */
+#define A8_EUNSUP  (-3) /* configuration this build does not implement (e.g. head_dim 96) */
 #define A8_EWSPACE (-4) /* decode workspace too small for b * nsplit row-splits */
 
 /* Library version string, "a8attn <version> gfx950 src:<hash>", the hash being that of the sources the library
@@ -68,7 +68,7 @@ const char *a8_hip_runtime_path(void);
  *                                                               [slot[r], h, pos[r] % ring, :]
  * Per row r and head h: x = f32(qkv) + f32(bias); q/k: o = bf16(x*cos + sign*x[(d+hd/2)%hd]*sin)
  * with sign = -1 for d < hd/2, evaluated without fused multiply-add; v: bf16(x).
- * hd must be 64.
+ * hd: a multiple of 16 up to 256 (the engine's 64, and 128).
  */
 int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bias,
                        const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab,
@@ -100,8 +100,11 @@ int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bias,
  * phases  bit 0: run the split kernel, bit 1: run the combine kernel (3 = both; the normal value).
  *         Running them separately lets a caller time each kernel. With counters, bit 1 is ignored.
  * Rows with lens == 0 produce NaN (0/0), exactly as the reference's combine does.
- * The cache positions must be contiguous rows (s_ks == hd == 64, true of every reference cache view);
- * otherwise A8_EUNSUP.
+ * The cache positions must be contiguous rows (s_ks == hd, true of every reference cache view);
+ * otherwise A8_EUNSUP. hd: 64, or 128 (the generic-head kernel: one launch whatever nsplit / waves, the
+ * workspace and counters unused; same results up to fp32 rounding). The decode entry points below
+ * (_stream, _flat, _noalloc) take hd 128 the same way; the fused store + decode ones (a8_store_decode_*)
+ * take 64 only (a caller with hd 128 calls a8_bias_rope_store, then the decode).
  */
 int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
                    const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
@@ -267,7 +270,7 @@ int a8_store_decode_stream(const void *qkv, int64_t s_qkv, const void *bias,
  * bq0, bn, bslot, bpos0 [nblk] int32: block j covers packed rows [bq0, bq0 + bn) (bn <= bm) at
  *         positions [bpos0, bpos0 + bn) of cache row bslot; keys [0, bpos0 + bn) are attended with
  *         key <= query position. Blocks with bn <= 0 are no-ops (graph-mode padding).
- * group   q heads per kv head (nq / nkv); bm must be 64; hd must be 64.
+ * group   q heads per kv head (nq / nkv); bm must be 64; hd 64, or 128 (the generic-head kernel).
  */
 int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
                     const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
@@ -287,7 +290,8 @@ int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
  * kc_all, vc_all  [layers, cache_rows, nkv, cache_len, hd] strides (d_l, d_r, d_h, d_p, 1) (shared)
  * slots           [n] int32: kc_all[l, slots[i], h, p] = k[l, h, p] and vc_all likewise, p < Lp.
  *                 A slot outside [0, cache_rows) is skipped (the reference would raise).
- * Positions must be contiguous rows on both sides (s_p == d_p == hd == 64); Lp <= cache_len.
+ * Positions must be contiguous rows on both sides (s_p == d_p == hd; hd a multiple of 8 up to 256);
+ * Lp <= cache_len.
  */
 int a8_prefix_copy(const void *k, const void *v, int64_t s_l, int64_t s_h, int64_t s_p,
                    void *kc_all, void *vc_all, int64_t d_l, int64_t d_r, int64_t d_h, int64_t d_p,

@@ -60,8 +60,9 @@ def _store_args(**kw):
 
 def test_store_rejects_before_launch(a8):
     lib = a8.load_library()
-    assert lib.a8_bias_rope_store(*_store_args(hd=128)) == -3
-    assert b"head_dim 128" in lib.a8_last_error()
+    assert lib.a8_bias_rope_store(*_store_args(hd=72)) == -3          # not a multiple of 16
+    assert b"head_dim 72" in lib.a8_last_error()
+    assert lib.a8_bias_rope_store(*_store_args(hd=512)) == -3
     assert lib.a8_bias_rope_store(*_store_args(ring=0)) == -1
     assert lib.a8_bias_rope_store(*_store_args(qkv=24)) == -2          # misaligned pointer
     assert lib.a8_bias_rope_store(*_store_args(s_qkv=1151)) == -2      # stride not a multiple of 8
@@ -79,7 +80,7 @@ def _decode_args(**kw):
 
 def test_decode_rejects_before_launch(a8):
     lib = a8.load_library()
-    assert lib.a8_decode_attn(*_decode_args(hd=128)) == -3
+    assert lib.a8_decode_attn(*_decode_args(hd=96)) == -3               # 64 or 128
     assert lib.a8_decode_attn(*_decode_args(nq=34, nkv=2)) == -3        # group 17 > 16
     assert lib.a8_decode_attn(*_decode_args(nq=15)) == -1               # nq not a multiple of nkv
     assert lib.a8_decode_attn(*_decode_args(waves=3)) == -1
@@ -91,6 +92,16 @@ def test_decode_rejects_before_launch(a8):
     assert lib.a8_decode_attn(*_decode_args(b=3, nsplit=2, ws=6, counters=16, n_counters=5)) == -4
     assert b"counters" in lib.a8_last_error()
     assert lib.a8_decode_attn(*_decode_args(nsplit=2, ws=4, counters=16, n_counters=2, phases=2)) == -1
+
+
+def test_fused_decode_refuses_other_head_dims(a8):
+    """The fused store + decode kernels are head_dim 64 only: 128 is refused before any launch (callers make
+    the two calls, as DecodeAttention.store_and_attend does)."""
+    lib = a8.load_library()
+    store = [16, 1152, None, 16, 16, 64, 8, 16, 16, None, 896, 64]
+    dec = [16, 16, 1024, 512, 128, 1, 8, 16, None, 16, 896, 64, 16, 16, 4]
+    st = lib.a8_store_decode_split(*store, *dec, None, 0, 1, 14, 2, 128, 1 << 30, 1, 4, 0.125, 3, None)
+    assert st == -3 and b"head_dim 128" in lib.a8_last_error()
 
 
 def _prefill_args(**kw):

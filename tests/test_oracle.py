@@ -127,9 +127,11 @@ def test_store_touches_only_slot_positions(ref):
         assert changed.sum() == len(want) * cache.shape[1]
 
 
-def test_store_rotation_closed_form(ref):
-    """q/k outputs equal the float64 rotation of (qkv + bias) to within bf16 rounding."""
-    nq, nkv, hd = 14, 2, 64
+@pytest.mark.parametrize("hd", [64, 128])
+def test_store_rotation_closed_form(ref, hd):
+    """q/k outputs equal the float64 rotation of (qkv + bias) to within bf16 rounding (the engine's head_dim
+    and 128, which the reference's generic-HD kernel also serves)."""
+    nq, nkv = 14, 2
     g = torch.Generator().manual_seed(3)
     R, W = 9, (nq + 2 * nkv) * hd
     qkv, bias = randn_bf16(g, R, W), randn_bf16(g, W, std=0.02)
@@ -144,8 +146,8 @@ def test_store_rotation_closed_form(ref):
     c = cos.double().numpy()[pos.numpy()][:, None]
     s = sin.double().numpy()[pos.numpy()][:, None]
     d = np.arange(hd)
-    sign = np.where(d < 32, -1.0, 1.0)
-    rot = x[:, :nq + nkv] * c + sign * x[:, :nq + nkv][..., (d + 32) % hd] * s
+    sign = np.where(d < hd // 2, -1.0, 1.0)
+    rot = x[:, :nq + nkv] * c + sign * x[:, :nq + nkv][..., (d + hd // 2) % hd] * s
     got_q = qo.double().numpy()
     got_k = np.stack([kc[r, :, pos[r]].double().numpy() for r in range(R)])
     got_v = np.stack([vc[r, :, pos[r]].double().numpy() for r in range(R)])
@@ -168,10 +170,11 @@ def test_decode_golden(ref, nsplit):
     assert err <= 1e-2, err
 
 
-def test_decode_textbook_random(ref):
+@pytest.mark.parametrize("hd", [64, 128])
+def test_decode_textbook_random(ref, hd):
     """Random lengths incl. exact tile multiples, against a float64 full-softmax restatement."""
     g = torch.Generator().manual_seed(5)
-    nq, nkv, hd, S, b = 14, 2, 64, 300, 7
+    nq, nkv, S, b = 14, 2, 300, 7
     q = randn_bf16(g, b, nq, hd)
     kc, vc = randn_bf16(g, b, nkv, S, hd), randn_bf16(g, b, nkv, S, hd)
     lens = torch.tensor([1, 2, 63, 64, 65, 128, 300], dtype=torch.int32)
@@ -180,7 +183,7 @@ def test_decode_textbook_random(ref):
         L = int(lens[i])
         for h in range(nq):
             K, V = kc[i, h // 7, :L].double(), vc[i, h // 7, :L].double()
-            p = torch.softmax(K @ q[i, h].double() / 8.0, 0)
+            p = torch.softmax(K @ q[i, h].double() * hd ** -0.5, 0)
             assert (out[i, h] - p @ V).abs().max() <= 1e-2
 
 
@@ -250,10 +253,11 @@ def test_prefill_golden(ref):
     assert err <= 1e-2, err
 
 
-def test_prefill_row_equals_decode(ref):
+@pytest.mark.parametrize("hd", [64, 128])
+def test_prefill_row_equals_decode(ref, hd):
     """Row j of a request attends exactly what decode with lens = p0 + j + 1 attends."""
     g = torch.Generator().manual_seed(8)
-    nq, nkv, hd, S = 14, 2, 64, 260
+    nq, nkv, S = 14, 2, 260
     kc, vc = randn_bf16(g, 2, nkv, S, hd), randn_bf16(g, 2, nkv, S, hd)
     ns, p0s, slots = [100, 37], [150, 0], [1, 0]
     R = sum(ns)
