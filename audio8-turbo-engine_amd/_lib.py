@@ -45,6 +45,7 @@ SIGNATURES = {
                                  _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _F, _P]),
     "a8_rmsnorm": (_I, [_P, _L, _P, _L, _P, _P, _L, _P, _L, _I, _I, _F, _P]),
     "a8_silu_mul": (_I, [_P, _L, _P, _L, _I, _I, _P]),
+    "a8_gemm_small": (_I, [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
     "a8_conv_cl": (_I, [_P, _L, _L, _P, _L, _L, _L, _I, _P, _P, _L, _L, _P, _L, _L, _P, _P,
                         _I, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
     "a8_conv_cl_ws_bytes": (_L, [_I, _I, _I, _I, _I, _I]),

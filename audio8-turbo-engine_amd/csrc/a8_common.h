@@ -61,6 +61,12 @@ __device__ __forceinline__ rsrc_t make_rsrc_wave(const void *base, uint32_t byte
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
   return make_rsrc(reinterpret_cast<const void *>(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
 }
+// Partials exchanged between the workgroups of one launch (the in-kernel merges): a partial goes out with
+// agent-coherent (sc1) buffer stores, which write through the XCD's L2; once they have completed (vmcnt(0))
+// an atomic on the unit's counter makes the arrival known, and the last arrival reads every partial with sc1
+// loads issued after its atomic returned. Only the bytes exchanged are kept coherent: an agent-scope fence
+// would write back and invalidate the whole L2 for every partial, under the other workgroups' loads.
+constexpr int kSC1 = 16;  // buffer cache policy: sc1, coherent across the device (agent scope)
 // 4-byte vector-memory load at byte offset `off`. Unlike a scalar load of a uniform address, it is
 // counted with the tile loads (vmcnt), so waiting for it never waits for the LDS traffic or vice versa.
 __device__ __forceinline__ int bld4(rsrc_t r, uint32_t off) {

@@ -267,12 +267,7 @@ __device__ __forceinline__ void compute_step(KTile (&T)[NT], uint16_t *vbuf, int
   }
 }
 
-// ---- Partials exchanged between the workgroups of one launch (the in-kernel merges) ----
-// A partial goes out with agent-coherent (sc1) buffer stores, which write through the XCD's L2; once they
-// have completed (vmcnt(0)) an atomic on the unit's counter makes the arrival known, and the last arrival
-// reads every partial with sc1 loads issued after its atomic returned. Only the bytes exchanged are kept
-// coherent: an agent-scope fence would write back and invalidate the whole L2 for every partial.
-constexpr int kSC1 = 16;  // buffer cache policy: sc1, coherent across the device (agent scope)
+// ---- Partials exchanged between the workgroups of one launch (the in-kernel merges; kSC1) ----
 
 // Called by a whole wave after its partial's stores: true in the wave that brings the count to `arrivals`,
 // which also puts the counter back to 0 for the next launch (every arrival of this one is in).

@@ -1,0 +1,297 @@
+// Small-M GEMM for the slow-AR layer's projections (a8_gemm_small): out[M, N] = bf16(X[M, K] . W[N, K]^T), fp32
+// accumulation, for the decode tick's token counts (M <= 192: the 192 slots of C3). It takes the place of the
+// reference's per-shape GEMM choice for small M (serve/fast_kernels.py:413-519, GemmDispatch: cuBLAS or a tuned
+// Triton config; here hipBLASLt or this kernel, chosen per (M, N, K) by timing, as there).
+//
+// What bounds it at these shapes: the weights (2-17 MB per projection) stream from HBM once, and every workgroup
+// re-reads the token rows X (344 KB at K = 896) from L2, at ~60 bytes per clock per CU (measured) -- so the
+// workgroup tile is all M rows x 64 weight rows, and K is split across workgroups only for narrow N.
+//
+// One workgroup = 64 weight rows (four 16-row n-subtiles) x all token rows (MT 16-row m-subtiles, MT even)
+// x a range of 64-wide k chunks. The chunk's X rows and W rows go from HBM / L2 into LDS by DMA (16-byte
+// pieces, row r's chunks permuted by chunk ^= r & 7 through the source offsets so the operand reads of
+// consecutive rows spread over the banks): the weights through a ring of 8 slots with 7 chunks in flight (they
+// come from HBM: ~1.5 us away), the token rows through a ring of 3 with 2 in flight (L2). Wave w computes
+// n-subtiles 2(w&1), 2(w&1)+1 x m-subtiles (w>>1) MT/2.. : per 32-k step two W operands and MT/2 X operands from
+// LDS, MT MFMAs (v_mfma_f32_16x16x32_bf16: A = W rows, B = X^T, so the C layout holds 4 consecutive output
+// columns of one token row per lane). The DMA is inline asm the compiler does not track; the kernel waits for
+// it with vmcnt counts (every wave issues the same number of requests per chunk, and loads complete in order).
+// The token rows may also be split into row blocks (blockIdx.z), for more workgroups where N is narrow. With
+// several k splits each workgroup writes fp32 partials (sc1 stores, coherent across the XCDs) and the tile's
+// last workgroup to arrive, known from a counter at the start of the workspace, sums them in a fixed order in
+// the same launch (no device-scope fence: that would write back and invalidate the whole XCD L2 under the
+// other workgroups' loads, measured 5-20x slower than the GEMM).
+#include <algorithm>
+
+#include "a8_common.h"
+
+namespace a8 {
+namespace {
+
+constexpr int kGmNB = 64;   // weight rows per workgroup
+constexpr int kGmKC = 64;   // k per chunk
+constexpr int kGmWSlots = 8;  // W ring slots: 7 chunks of weights in flight (HBM latency), X only 2 (L2)
+constexpr int kGmMaxM = 192;
+constexpr int kGmCntBytes = 4096;  // k splits: the workspace starts with one 32-bit counter per tile (<= 1024)
+
+__device__ __forceinline__ void gm_dma(u32x4 rs, uint32_t lds, uint32_t voff) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "{m0}"(lds), "v"(voff), "s"(rs) : "memory");
+}
+__device__ __forceinline__ u32x4 gm_rsrc(const void *base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xFFFFu, bytes, 0x00020000u};
+}
+template <int N>
+__device__ __forceinline__ void gm_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+template <int MT, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__restrict__ x, int64_t ldx,
+                                                           const uint16_t *__restrict__ w, int64_t ldw,
+                                                           uint16_t *__restrict__ out, int64_t ldo,
+                                                           float *__restrict__ part, int32_t *__restrict__ cnt,
+                                                           int Mall, int N, int K, int cps, int S) {
+  static_assert(NW == 4 || NW == 8, "waves");
+  static_assert(MT >= 2 && MT * 16 <= kGmMaxM && (2 * MT) % NW == 0, "token subtiles");
+  constexpr int XB = MT * 16 * 128;        // X bytes per ring slot (token rows x 128 bytes)
+  constexpr int WB = kGmNB * 128;          // W bytes per ring slot
+  constexpr int DX = 2 * MT / NW;          // X requests per wave per chunk (2 MT of 1 KB)
+  constexpr int DW = 8 / NW;               // W requests per wave per chunk (8 of 1 KB)
+  constexpr int MH = 2 * MT / NW;          // m-subtiles per wave (waves: 2 along n x NW / 2 along m)
+  __shared__ __attribute__((aligned(16))) char lds[3 * XB + kGmWSlots * WB];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int r16 = lane & 15, g = lane >> 4;
+  const int nt = blockIdx.x, sp = blockIdx.y;
+  // row block z: token rows z MT 16 .. of the Mall rows (the host picks MT so that the blocks cover them)
+  const int mb0 = (int)blockIdx.z * MT * 16, M = min(MT * 16, Mall - mb0);
+  x += (int64_t)mb0 * ldx;
+  out += (int64_t)mb0 * ldo;
+  const int nch = K / kGmKC;
+  const int c0 = sp * cps, c1 = min(c0 + cps, nch);
+  if (c0 >= c1) return;  // (the host sizes the grid so that this does not happen)
+  const int n0 = nt * kGmNB;
+
+  // sources: rows past M / N read as zeros (their offsets lie past the range: ld >= K); a chunk past the
+  // workgroup's range is requested from an empty range (zeros into a free slot, no memory traffic), so every
+  // wave issues the same requests every chunk and the waits below are constant
+  const u32x4 xr = gm_rsrc(x, (uint32_t)((int64_t)(M - 1) * ldx * 2 + (int64_t)K * 2));
+  const u32x4 wr = gm_rsrc(w + (int64_t)n0 * ldw, (uint32_t)((int64_t)(N - n0 - 1) * ldw * 2 + (int64_t)K * 2));
+  u32x4 xr0 = xr, wr0 = wr;
+  xr0[2] = 0u;
+  wr0[2] = 0u;
+  const uint32_t prow = (uint32_t)(lane >> 3), pch = (uint32_t)(lane & 7);
+  uint32_t xso[DX], xdo[DX], wso[DW], wdo[DW];
+#pragma unroll
+  for (int j = 0; j < DX; ++j) {  // X instruction i = wv + NW j: token rows 8i..8i+7
+    const uint32_t i = (uint32_t)(wv + NW * j), row = 8u * i + prow;
+    xso[j] = row * (uint32_t)(ldx * 2) + ((pch ^ (row & 7u)) << 4);
+    xdo[j] = i * 1024u;
+  }
+#pragma unroll
+  for (int j = 0; j < DW; ++j) {  // W instruction i = wv + NW j: weight rows 8i..8i+7 of the tile
+    const uint32_t i = (uint32_t)(wv + NW * j), row = 8u * i + prow;
+    wso[j] = row * (uint32_t)(ldw * 2) + ((pch ^ (row & 7u)) << 4);
+    wdo[j] = i * 1024u;
+  }
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(lds);
+  const uint32_t wring = lds0 + 3u * XB;
+  auto issue_x = [&](int c, int slot) __attribute__((always_inline)) {
+    const u32x4 rs = c < c1 ? xr : xr0;
+    const uint32_t kb = (uint32_t)(c * kGmKC * 2);
+#pragma unroll
+    for (int j = 0; j < DX; ++j) gm_dma(rs, lds0 + (uint32_t)(slot * XB) + xdo[j], xso[j] + kb);
+  };
+  auto issue_w = [&](int c) __attribute__((always_inline)) {
+    const u32x4 rs = c < c1 ? wr : wr0;
+    const uint32_t kb = (uint32_t)(c * kGmKC * 2);
+    const uint32_t slot = (uint32_t)(c - c0) % (uint32_t)kGmWSlots;
+#pragma unroll
+    for (int j = 0; j < DW; ++j) gm_dma(rs, wring + slot * WB + wdo[j], wso[j] + kb);
+  };
+
+  // operand reads: lane (g, r16) takes row r16 of a subtile, k 8g..8g+7 of the 32-k step s (chunk 4s + g)
+  const int jn0 = 2 * (wv & 1), im0 = (wv >> 1) * MH;
+  f32x4 acc[2][MH];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < MH; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // W chunks c0 .. c0 + P - 1 (P = kGmWSlots - 1 in flight), then X chunks c0, c0 + 1; per chunk c: the wait,
+  // the meeting (everyone is done with chunk c - 1, whose slots the next requests refill), X(c + 2), W(c + P)
+  constexpr int P = kGmWSlots - 1;
+#pragma unroll
+  for (int c = 0; c < P; ++c) issue_w(c0 + c);
+  issue_x(c0, 0);
+  issue_x(c0 + 1, 1);
+  int xs = 0;
+  for (int c = c0; c < c1; ++c) {
+    // X(c) in LDS (and W(c), requested earlier): at most the requests issued after X(c) outstanding
+    if (c == c0)
+      gm_wait_vm<DX>();
+    else if (c == c0 + 1)
+      gm_wait_vm<DX + DW>();
+    else
+      gm_wait_vm<DX + 2 * DW>();
+    lds_barrier();
+    issue_x(c + 2, xs == 0 ? 2 : xs - 1);
+    issue_w(c + P);
+    const char *sx = lds + xs * XB;
+    const char *sw = lds + 3 * XB + ((c - c0) % kGmWSlots) * WB;
+    // every operand of the chunk is read before its first product: one LDS round trip per chunk, not one per
+    // pair of products (the scheduler otherwise places each read just before its use)
+    u32x4 A[2][2], B[2][MH];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint32_t ch = (uint32_t)(4 * s + g);
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const uint32_t row = (uint32_t)(16 * (jn0 + a) + r16);
+        A[s][a] = ld16(sw + row * 128u + ((ch ^ (row & 7u)) << 4));
+      }
+#pragma unroll
+      for (int b = 0; b < MH; ++b) {
+        const uint32_t row = (uint32_t)(16 * (im0 + b) + r16);
+        B[s][b] = ld16(sx + row * 128u + ((ch ^ (row & 7u)) << 4));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int b = 0; b < MH; ++b)
+#pragma unroll
+        for (int a = 0; a < 2; ++a) acc[a][b] = mfma16x16x32(A[s][a], B[s][b], acc[a][b]);
+    xs = xs == 2 ? 0 : xs + 1;
+  }
+  // the requests past the range still write (zeros) into LDS: let them land before the workgroup ends
+  gm_wait_vm<0>();
+
+  // lane (g, r16) of tile (a, b): token row 16(im0 + b) + r16, output columns n0 + 16(jn0 + a) + 4g..+3
+  if (!part) {
+#pragma unroll
+    for (int b = 0; b < MH; ++b) {
+      const int m = 16 * (im0 + b) + r16;
+      if (m >= M) continue;
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int n = n0 + 16 * (jn0 + a) + 4 * g;
+        if (n < N)
+          st8(out + (int64_t)m * ldo + n,
+              u32x2{pack_bf16x2(acc[a][b][0], acc[a][b][1]), pack_bf16x2(acc[a][b][2], acc[a][b][3])});
+      }
+    }
+    return;
+  }
+
+  // k splits: the partial [S][Mall][N] goes out with sc1 stores; the tile's last workgroup to arrive sums the
+  // S partials in the order s = 0 .. S-1, whichever it is (the result does not depend on the arrival order),
+  // and the counter goes back to zero for the next launch
+  const rsrc_t pr = make_rsrc(part, (uint32_t)((int64_t)S * Mall * N * 4));
+#pragma unroll
+  for (int b = 0; b < MH; ++b) {
+    const int m = 16 * (im0 + b) + r16;
+    if (m >= M) continue;
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int n = n0 + 16 * (jn0 + a) + 4 * g;
+      if (n < N)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[a][b]), pr,
+                                               (uint32_t)((((int64_t)sp * Mall + mb0 + m) * N + n) * 4), 0, kSC1);
+    }
+  }
+  __shared__ int last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial has reached the coherent level
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();                     // ... and every wave's
+  if (threadIdx.x == 0) {
+    int32_t *c = cnt + (int)blockIdx.z * (int)gridDim.x + nt;
+    const int old = atomicAdd(c, 1);
+    last = old == S - 1;
+    if (old == S - 1) *c = 0;  // every arrival of this launch is in
+  }
+  __syncthreads();
+  if (!last) return;
+  const int ncol = min(kGmNB, N - n0) >> 3;  // 8-column groups of the tile (N is a multiple of 8)
+  for (int t = threadIdx.x; t < M * 8; t += 64 * NW) {
+    const int m = t >> 3, q = t & 7;
+    if (q >= ncol) continue;
+    const int n = n0 + 8 * q;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint32_t o0 = (uint32_t)((((int64_t)mb0 + m) * N + n) * 4), os = (uint32_t)((int64_t)Mall * N * 4);
+    // four splits' loads in flight at a time (past S: offsets past the range, zeros, not added)
+    for (int j = 0; j < S; j += 4) {
+      u32x4 lo[4], hi[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t o = j + u < S ? o0 + (uint32_t)(j + u) * os : 0xFFFFFFE0u;
+        lo[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, o, 0, kSC1));
+        hi[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, o + 16u, 0, kSC1));
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (j + u >= S) break;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] += __uint_as_float(lo[u][i]);
+          v[4 + i] += __uint_as_float(hi[u][i]);
+        }
+      }
+    }
+    st16(out + (int64_t)m * ldo + n, u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                                            pack_bf16x2(v[6], v[7])});
+  }
+}
+
+bool al16g(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+}  // namespace a8
+
+extern "C" int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo,
+                             void *ws, int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, void *stream) {
+  using namespace a8;
+  if (M < 0 || N < 0 || K < 0 || splits < 1 || mblocks < 1)
+    return set_error(A8_EINVAL, "gemm_small: bad sizes M=%d N=%d K=%d splits=%d mblocks=%d", M, N, K, splits, mblocks);
+  if (M == 0 || N == 0) return 0;
+  if (M > kGmMaxM || K == 0 || K % kGmKC || N % 8)
+    return set_error(A8_EUNSUP, "gemm_small: M=%d N=%d K=%d outside M <= %d, K a multiple of %d, N of 8", M, N, K,
+                     kGmMaxM, kGmKC);
+  if (!x || !w || !out) return set_error(A8_EINVAL, "gemm_small: null pointer");
+  if (!al16g(x) || !al16g(w) || !al16g(out) || (ldx | ldw | ldo) & 7 || ldx < K || ldw < K || ldo < N)
+    return set_error(A8_EALIGN, "gemm_small: pointers must be 16-byte aligned, leading dims multiples of 8 and "
+                     ">= the row length");
+  if ((int64_t)(M - 1) * ldx * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32) ||
+      (int64_t)(N - 1) * ldw * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32))
+    return set_error(A8_EUNSUP, "gemm_small: operands span more than 4 GiB");
+  const int nch = K / kGmKC;
+  const int S = std::min(splits, nch);
+  const int cps = (nch + S - 1) / S;
+  const int S_used = (nch + cps - 1) / cps;  // every split has at least one chunk
+  if (S_used > 1 && (!ws || ws_bytes < kGmCntBytes + (int64_t)S_used * M * N * 4 || !al16g(ws)))
+    return set_error(A8_EWSPACE, "gemm_small: %d splits need a 16-byte aligned workspace of %lld bytes", S_used,
+                     (long long)(kGmCntBytes + (int64_t)S_used * M * N * 4));
+  if (S_used > 1 && (int64_t)S_used * M * N * 4 >= ((int64_t)1 << 32))
+    return set_error(A8_EUNSUP, "gemm_small: %d splits of %d x %d partials span more than 4 GiB", S_used, M, N);
+  // rows per block: an even number of 16-row subtiles covering M / mblocks; blocks that would be empty are dropped
+  const int MT = std::min(12, ((((M + mblocks - 1) / mblocks) + 31) / 32) * 2);
+  const int nmb = (M + MT * 16 - 1) / (MT * 16);
+  const int ntile = (N + kGmNB - 1) / kGmNB;
+  if (S_used > 1 && (int64_t)ntile * nmb > kGmCntBytes / 4)
+    return set_error(A8_EUNSUP, "gemm_small: %d x %d tiles exceed the %d counters for k splits", ntile, nmb,
+                     kGmCntBytes / 4);
+  int32_t *cnt = S_used > 1 ? (int32_t *)ws : nullptr;
+  float *part = S_used > 1 ? (float *)((char *)ws + kGmCntBytes) : nullptr;
+  const dim3 grid((unsigned)ntile, (unsigned)S_used, (unsigned)nmb);
+  const hipStream_t st = (hipStream_t)stream;
+  // 8 waves (two per SIMD, one covering the other's LDS round trips) where the token subtiles split four ways
+  const bool w8 = MT % 4 == 0;
+  auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
+            : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
+  hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, st, (const uint16_t *)x, ldx, (const uint16_t *)w, ldw,
+                     (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used);
+  return (int)hipGetLastError();
+}

@@ -482,6 +482,130 @@ def silu_mul(gu, out=None):
     return y
 
 
+def gemm_ws_bytes(M, N, splits):
+    """Workspace bytes gemm_small needs for `splits` k ranges (0 for one): 4096 bytes of tile counters, then
+    the fp32 partials. Allocate it zeroed (torch.zeros): every call leaves the counters at zero."""
+    return 0 if splits <= 1 else 4096 + splits * M * N * 4
+
+
+def gemm_small(x, w, out=None, splits=1, ws=None, mblocks=1):
+    """out[M, N] = x[M, K] @ w[N, K]^T with this package's small-M kernel (a8_gemm_small): bf16, fp32
+    accumulation, M <= 192, K a multiple of 64, N of 8. splits > 1 splits K across workgroups, with fp32
+    partials in `ws` (a device tensor of at least gemm_ws_bytes(M, N, splits) bytes, zeroed when allocated)
+    summed in a fixed order by each tile's last workgroup;
+    mblocks > 1 splits the token rows into blocks (more workgroups for narrow N). Neither changes the result.
+    Raises (A8Error) where the kernel does not apply; GemmDispatch only calls it where it does."""
+    _check_bf16("x", x, 2)
+    _check_bf16("w", w, 2)
+    M, K = x.shape
+    N = w.shape[0]
+    _need(w.shape[1] == K, f"w shape {tuple(w.shape)} does not match K = {K}")
+    y = out if out is not None else torch.empty(M, N, dtype=x.dtype, device=x.device)
+    _check_bf16("out", y, 2)
+    _need(y.shape[0] == M and y.shape[1] == N, f"out shape {tuple(y.shape)} does not match [{M}, {N}]")
+    _check_device(x=x, w=w, out=y, ws=ws)
+    st = _lib.load().a8_gemm_small(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), y.data_ptr(), y.stride(0),
+                                   ws.data_ptr() if ws is not None else None,
+                                   ws.numel() * ws.element_size() if ws is not None else 0, M, N, K, int(splits),
+                                   int(mblocks), _lib.stream_of(x))
+    _lib.check(st, "gemm_small")
+    return y
+
+
+class GemmDispatch:
+    """Per-(M, N, K) choice between the library GEMM (torch.matmul -> hipBLASLt) and gemm_small, measured on
+    the running GPU at startup, outside graph capture (the reference's GemmDispatch, fast_kernels.py:413-519,
+    chooses between cuBLAS and tuned Triton configs the same way). `tune(weights, Ms)` times both (with each
+    split count) for every weight shape and token count; `__call__(x, w)` then takes the faster, and the
+    library GEMM for shapes not tuned. The split partials share one workspace sized by tune (calls on one
+    instance run in stream order)."""
+
+    SPLITS = (1, 2, 3, 4, 7, 8, 14)
+    MBLOCKS = (1, 2, 3, 6)
+
+    def __init__(self):
+        self.small = {}     # (M, N, K) -> (splits, mblocks) or None (library GEMM)
+        self.enabled = True
+        self.ws = None
+        self.log = []
+
+    @staticmethod
+    def _time(fns, n=20):
+        """Mean time of one call, from a graph of n calls cycling through `fns` (one per weight of the shape,
+        so that with a model's layers the weights are not all served from cache)."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for f in fns[:2]:
+                f()
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fns[i % len(fns)]()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (2 * n)
+
+    @staticmethod
+    def applies(M, N, K):
+        return 0 < M <= 192 and K % 64 == 0 and N % 8 == 0
+
+    @torch.inference_mode()
+    def tune(self, weights, Ms, log=None):
+        """weights: iterable of [N, K] bf16 tensors (a model's projections: the calls are timed cycling through
+        every weight of a shape, as the model's layers would); Ms: token counts."""
+        shapes = {}
+        for w in weights:
+            shapes.setdefault((w.shape[0], w.shape[1]), []).append(w)
+        need = 0
+        for (N, K), ws_ in shapes.items():
+            for M in sorted(set(int(m) for m in Ms)):
+                if not self.applies(M, N, K):
+                    self.small[(M, N, K)] = None
+                    continue
+                x = torch.randn(M, K, device=ws_[0].device, dtype=ws_[0].dtype)
+                y = torch.empty(M, N, device=ws_[0].device, dtype=ws_[0].dtype)
+                n = max(20, len(ws_))
+                best, best_t = None, self._time([lambda w=w: torch.matmul(x, w.t(), out=y) for w in ws_], n)
+                lib_t = best_t
+                for sp in self.SPLITS:
+                    if sp > K // 64:
+                        continue
+                    wsp = torch.zeros(gemm_ws_bytes(M, N, sp), dtype=torch.uint8, device=x.device) if sp > 1 else None
+                    for mb in self.MBLOCKS:
+                        if mb > 1 and (M + mb - 1) // mb < 32:
+                            continue
+                        t = self._time([lambda w=w: gemm_small(x, w, y, splits=sp, ws=wsp, mblocks=mb) for w in ws_], n)
+                        if t < best_t:
+                            best, best_t = (sp, mb), t
+                self.small[(M, N, K)] = best
+                if best is not None and best[0] > 1:
+                    need = max(need, gemm_ws_bytes(M, N, best[0]))
+                self.log.append(((M, N, K), lib_t, best, best_t))
+                if log:
+                    log(f"[gemm] M={M} N={N} K={K}: library {lib_t * 1e3:.1f} us, "
+                        + (f"gemm_small splits={best[0]} mblocks={best[1]} {best_t * 1e3:.1f} us" if best else "kept"))
+        if need and (self.ws is None or self.ws.numel() < need):
+            dev = next(iter(shapes.values()))[0].device
+            self.ws = torch.zeros(need, dtype=torch.uint8, device=dev)  # the tile counters start at zero
+
+    def __call__(self, x, w):
+        if not self.enabled or x.dim() != 2 or x.stride(1) != 1:
+            return torch.matmul(x, w.t())
+        best = self.small.get((x.shape[0], w.shape[0], w.shape[1]))
+        if best is None:
+            return torch.matmul(x, w.t())
+        sp, mb = best
+        return gemm_small(x, w, splits=sp, ws=self.ws if sp > 1 else None, mblocks=mb)
+
+
 _F16 = torch.float16
 
 

@@ -4,8 +4,9 @@ Per layer (fast_engine.py:117-138): qkv = h @ wqkv^T -> bias + RoPE + K/V store 
 attention -> a = o @ wo^T -> (h, res) = rmsnorm(a, ln2, residual=res) -> m = silu_mul(h @ w13^T) @ w2^T ->
 (h, res) = rmsnorm(m, next ln1 or the final norm, residual=res). The attention is AttnStack (this package's
 kernels, the reference's cache layout and store-then-attend order); the norms and the gated activation are
-this package's kernels (rmsnorm, silu_mul); the four projections are plain library GEMMs (torch.matmul ->
-hipBLASLt), exactly the reference's default `mm` (fast_engine.py:90).
+this package's kernels (rmsnorm, silu_mul); the four projections go through `mm`, the reference's argument
+(fast_engine.py:90): torch.matmul (hipBLASLt) by default, or a GemmDispatch, which takes this package's
+small-M GEMM (gemm_small) for the shapes where it measured faster.
 
 Weights are the reference's fused layout per layer: wqkv [(nq+2nkv)hd, hidden] (q/k rows already in
 rotate_half order, fast_engine.py:100-101), bqkv or None, wo [hidden, nq hd], w13 = cat(w1, w3) [2 inter,
@@ -46,7 +47,7 @@ class SlowStack:
     every row attends its own slot (AttnStack.forward)."""
 
     def __init__(self, layers, norm, nq, nkv, hd, eps, rope_base, max_rows, cache_rows, cache_len, max_pos, dev,
-                 nsplit_max=16, ring=None):
+                 nsplit_max=16, ring=None, mm=None):
         self.layers = layers
         self.norm = norm
         self.nq, self.nkv, self.hd, self.eps = nq, nkv, hd, float(eps)
@@ -54,10 +55,9 @@ class SlowStack:
                               nsplit_max=nsplit_max, ring=ring)
         self.kc_all, self.vc_all = self.attn.kc_all, self.attn.vc_all
         self.kc, self.vc = self.attn.kc, self.attn.vc
-
-    @staticmethod
-    def mm(x, w):
-        return torch.matmul(x, w.t())
+        # the projections' GEMM: the reference's `mm` argument (fast_engine.py:90) -- torch.matmul by default, or
+        # a GemmDispatch (this package's small-M kernel where it measured faster)
+        self.mm = mm if mm is not None else (lambda x, w: torch.matmul(x, w.t()))
 
     def forward(self, x, pos, slot, lens, nsplit=1, rowmap=True, plan=None, fuse=False):
         R = x.shape[0]

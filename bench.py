@@ -254,8 +254,27 @@ def per_config(a8, torch, dev, steps):
     wbytes = layers * 2 * (hidden * (NQ + 2 * NKV) * HD + hidden * NQ * HD + hidden * 2 * inter + inter * hidden)
     res["slow_ar_step"] = {"us_per_step": round(us, 1), "us_per_layer": round(us / layers, 2), "rows": b, "kv_len": S,
                            "hidden": hidden, "inter": inter, "weight_bytes": wbytes,
-                           "note": "the full slow-AR decode step around the attention path; synthetic weights"}
-    del g, st, wts, xbuf
+                           "note": "the full slow-AR decode step around the attention path; synthetic weights; "
+                                   "projections through hipBLASLt (the reference's default mm)"}
+    del g
+    # the same step with the projections through GemmDispatch: per shape, hipBLASLt or this package's small-M
+    # GEMM (gemm_small, with its split count and row blocks), whichever the timing at startup finds faster --
+    # timed cycling through the 24 layers' weights, as the step reads them
+    mm = a8.GemmDispatch()
+    mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b])
+    st.mm = mm
+    xbuf.copy_(x0)
+    g = capture(torch, lambda: st.forward(xbuf, pos, slot, lens_d, rowmap=False, fuse=True))
+    us2 = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
+    res["slow_ar_step_dispatch"] = {
+        "us_per_step": round(us2, 1), "us_per_layer": round(us2 / layers, 2),
+        "choices": {f"{N}x{K}": (None if c is None else {"splits": c[0], "mblocks": c[1]})
+                    for (M, N, K), c in mm.small.items()},
+        "tune_us": {f"{N}x{K}": [round(lt * 1e3, 2), None if bt is None else round(bt * 1e3, 2)]
+                    for (M, N, K), lt, _, bt in mm.log},
+        "note": "projections through GemmDispatch (library vs gemm_small per shape, timed at startup); "
+                "tune_us = [library, chosen] per call"}
+    del g, st, wts, xbuf, mm
     torch.cuda.empty_cache()
 
     # Codec window transformer (beside configs C1-C5): the same kernels on a 128-position

@@ -313,6 +313,26 @@ int a8_rmsnorm(const void *x, int64_t sx, const void *residual, int64_t sr, cons
 int a8_silu_mul(const void *gu, int64_t s_gu, void *y, int64_t s_y, int rows, int I, void *stream);
 
 /*
+ * Small-M GEMM for the slow-AR layer's projections (qkv, o, w13, w2 at the decode tick's token count):
+ * out[M, N] = bf16(x[M, K] . w[N, K]^T), fp32 accumulation. Takes the small-M side of the reference's
+ * per-shape GEMM choice (serve/fast_kernels.py:413-519, GemmDispatch.__call__: cuBLAS or a tuned Triton
+ * linear_triton, 395-410), which the package's GemmDispatch makes between this and hipBLASLt by timing.
+ * x [M, K] row stride ldx, w [N, K] row stride ldw (row-major: nn.Linear's weight), out [M, N] row stride ldo.
+ * M <= 192, K a multiple of 64, N a multiple of 8, 16-byte aligned pointers, leading dims multiples of 8 and
+ * at least the row length; else A8_EUNSUP / A8_EALIGN (the caller takes its library GEMM).
+ * splits: k ranges computed by separate workgroups (1 = none; clamped to K / 64, then to the count that gives
+ * every range a chunk: splits_used). With more than one, ws (16-byte aligned, >= 4096 + splits_used * M * N * 4
+ * bytes, else A8_EWSPACE) holds 1024 32-bit tile counters in its first 4096 bytes, then the fp32 partials; the
+ * last workgroup of each tile to finish sums them in a fixed order, in the same launch: deterministic. The
+ * counters must be zero before a workspace's first use (allocate it zeroed); every call leaves them zero.
+ * mblocks: row blocks the M token rows are split into (1 = all rows in each workgroup; a block holds an even
+ * number of 16-row subtiles, so fewer blocks may be used), for more workgroups where N is narrow. Neither
+ * changes the result. Two calls sharing ws must not overlap in time.
+ */
+int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo,
+                  void *ws, int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, void *stream);
+
+/*
  * The streaming vocoder's channels-last convolutions (the codec decoder's default conv path,
  * serve/fast_engine.py:218-233), fp16 storage:
  * a8_conv_cl replaces serve/fast_kernels.py:600-623 (conv_cl, kernel 551-597): for rows (b, t), t < TR,
