@@ -70,7 +70,10 @@ __device__ __forceinline__ u32x4 snake8(u32x4 v, const float *a, const float *ib
 
 constexpr int kSnakeMaxC = 1024;  // input channels a conv with the snake on its loads may have
 
-template <int WM, int NT, int KSUB, bool SNAKE>
+// RU: a whole residual unit (the reference's ru_fused, serve/fast_kernels.py:626-692), the 1x1 conv in the
+// k-tap conv's epilogue: h = acc + bias (fp32), snake with a2 / ib2 (fp32, one fp16 rounding), then
+// out = h' . w2 + b2 + res. Needs the whole channel width in one tile (Cout = BN, one column tile).
+template <int WM, int NT, int KSUB, bool SNAKE, bool RU = false>
 __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__ x, int64_t s_xb, int64_t s_xt,
                                                  const uint16_t *__restrict__ w, int64_t s_wp, int64_t s_wt,
                                                  int64_t s_wc, const uint16_t *__restrict__ bias,
@@ -79,8 +82,11 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
                                                  const float *__restrict__ sa, const float *__restrict__ sib, int M,
                                                  int TR, int Cin, int Cout, int CoutW, int taps, int dil, int PH,
                                                  float *__restrict__ part, int ksplit, uint32_t x_span,
-                                                 uint32_t w_span) {
-  warm_kernargs<180>();  // the explicit arguments above span 0x00-0xb3
+                                                 uint32_t w_span, const uint16_t *__restrict__ w2,
+                                                 const uint16_t *__restrict__ b2, const float *__restrict__ a2,
+                                                 const float *__restrict__ ib2, uint32_t w2_span) {
+  warm_kernargs<220>();  // the explicit arguments above span 0x00-0xdb
+  static_assert(!RU || (!SNAKE && NT % 2 == 0), "residual unit: input pre-activated, 32-channel k steps");
   constexpr int BN = 16 * NT, BM = 64 * WM, KS = 32 * KSUB, NCH = BN / 8;
   // two weight slices [k][n] (KS x BN): one is read while the next is written. A k row is BN + 16 elements
   // apart: the 16 rows one transposing read touches then fall on distinct bank groups (at a pitch of BN,
@@ -223,6 +229,69 @@ __global__ __launch_bounds__(256, 2) void k_conv_cl(const uint16_t *__restrict__
   // the DMA issued by the last step (its own slice again) still writes LDS: let it land before the
   // workgroup ends. s_waitcnt vmcnt(0).
   __builtin_amdgcn_s_waitcnt(0x0F70);
+  if constexpr (RU) {
+    // Residual unit, second conv (1x1, k = Cout = BN channels) on the first one's output, in registers.
+    // h = acc + bias, then the snake (fp32, one rounding to fp16), packed straight into the 1x1's B
+    // operands: slot 8g + j of 32-channel step u holds channel 32u + 16 (j / 4) + 4g + j % 4 -- where this
+    // lane's accumulators already are (acc[i][2u], acc[i][2u + 1]); the A operands read w2 in the same
+    // channel order (rows 4g.. and 16 + 4g.. of each 32-row block). No data moves between lanes.
+    constexpr int KU = NT / 2;
+    u32x4 hb[WM][KU];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int n = 16 * nt + 4 * g;
+      const u32x2 bv = ld8(bias + n);
+      const f32x4 av = *reinterpret_cast<const f32x4 *>(a2 + n), iv = *reinterpret_cast<const f32x4 *>(ib2 + n);
+      const float bb[4] = {h_lo(bv[0]), h_hi(bv[0]), h_lo(bv[1]), h_hi(bv[1])};
+#pragma unroll
+      for (int i = 0; i < WM; ++i) {
+        float hv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float h = acc[i][nt][e] + bb[e];
+          const float sv = sin_hw(h * av[e]);
+          hv[e] = h + iv[e] * sv * sv;
+        }
+        hb[i][nt >> 1][2 * (nt & 1)] = pack_f16x2(hv[0], hv[1]);
+        hb[i][nt >> 1][2 * (nt & 1) + 1] = pack_f16x2(hv[2], hv[3]);
+        acc[i][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+    // w2 [k][n] (row pitch s_wc, as w's) through the same two LDS slice areas, KS rows a slice; every wave
+    // is done with them once it passes the barrier (its last slice's reads are in its accumulators)
+    const rsrc_t w2r = make_rsrc(w2, w2_span);
+    auto issue_w2 = [&](int s2, uint16_t *dst) __attribute__((always_inline)) {
+      const int k0 = s2 * KS;
+      const uint32_t so = (uint32_t)((int64_t)k0 * s_wc * 2);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        bld16_lds<0>(w2r, dst + (4 * r + wv) * 512, k0 + wk[r] < Cin ? wb[r] : kOob, so);  // (p = 0, n0 = 0)
+    };
+    const int aoff2 = (4 * g + (r16 >> 2)) * BNP + 4 * (r16 & 3);
+    constexpr int S2 = BN / KS;  // the host launches RU only where KS divides BN
+    static_assert(BN % KS == 0, "1x1 slices");
+    __syncthreads();
+    issue_w2(0, wlA);
+#pragma unroll
+    for (int s2 = 0; s2 < S2; ++s2) {
+      uint16_t *cur = (s2 & 1) ? wlB : wlA, *nxt = (s2 & 1) ? wlA : wlB;
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's DMA of slice s2
+      __syncthreads();                     // every wave's; every wave is done with nxt
+      if (s2 + 1 < S2) issue_w2(s2 + 1, nxt);
+#pragma unroll
+      for (int u = 0; u < KSUB; ++u) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const uint16_t *ap = cur + aoff2 + 32 * u * BNP + 16 * nt;
+          const u32x2 lo = lds_tr16(ap), hi = lds_tr16(ap + 16 * BNP);
+          const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+          for (int i = 0; i < WM; ++i) acc[i][nt] = mfma16x16x32_f16(a, hb[i][s2 * KSUB + u], acc[i][nt]);
+        }
+      }
+    }
+    bias = b2;  // the epilogue below adds the second conv's bias and the unit's input
+  }
   // acc[i][nt]: lane (r16, g) holds Y[row m0 + (wv WM + i) 16 + r16][n = n0 + 16 nt + 4g + e], e = 0..3
   if (part) {  // split-K: raw fp32 sums to part[ks][p][m][n], row pitch gridDim.y BN; k_conv_fin finishes
     const int64_t NP = (int64_t)gridDim.y * BN;
@@ -385,6 +454,13 @@ static ConvPlan conv_plan(int64_t M, int Cin, int Cout, int taps, int ph, bool a
       break;
     }
   }
+  // shapes that would not fit two workgroups per CU: 96-channel slices of 12 / 16 column tiles (> 80 KB of
+  // LDS) take 32-channel slices; two row tiles of 16 column tiles (> 256 registers) take one
+  if (pl.KSUB == 3 && pl.NT >= 12) pl.KSUB = 1;
+  if (pl.WM == 2 && pl.NT == 16 && pl.KSUB >= 2) {
+    pl.WM = 1;
+    best_wgs = ((M + 63) / 64) * ((Cout + 255) / 256) * ph;
+  }
   pl.ntiles = (Cout + 16 * pl.NT - 1) / (16 * pl.NT);
   const int64_t wgs = best_wgs;
   if (allow_split && wgs < 512 && steps >= 16 && fin_fits) {
@@ -443,7 +519,8 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
   const dim3 grid((unsigned)((M + 64 * WM - 1) / (64 * WM)), (unsigned)pl.ntiles, (unsigned)(ph * pl.ksplit));
 #define A8_CONV_ARGS (const uint16_t *)x, s_xb, s_xt, (const uint16_t *)w, s_wp, s_wt, s_wc, (const uint16_t *)bias, \
                      (const uint16_t *)res, s_rb, s_rt, (uint16_t *)y, s_yb, s_yt, snake_a, snake_ib, (int)M, TR, Cin, \
-                     Cout, cout_w, taps, dil, ph, part, pl.ksplit, (uint32_t)x_span, (uint32_t)w_span
+                     Cout, cout_w, taps, dil, ph, part, pl.ksplit, (uint32_t)x_span, (uint32_t)w_span, nullptr,     \
+                     nullptr, nullptr, nullptr, 0u
 #define A8_CONV_L(wm, nt, ksub, sn) \
   hipLaunchKernelGGL((k_conv_cl<wm, nt, ksub, sn>), grid, dim3(256), 0, (hipStream_t)stream, A8_CONV_ARGS)
 #define A8_CONV_NT(wm, ksub, sn)                 \
@@ -454,13 +531,32 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
     case 12: A8_CONV_L(wm, 12, ksub, sn); break; \
     default: A8_CONV_L(wm, 16, ksub, sn); break; \
   }
-#define A8_CONV_K(wm, sn)         \
-  if (pl.KSUB == 2) {             \
-    A8_CONV_NT(wm, 2, sn)         \
-  } else if (pl.KSUB == 3) {      \
-    A8_CONV_NT(wm, 3, sn)         \
-  } else {                        \
-    A8_CONV_NT(wm, 1, sn)         \
+#define A8_CONV_NT_NARROW(wm, ksub, sn)        \
+  switch (NT) {                                \
+    case 4: A8_CONV_L(wm, 4, ksub, sn); break; \
+    case 6: A8_CONV_L(wm, 6, ksub, sn); break; \
+    default: A8_CONV_L(wm, 8, ksub, sn); break; \
+  }
+#define A8_CONV_NT_NO16(wm, ksub, sn)            \
+  switch (NT) {                                  \
+    case 4: A8_CONV_L(wm, 4, ksub, sn); break;   \
+    case 6: A8_CONV_L(wm, 6, ksub, sn); break;   \
+    case 8: A8_CONV_L(wm, 8, ksub, sn); break;   \
+    default: A8_CONV_L(wm, 12, ksub, sn); break; \
+  }
+  // (conv_plan keeps KSUB 3 to NT <= 8 and two row tiles with KSUB 2 to NT <= 12: those instances are the
+  // ones that fit two workgroups per CU)
+#define A8_CONV_K(wm, sn)              \
+  if (pl.KSUB == 2) {                  \
+    if (wm == 2) {                     \
+      A8_CONV_NT_NO16(2, 2, sn)        \
+    } else {                           \
+      A8_CONV_NT(1, 2, sn)             \
+    }                                  \
+  } else if (pl.KSUB == 3) {           \
+    A8_CONV_NT_NARROW(wm, 3, sn)       \
+  } else {                             \
+    A8_CONV_NT(wm, 1, sn)              \
   }
   if (WM == 2) {
     if (snake_a) {
@@ -478,6 +574,8 @@ extern "C" int a8_conv_cl(const void *x, int64_t s_xb, int64_t s_xt, const void 
 #undef A8_CONV_K
 #undef A8_CONV_L
 #undef A8_CONV_NT
+#undef A8_CONV_NT_NARROW
+#undef A8_CONV_NT_NO16
 #undef A8_CONV_ARGS
   if (part) {
     const hipError_t e = hipGetLastError();  // the finish would sum a workspace the main launch never wrote
@@ -496,6 +594,49 @@ extern "C" int64_t a8_conv_cl_ws_bytes(int B, int TR, int Cin, int Cout, int tap
   const int64_t M = (int64_t)B * TR;
   if (M > INT32_MAX / 2) return 0;
   return conv_plan(M, Cin, Cout, taps, ph).ws_bytes;
+}
+
+extern "C" int a8_ru_cl(const void *xin, int64_t s_xb, int64_t s_xt, const void *w1, int64_t s_wt, int64_t s_wc,
+                        const void *b1, const float *a2, const float *ib2, const void *w2, const void *b2,
+                        const void *res, int64_t s_rb, int64_t s_rt, void *y, int64_t s_yb, int64_t s_yt, int B,
+                        int Tin, int TR, int C, int taps, int dil, void *stream) {
+  using namespace a8;
+  if (B < 0 || TR < 0 || C <= 0 || taps <= 0 || dil <= 0)
+    return set_error(A8_EINVAL, "ru_cl: bad sizes B=%d TR=%d C=%d taps=%d dil=%d", B, TR, C, taps, dil);
+  if ((int64_t)TR + (int64_t)(taps - 1) * dil > Tin)
+    return set_error(A8_EINVAL, "ru_cl: %d input rows, %d needed", Tin, TR + (taps - 1) * dil);
+  if (C != 96 && C != 192) return set_error(A8_EUNSUP, "ru_cl: %d channels (96 or 192: one tile holds the row)", C);
+  if (B == 0 || TR == 0) return 0;
+  if (!xin || !w1 || !b1 || !a2 || !ib2 || !w2 || !b2 || !res || !y) return set_error(A8_EINVAL, "ru_cl: null pointer");
+  if (!al16(xin) || !al16(w1) || !al16(w2) || !al16(a2) || !al16(ib2) || (reinterpret_cast<uintptr_t>(b1) & 7u) ||
+      (s_xb | s_xt | s_wt) & 7 || s_wc != C || (reinterpret_cast<uintptr_t>(y) & 1u) ||
+      (reinterpret_cast<uintptr_t>(res) & 1u))
+    return set_error(A8_EALIGN, "ru_cl: xin / w1 / w2 / a2 / ib2 16-byte aligned, b1 8, strides multiples of 8, "
+                     "weight rows of C = %d", C);
+  const int64_t M = (int64_t)B * TR;
+  if (M > INT32_MAX / 2) return set_error(A8_EUNSUP, "ru_cl: %lld rows too many", (long long)M);
+  const int64_t x_span = ((int64_t)(B - 1) * s_xb + (int64_t)(Tin - 1) * s_xt + C) * 2;
+  const int64_t w_span = ((int64_t)(taps - 1) * s_wt + (int64_t)(C - 1) * s_wc + C) * 2;
+  const int64_t w2_span = ((int64_t)(C - 1) * s_wc + C) * 2;
+  if (x_span >= ((int64_t)1 << 31) || w_span >= ((int64_t)1 << 31) || s_xb < 0 || s_xt < 0 || s_wt < 0)
+    return set_error(A8_EUNSUP, "ru_cl: xin spans %lld bytes, w1 %lld (each must be below 2 GiB)", (long long)x_span,
+                     (long long)w_span);
+  // the whole row in one tile (NT = C / 16); two row tiles per wave where that still gives >= 512 workgroups
+  const int WM = (M + 127) / 128 >= 512 ? 2 : 1;
+  const dim3 grid((unsigned)((M + 64 * WM - 1) / (64 * WM)), 1u, 1u);
+#define A8_RU_L(wm, nt, ksub)                                                                                        \
+  hipLaunchKernelGGL((k_conv_cl<wm, nt, ksub, false, true>), grid, dim3(256), 0, (hipStream_t)stream,                \
+                     (const uint16_t *)xin, s_xb, s_xt, (const uint16_t *)w1, (int64_t)0, s_wt, s_wc,                \
+                     (const uint16_t *)b1, (const uint16_t *)res, s_rb, s_rt, (uint16_t *)y, s_yb, s_yt, nullptr,     \
+                     nullptr, (int)M, TR, C, C, C, taps, dil, 1, nullptr, 1, (uint32_t)x_span, (uint32_t)w_span,     \
+                     (const uint16_t *)w2, (const uint16_t *)b2, a2, ib2, (uint32_t)w2_span)
+  if (C == 192) {
+    if (WM == 2) A8_RU_L(2, 12, 2); else A8_RU_L(1, 12, 2);
+  } else {
+    if (WM == 2) A8_RU_L(2, 6, 3); else A8_RU_L(1, 6, 3);
+  }
+#undef A8_RU_L
+  return (int)hipGetLastError();
 }
 
 extern "C" int a8_snake_cat(const void *x, int64_t s_xb, int64_t s_xt, const void *state, int64_t s_sb, int64_t s_st,

@@ -654,6 +654,34 @@ def conv_cl(xin, w, bias, TR, taps, dil, ph, out, res=None, f16acc=True, cfg=Non
     return out
 
 
+def ru_cl(xin, w1, b1, a2, ib2, w2, b2, res, out, TR, taps, dil):
+    """One whole residual unit in one launch (the reference's ru_fused, fast_kernels.py:626-692):
+        out[b, t] = res[b, t] + b2 + snake2(bias1 + sum_j xin[b, t + j*dil] @ w1[j]) @ w2
+    with xin [B, Tin, C] the activated input ([state | snake1(x)], snake_cat's output), w1 [taps, C, C] and w2
+    [C, C] fp16 ([k][n], CLConv's packing without the phase dim), b1 / b2 fp16 [C], a2 / ib2 the second snake's
+    fp32 [C] vectors, res the unit's raw input [B, >=TR, C]. The first conv's output h stays in registers in
+    fp32 (h + b1, the snake, one rounding to fp16), as in ru_fused; accumulation is fp32 throughout. C is 96 or
+    192 (one workgroup tile holds a row's channels)."""
+    for name, t, d in (("xin", xin, 3), ("w1", w1, 3), ("w2", w2, 2), ("res", res, 3), ("out", out, 3)):
+        _need(isinstance(t, torch.Tensor) and t.dtype == _F16, f"{name} must be a float16 tensor", TypeError)
+        _need(t.dim() == d and t.stride(-1) == 1, f"{name} must have {d} dims with a contiguous last dim")
+    B, Tin, C = xin.shape
+    _need(w1.shape == (taps, C, C) and w1.stride(1) == C, f"w1 {tuple(w1.shape)} must be [{taps}, {C}, {C}], rows of {C}")
+    _need(w2.shape == (C, C) and w2.stride(0) == C, f"w2 {tuple(w2.shape)} must be [{C}, {C}], contiguous")
+    _need(res.shape[0] == B and res.shape[1] >= TR and res.shape[2] == C, f"res {tuple(res.shape)} must be [{B}, >={TR}, {C}]")
+    _need(out.shape[0] == B and out.shape[1] >= TR and out.shape[2] == C, f"out {tuple(out.shape)} must be [{B}, >={TR}, {C}]")
+    for name, v, dt in (("b1", b1, _F16), ("b2", b2, _F16), ("a2", a2, torch.float32), ("ib2", ib2, torch.float32)):
+        _need(isinstance(v, torch.Tensor) and v.dtype == dt and v.is_contiguous() and v.numel() >= C,
+              f"{name} must be a contiguous {dt} vector of >= {C} entries")
+    _check_device(xin=xin, w1=w1, w2=w2, res=res, out=out, b1=b1, b2=b2, a2=a2, ib2=ib2)
+    st = _lib.load().a8_ru_cl(
+        xin.data_ptr(), xin.stride(0), xin.stride(1), w1.data_ptr(), w1.stride(0), w1.stride(1), b1.data_ptr(),
+        a2.data_ptr(), ib2.data_ptr(), w2.data_ptr(), b2.data_ptr(), res.data_ptr(), res.stride(0), res.stride(1),
+        out.data_ptr(), out.stride(0), out.stride(1), B, Tin, TR, C, taps, dil, _lib.stream_of(xin))
+    _lib.check(st, "ru_cl")
+    return out
+
+
 def conv_cl_ws_bytes(B, TR, Cin, Cout, taps, ph):
     """Bytes of the split-K workspace conv_cl uses for this shape (0: K is not split)."""
     return int(_lib.load().a8_conv_cl_ws_bytes(B, TR, Cin, Cout, taps, ph))

@@ -12,8 +12,10 @@ builds [state, snake(x)] and conv_cl reads it, and the state keeps the last ctx 
 
 CLDecoder (fast_engine.py:276-310): conv_in, then per block [snake + transposed conv, 3 residual units
 (snake, dilated conv k, snake, 1x1 conv, + input)], snake + conv_out (one channel), tanh. The reference's
-opt-in fused residual unit (_FusedRU, off unless TTS_VOC_FUSED_RU names a width) computes the same unit; here a
-residual unit is always the two convs, the reference's default.
+fused residual unit (_FusedRU, on for the widths TTS_VOC_FUSED_RU names) is FusedRU here, on ru_cl, and
+`fused_ru` names its widths (default 96 and 192, the two ru_cl takes; () keeps every unit as the two convs,
+the reference's default). The fused unit keeps the first conv's output in fp32 where the two convs round it
+to fp16, as the reference's does.
 
 The checkpoint's decoder (its modeling file and weights) is absent offline: `decoder_weights` draws a synthetic
 decoder of a stated shape (default: a DAC-style 44.1 kHz decoder, 1024 -> 1536 channels, strides 8, 8, 4, 2,
@@ -22,7 +24,7 @@ from __future__ import annotations
 
 import torch
 
-from .fast_kernels import conv_cl, conv_cl_ws_bytes, snake_cat
+from .fast_kernels import conv_cl, conv_cl_ws_bytes, ru_cl, snake_cat
 
 F16 = torch.float16
 
@@ -93,6 +95,34 @@ class CLConv:
         return y
 
 
+class FusedRU:
+    """A residual unit (snake, causal conv k dil, snake, conv 1x1, + input) as one launch after the state concat
+    (the reference's _FusedRU, fast_engine.py:235-273, on ru_cl): the k-tap conv's output stays in registers
+    (fp32, the second snake applied there, one rounding to fp16) and feeds the 1x1 conv in the same workgroup.
+    Uses c1's state (activated context) and refreshes it after, as the two-conv path does (any chunk length).
+    Widths 96 and 192 (RU_WIDTHS): one workgroup tile holds a row's channels."""
+
+    RU_WIDTHS = (96, 192)
+
+    def __init__(self, c1, c2):
+        assert c1.Cin == c1.Cout == c2.Cin == c2.Cout and c2.taps == 1 and c1.ph == c2.ph == 1
+        assert c1.state is not None and c1.a is not None and c2.a is not None
+        assert c1.Cin in self.RU_WIDTHS and c1.bias is not None and c2.bias is not None
+        self.c1, self.c2 = c1, c2
+        self.w1 = c1.W[0]            # [taps, C, C]
+        self.w2 = c2.W[0, 0]         # [C, C]
+
+    def __call__(self, x, b):
+        c1, c2 = self.c1, self.c2
+        T = x.shape[1]
+        xin = torch.empty(b, c1.ctx + T, c1.Cin, dtype=F16, device=x.device)
+        snake_cat(x, c1.state[:b], c1.a, c1.ib, xin)
+        y = torch.empty(b, T, c1.Cout, dtype=F16, device=x.device)
+        ru_cl(xin, self.w1, c1.bias, c2.a, c2.ib, self.w2, c2.bias, x, y, T, c1.taps, c1.dil)
+        c1.state[:b].copy_(xin[:, T:])
+        return y
+
+
 def decoder_weights(cin=1024, ch=1536, rates=(8, 8, 4, 2), k=7, dils=(1, 3, 9), dev="cpu", seed=0):
     """A synthetic decoder in the modules' own layouts: conv_in (w [ch, cin, k], b), blocks of (alpha, transposed
     w [C, C/2, 2s], b, stride, units of (alpha1, w1 [C/2, C/2, k], b1, dil, alpha2, w2 [C/2, C/2, 1], b2)),
@@ -128,8 +158,9 @@ class CLDecoder:
     weights; every conv's state is registered in `states` (per row, for snapshots / row resets). frame: the
     input rows a call takes (sizes each conv's split-K workspace once; the streaming decoder's frame is 4)."""
 
-    def __init__(self, wts, Bmax, dev, states=None, frame=4):
+    def __init__(self, wts, Bmax, dev, states=None, frame=4, fused_ru=FusedRU.RU_WIDTHS):
         self.states = states if states is not None else []
+        fuse = set(int(c) for c in (fused_ru or ()))
         S = self.states
         w, b = wts["conv_in"]
         t = int(frame)
@@ -138,8 +169,13 @@ class CLDecoder:
         for a0, tw, tb, s, units in wts["blocks"]:
             tc = CLConv(tw, tb, Bmax, dev, S, alpha=a0, trans=True, stride=s, tmax=t)
             t *= s
-            us = [(CLConv(w1, b1, Bmax, dev, S, alpha=a1, dilation=d, tmax=t),
-                   CLConv(w2, b2, Bmax, dev, S, alpha=a2, tmax=t)) for a1, w1, b1, d, a2, w2, b2 in units]
+            us = []
+            for a1, w1, b1, d, a2, w2, b2 in units:
+                c1 = CLConv(w1, b1, Bmax, dev, S, alpha=a1, dilation=d, tmax=t)
+                c2 = CLConv(w2, b2, Bmax, dev, S, alpha=a2, tmax=t)
+                fu = FusedRU(c1, c2) if (c1.Cin in fuse and c1.Cin in FusedRU.RU_WIDTHS and
+                                         torch.device(dev).type == "cuda") else None
+                us.append((c1, c2, fu))
             self.blocks.append((tc, us))
         af, wf, bf = wts["final"]
         self.final = CLConv(wf, bf, Bmax, dev, S, alpha=af, tmax=t)
@@ -157,6 +193,6 @@ class CLDecoder:
         x = self.dec_in(x.to(F16).contiguous(), b)
         for tc, units in self.blocks:
             x = tc(x, b)
-            for c1, c2 in units:
-                x = c2(c1(x, b), b, res=x)
+            for c1, c2, fu in units:
+                x = fu(x, b) if fu is not None else c2(c1(x, b), b, res=x)
         return self.final(x, b)[..., 0].float().tanh()

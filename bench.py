@@ -328,19 +328,38 @@ def per_config(a8, torch, dev, steps):
         flops += len(units) * 2 * b * t * C * C * 8
     flops += 2 * b * t * 1 * 7 * C
     del g
-    # the dominant launch: a residual unit's k=7 conv at the 192-channel block (1024 output rows per row)
-    c1 = dec.blocks[2][1][0][0]
+    # the same frame with every residual unit as its two convs (fused_ru=(): the reference's default path)
+    dec2 = voc.CLDecoder(wts, b, dev, fused_ru=())
+    g = capture(torch, lambda: dec2(xf, b))
+    us_two = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
+    del g
+    # the dominant launches: a residual unit at the 192-channel block (1024 output rows per row), as its k=7
+    # conv alone (two-conv path) and as the whole fused unit
+    c1, c2, fu = dec.blocks[2][1][0]
     xr = torch.randn(b, 1024, 192, generator=gen, device=dev).to(torch.float16)
     g = capture(torch, lambda: c1(xr, b))
     us_c = time_median(torch, g, steps, 10) * 1e3
+    del g
+    g = capture(torch, lambda: c2(c1(xr, b), b, res=xr))
+    us_u2 = time_median(torch, g, steps, 10) * 1e3
+    del g
+    g = capture(torch, lambda: fu(xr, b))
+    us_ru = time_median(torch, g, steps, 10) * 1e3
     fl_c = 2 * b * 1024 * 192 * 7 * 192
+    fl_u = fl_c + 2 * b * 1024 * 192 * 192
     res["vocoder_frame"] = {"us_per_frame": round(us, 1), "TFLOP/s": round(flops / us / 1e6, 1),
                             "frac_fp16_mfma": round(flops / us / 1e6 / 2500.0, 4), "rows": b, "flops": flops,
+                            "us_per_frame_two_conv_units": round(us_two, 1),
                             "conv_k7_c192": {"us": round(us_c, 1), "TFLOP/s": round(fl_c / us_c / 1e6, 1),
                                              "note": "snake_cat + conv_cl + state copy, M = 196608, N = 192, "
                                                      "K = 1344"},
-                            "note": "one frame of the streaming decoder; synthetic DAC-style weights"}
-    del g, dec, wts, xf, xr
+                            "unit_c192": {"fused_us": round(us_ru, 1), "two_conv_us": round(us_u2, 1),
+                                          "fused_TFLOP/s": round(fl_u / us_ru / 1e6, 1),
+                                          "note": "one residual unit, 192 rows x 1024 positions x 192 channels: "
+                                                  "snake_cat + ru_cl + state copy vs the k=7 and 1x1 convs"},
+                            "note": "one frame of the streaming decoder; synthetic DAC-style weights; residual "
+                                    "units of 96 / 192 channels fused (ru_cl), the others two convs"}
+    del g, dec, dec2, wts, xf, xr
     torch.cuda.empty_cache()
 
     # C4: 64 requests, n ~ U[40, 400], after a 300-position voice prefix; store + packed prefill per layer

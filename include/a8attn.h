@@ -357,6 +357,21 @@ int a8_snake_cat(const void *x, int64_t s_xb, int64_t s_xt, const void *state, i
                  const float *a, const float *ib, void *y, int64_t s_yb, int64_t s_yt, int B, int T, int CTX, int C,
                  void *stream);
 
+/*
+ * a8_ru_cl replaces serve/fast_kernels.py:679-692 (ru_fused, kernel 626-676; used by _FusedRU,
+ * serve/fast_engine.py:235-273): one whole residual unit in one launch, for rows (b, t), t < TR:
+ *   h = b1 + sum_{j < taps} xin[b, t + j*dil] w1[j]            (fp32, never stored)
+ *   y[b, t, n] = res[b, t, n] + b2[n] + sum_k fp16(h + ib2 sin(a2 h)^2)[k] w2[k, n]
+ * xin [B, Tin, C] the activated input ([state | snake1(x)]: a8_snake_cat's output, Tin >= TR + (taps-1) dil),
+ * w1 [taps, C, C] (tap stride s_wt, row stride s_wc = C) and w2 [C, C] fp16 [k][n] rows, b1 / b2 fp16 [C]
+ * (b1 8-byte aligned), a2 / ib2 fp32 [C] (16-byte aligned), res the unit's raw input. fp32 accumulation.
+ * C must be 96 or 192 (one workgroup holds a row's channels): else A8_EUNSUP.
+ */
+int a8_ru_cl(const void *xin, int64_t s_xb, int64_t s_xt, const void *w1, int64_t s_wt, int64_t s_wc, const void *b1,
+             const float *a2, const float *ib2, const void *w2, const void *b2, const void *res, int64_t s_rb,
+             int64_t s_rt, void *y, int64_t s_yb, int64_t s_yt, int B, int Tin, int TR, int C, int taps, int dil,
+             void *stream);
+
 #ifdef __cplusplus
 }
 #endif

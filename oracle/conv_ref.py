@@ -9,13 +9,16 @@ Restates, in torch on the CPU (fp16 storage, fp32 math):
     conv_cl    serve/fast_kernels.py:551-623 (_conv_cl_kernel, conv_cl): out[b, t*ph + p] = bias
                + sum_j x[b, t + j*dil] @ w[p, j] (+ res[b, t*ph + p]), fp32 accumulation, one fp16 rounding
     snake_cat  serve/fast_kernels.py:695-729 (_snake_cat_kernel, snake_cat): concat(state, snake(x)) in time
+    ru_fused   serve/fast_kernels.py:626-692 (_ru_fused_kernel, ru_fused): a whole residual unit, h kept fp32
     decoder    serve/fast_engine.py:276-310 (_CLDecoder) over a whole utterance from silence, written directly
                on torch's conv1d / conv_transpose1d of the modules' own weights (channels first, float64,
                rounded to fp16 where the channels-last path stores: the snake's output and each conv's output)
 
 Pinned by tests/test_oracle.py against torch.nn.functional.conv1d (causal / dilated, ph = 1) and
 conv_transpose1d (the phase split of a stride-s transposed conv, as fast_engine.py:186-194 builds it), in
-float64, and by a brute-force loop on tiny sizes.
+float64, and by a brute-force loop on tiny sizes; ru_fused against the two-conv unit (snake_cat, conv_cl,
+conv_cl with the residual) bit for bit where the second snake is the identity (ib2 = 0: h rounds to fp16
+either way), and against a float64 loop with the snake.
 """
 from __future__ import annotations
 
@@ -52,6 +55,27 @@ def snake_cat(x, state, a, ib):
     """concat(state (CTX activated rows), snake(x) (T rows)) along time (fast_kernels.py:695-715)."""
     y = snake(x, a, ib) if a is not None else x
     return torch.cat([state, y], 1) if state is not None else y
+
+
+def ru_fused(x, state, a1, ib1, w1, b1, a2, ib2, w2, b2, taps, dil):
+    """One whole residual unit (fast_kernels.py:626-692, _ru_fused_kernel / ru_fused; _FusedRU, fast_engine.py
+    :235-273): out = x + b2 + snake2(b1 + conv_k(snake1([state | x]), dil)) @ w2, channels last.
+    x [B, T, C] raw fp16, state [B, CTX, C] activated (CTX = (taps - 1) dil), w1 [taps, C, C] and w2 [C, C] fp16
+    [k][n], b1 / b2 fp16 [C], a1 / ib1 / a2 / ib2 fp32 [C]. The first conv's output h = acc + b1 stays fp32; the
+    second snake runs on it in fp32 and rounds once to fp16 (fast_kernels.py:659-663); sums in fp32 (the
+    reference's F16ACC fp16 partial sums are the less exact variant and are not modelled)."""
+    xin = snake_cat(x, state, a1, ib1).float()
+    B, T, C = x.shape
+    h = torch.zeros(B, T, C, dtype=torch.float32)
+    for j in range(taps):
+        h += xin[:, j * dil:j * dil + T, :] @ w1[j].float()
+    h += b1[:C].float()
+    s = torch.sin(h * a2[:C].float())
+    hf = (h + ib2[:C].float() * s * s).to(F16).float()
+    out = hf @ w2.float()
+    out += b2[:C].float()
+    out += x.float()
+    return out.to(F16)
 
 
 def _f16(t):

@@ -146,3 +146,41 @@ def test_conv_cl_split_k_equals_one_pass(a8, dev):
     assert torch.equal(outs[0], outs[1])
     d = (outs[0].float() - outs[2].float()).abs()
     assert (d <= outs[2].float().abs() * 2 ** -10 + 1e-3).all()
+
+
+@pytest.mark.parametrize("B,T,C,dil", [(8, 64, 96, 9), (8, 64, 192, 3), (64, 1024, 192, 1), (65, 1009, 96, 3),
+                                       (3, 5, 96, 9), (2, 130, 192, 9)])
+def test_ru_cl_against_oracle(a8, cref, dev, B, T, C, dil):
+    """A whole residual unit in one launch (ru_cl) against the oracle's ru_fused: snake_cat of the state and
+    the raw input, then the fused k=7 conv, second snake, 1x1 conv, bias and residual; long inputs (block 2 /
+    3 row counts), a ragged last tile, T shorter than the context, every dilation of the decoder."""
+    say(f"case: ru_cl B={B} T={T} C={C} dil={dil}")
+    g = torch.Generator().manual_seed(B * 7 + C + dil)
+    taps = 7
+    ctx = (taps - 1) * dil
+    x = torch.randn(B, T, C, generator=g).half()
+    st = torch.randn(B, ctx, C, generator=g).half()
+    a1, a2 = torch.rand(C, generator=g) + 0.5, torch.rand(C, generator=g) + 0.5
+    ib1, ib2 = 1.0 / (a1 + 1e-9), 1.0 / (a2 + 1e-9)
+    w1 = (torch.randn(taps, C, C, generator=g) / (taps * C) ** 0.5).half()
+    w2 = (torch.randn(C, C, generator=g) / C ** 0.5).half()
+    b1, b2 = (0.1 * torch.randn(C, generator=g)).half(), (0.1 * torch.randn(C, generator=g)).half()
+    want = cref.ru_fused(x, st, a1, ib1, w1, b1, a2, ib2, w2, b2, taps, dil)
+    xd = x.to(dev)
+    xin = torch.empty(B, ctx + T, C, dtype=F16, device=dev)
+    a8.snake_cat(xd, st.to(dev), a1.to(dev), ib1.to(dev), xin)
+    out = torch.full((B, T, C), 9.0, dtype=F16, device=dev)
+    a8.ru_cl(xin, w1.to(dev), b1.to(dev), a2.to(dev), ib2.to(dev), w2.to(dev), b2.to(dev), xd, out, T, taps, dil)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.cpu().float()).all()
+    assert _close(out, want)
+
+
+def test_ru_cl_refuses_other_widths(a8, dev):
+    """Widths whose row does not fit one tile are refused (the caller takes the two convs)."""
+    C = 384
+    xin = torch.zeros(1, 10, C, dtype=F16, device=dev)
+    w1, w2 = torch.zeros(7, C, C, dtype=F16, device=dev), torch.zeros(C, C, dtype=F16, device=dev)
+    v16, v32 = torch.zeros(C, dtype=F16, device=dev), torch.zeros(C, device=dev)
+    with pytest.raises(RuntimeError, match="ru_cl"):
+        a8.ru_cl(xin, w1, v16, v32, v32, w2, v16, xin, torch.empty(1, 4, C, dtype=F16, device=dev), 4, 7, 1)

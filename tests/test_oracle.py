@@ -504,6 +504,57 @@ def test_snake_cat_layout(cref):
     assert torch.equal(cref.snake_cat(x, None, None, None), x)
 
 
+@pytest.mark.parametrize("C,taps,dil,T", [(16, 7, 3, 20), (32, 3, 1, 5), (96, 7, 9, 40)])
+def test_ru_fused_is_the_two_conv_unit_when_the_second_snake_is_identity(cref, C, taps, dil, T):
+    """ib2 = 0: snake2 is the identity, so the fused unit's fp32 h rounds to fp16 exactly where conv_cl's
+    output would: ru_fused must equal snake_cat -> conv_cl (k taps, b1) -> conv_cl (1x1, b2, + x) bit for bit."""
+    g = torch.Generator().manual_seed(C + taps)
+    B, ctx = 3, (taps - 1) * dil
+    x = torch.randn(B, T, C, generator=g).half()
+    st = torch.randn(B, ctx, C, generator=g).half()
+    a1, a2 = torch.rand(C, generator=g) + 0.5, torch.rand(C, generator=g) + 0.5
+    ib1 = 1.0 / (a1 + 1e-9)
+    w1 = (torch.randn(taps, C, C, generator=g) / (taps * C) ** 0.5).half()
+    w2 = (torch.randn(C, C, generator=g) / C ** 0.5).half()
+    b1, b2 = torch.randn(C, generator=g).half(), torch.randn(C, generator=g).half()
+    got = cref.ru_fused(x, st, a1, ib1, w1, b1, a2, torch.zeros(C), w2, b2, taps, dil)
+    xin = cref.snake_cat(x, st, a1, ib1)
+    h = cref.conv_cl(xin, w1.unsqueeze(0), b1, T, taps, dil, 1, C)
+    want = cref.conv_cl(h, w2.view(1, 1, C, C), b2, T, 1, 1, 1, C, res=x)
+    assert torch.equal(got, want)
+
+
+def test_ru_fused_against_float64_loop(cref):
+    """With the second snake: a float64 loop over rows, taps and channels (the state rows for t + j dil < ctx,
+    the activated input after), the snake on fp32-exact h, one fp16 rounding of h', then the 1x1, b2 and x.
+    Within one fp16 ulp (fp32 vs float64 sums may flip a rounding of h')."""
+    g = torch.Generator().manual_seed(7)
+    B, T, C, taps, dil = 2, 6, 16, 3, 2
+    ctx = (taps - 1) * dil
+    x = torch.randn(B, T, C, generator=g).half()
+    st = torch.randn(B, ctx, C, generator=g).half()
+    a1, a2 = torch.rand(C, generator=g) + 0.5, torch.rand(C, generator=g) + 0.5
+    ib1, ib2 = 1.0 / (a1 + 1e-9), 1.0 / (a2 + 1e-9)
+    w1 = (torch.randn(taps, C, C, generator=g) / (taps * C) ** 0.5).half()
+    w2 = (torch.randn(C, C, generator=g) / C ** 0.5).half()
+    b1, b2 = torch.randn(C, generator=g).half(), torch.randn(C, generator=g).half()
+    got = cref.ru_fused(x, st, a1, ib1, w1, b1, a2, ib2, w2, b2, taps, dil).double()
+    xd = x.double()
+    sx = (xd + ib1.double() * torch.sin(a1.double() * xd) ** 2).half().double()   # snake1, one fp16 rounding
+    want = torch.empty(B, T, C, dtype=torch.float64)
+    for b in range(B):
+        for t in range(T):
+            h = b1.double().clone()
+            for j in range(taps):
+                r = t + j * dil - ctx
+                row = st[b, ctx + r].double() if r < 0 else sx[b, r]
+                h += row @ w1[j].double()
+            hs = (h + ib2.double() * torch.sin(a2.double() * h) ** 2).half().double()
+            want[b, t] = hs @ w2.double() + b2.double() + xd[b, t]
+    err = (got - want).abs()
+    assert (err <= want.abs() * 2 ** -9 + 2e-3).all(), err.max().item()
+
+
 def test_vocoder_pack_conv_against_torch_conv():
     """The product's weight packing (vocoder.pack_conv, fast_engine.py:186-206) under the oracle's conv_cl
     equals torch's conv1d / conv_transpose1d of the module weights (conv_ref._conv_fc: causal zero context,
