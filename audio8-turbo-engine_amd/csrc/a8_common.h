@@ -38,6 +38,14 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
+// The gated MLP activation on two bf16 pairs (serve/fast_kernels.py:526-545, _silu_mul_kernel): the gate's
+// SiLU rounded to bf16 first (act(gate) in bf16, as the model's MLP), then times up, rounded again. Shared by
+// k_silu_mul and the w13 GEMM's gated epilogue, so the fused and separate paths give the same bits.
+__device__ __forceinline__ uint32_t silu_mul_bf16x2(uint32_t g2, uint32_t u2) {
+  const float g0 = bf_lo(g2), g1 = bf_hi(g2);
+  const uint32_t gs = pack_bf16x2(g0 / (1.f + expf(-g0)), g1 / (1.f + expf(-g1)));
+  return pack_bf16x2(bf_lo(gs) * bf_lo(u2), bf_hi(gs) * bf_hi(u2));
+}
 
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
 __device__ __forceinline__ void st16(void *p, u32x4 v) { *reinterpret_cast<u32x4 *>(p) = v; }

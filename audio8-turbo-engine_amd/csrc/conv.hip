@@ -605,7 +605,8 @@ extern "C" int a8_ru_cl(const void *xin, int64_t s_xb, int64_t s_xt, const void 
     return set_error(A8_EINVAL, "ru_cl: bad sizes B=%d TR=%d C=%d taps=%d dil=%d", B, TR, C, taps, dil);
   if ((int64_t)TR + (int64_t)(taps - 1) * dil > Tin)
     return set_error(A8_EINVAL, "ru_cl: %d input rows, %d needed", Tin, TR + (taps - 1) * dil);
-  if (C != 96 && C != 192) return set_error(A8_EUNSUP, "ru_cl: %d channels (96 or 192: one tile holds the row)", C);
+  if (C != 96 && C != 192 && C != 384)
+    return set_error(A8_EUNSUP, "ru_cl: %d channels (96, 192 or 384: one tile holds the row)", C);
   if (B == 0 || TR == 0) return 0;
   if (!xin || !w1 || !b1 || !a2 || !ib2 || !w2 || !b2 || !res || !y) return set_error(A8_EINVAL, "ru_cl: null pointer");
   if (!al16(xin) || !al16(w1) || !al16(w2) || !al16(a2) || !al16(ib2) || (reinterpret_cast<uintptr_t>(b1) & 7u) ||
@@ -622,7 +623,8 @@ extern "C" int a8_ru_cl(const void *xin, int64_t s_xb, int64_t s_xt, const void 
     return set_error(A8_EUNSUP, "ru_cl: xin spans %lld bytes, w1 %lld (each must be below 2 GiB)", (long long)x_span,
                      (long long)w_span);
   // the whole row in one tile (NT = C / 16); two row tiles per wave where that still gives >= 512 workgroups
-  const int WM = (M + 127) / 128 >= 512 ? 2 : 1;
+  // (384 channels: one row tile and 32-channel slices, to stay within two workgroups per CU)
+  const int WM = C <= 192 && (M + 127) / 128 >= 512 ? 2 : 1;
   const dim3 grid((unsigned)((M + 64 * WM - 1) / (64 * WM)), 1u, 1u);
 #define A8_RU_L(wm, nt, ksub)                                                                                        \
   hipLaunchKernelGGL((k_conv_cl<wm, nt, ksub, false, true>), grid, dim3(256), 0, (hipStream_t)stream,                \
@@ -630,7 +632,9 @@ extern "C" int a8_ru_cl(const void *xin, int64_t s_xb, int64_t s_xt, const void 
                      (const uint16_t *)b1, (const uint16_t *)res, s_rb, s_rt, (uint16_t *)y, s_yb, s_yt, nullptr,     \
                      nullptr, (int)M, TR, C, C, C, taps, dil, 1, nullptr, 1, (uint32_t)x_span, (uint32_t)w_span,     \
                      (const uint16_t *)w2, (const uint16_t *)b2, a2, ib2, (uint32_t)w2_span)
-  if (C == 192) {
+  if (C == 384) {
+    A8_RU_L(1, 24, 1);
+  } else if (C == 192) {
     if (WM == 2) A8_RU_L(2, 12, 2); else A8_RU_L(1, 12, 2);
   } else {
     if (WM == 2) A8_RU_L(2, 6, 3); else A8_RU_L(1, 6, 3);

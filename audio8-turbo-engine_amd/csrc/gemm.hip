@@ -52,7 +52,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
                                                            const uint16_t *__restrict__ w, int64_t ldw,
                                                            uint16_t *__restrict__ out, int64_t ldo,
                                                            float *__restrict__ part, int32_t *__restrict__ cnt,
-                                                           int Mall, int N, int K, int cps, int S) {
+                                                           int Mall, int N, int K, int cps, int S, int I) {
   static_assert(NW == 4 || NW == 8, "waves");
   static_assert(MT >= 2 && MT * 16 <= kGmMaxM && (2 * MT) % NW == 0, "token subtiles");
   constexpr int XB = MT * 16 * 128;        // X bytes per ring slot (token rows x 128 bytes)
@@ -76,13 +76,20 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
   // sources: rows past M / N read as zeros (their offsets lie past the range: ld >= K); a chunk past the
   // workgroup's range is requested from an empty range (zeros into a free slot, no memory traffic), so every
   // wave issues the same requests every chunk and the waits below are constant
+  // gated (I > 0: w = [gate; up], I rows each, out = silu(x gate^T) * (x up^T), I columns): the tile's weight
+  // rows 0..31 are gate rows 32 nt.., rows 32..63 the up rows I + 32 nt.. -- 32 output columns a workgroup
+  const bool gated = I > 0;
+  const int wrow0 = gated ? 32 * nt : n0, wlim = gated ? I : N;
+  const uint32_t wbytes = (uint32_t)((int64_t)(wlim - wrow0 - 1) * ldw * 2 + (int64_t)K * 2);
   const u32x4 xr = gm_rsrc(x, (uint32_t)((int64_t)(M - 1) * ldx * 2 + (int64_t)K * 2));
-  const u32x4 wr = gm_rsrc(w + (int64_t)n0 * ldw, (uint32_t)((int64_t)(N - n0 - 1) * ldw * 2 + (int64_t)K * 2));
+  const u32x4 wr = gm_rsrc(w + (int64_t)wrow0 * ldw, wbytes);
+  const u32x4 wu = gated ? gm_rsrc(w + (int64_t)(I + wrow0) * ldw, wbytes) : wr;
   u32x4 xr0 = xr, wr0 = wr;
   xr0[2] = 0u;
   wr0[2] = 0u;
   const uint32_t prow = (uint32_t)(lane >> 3), pch = (uint32_t)(lane & 7);
   uint32_t xso[DX], xdo[DX], wso[DW], wdo[DW];
+  u32x4 wres[DW];
 #pragma unroll
   for (int j = 0; j < DX; ++j) {  // X instruction i = wv + NW j: token rows 8i..8i+7
     const uint32_t i = (uint32_t)(wv + NW * j), row = 8u * i + prow;
@@ -92,7 +99,10 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
 #pragma unroll
   for (int j = 0; j < DW; ++j) {  // W instruction i = wv + NW j: weight rows 8i..8i+7 of the tile
     const uint32_t i = (uint32_t)(wv + NW * j), row = 8u * i + prow;
-    wso[j] = row * (uint32_t)(ldw * 2) + ((pch ^ (row & 7u)) << 4);
+    const bool up = gated && i >= 4u;  // (wave-uniform) the up half of a gated tile, from its own source
+    wres[j] = up ? wu : wr;
+    const uint32_t srow = up ? row - 32u : row;
+    wso[j] = srow * (uint32_t)(ldw * 2) + ((pch ^ (row & 7u)) << 4);
     wdo[j] = i * 1024u;
   }
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(lds);
@@ -104,11 +114,10 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
     for (int j = 0; j < DX; ++j) gm_dma(rs, lds0 + (uint32_t)(slot * XB) + xdo[j], xso[j] + kb);
   };
   auto issue_w = [&](int c) __attribute__((always_inline)) {
-    const u32x4 rs = c < c1 ? wr : wr0;
     const uint32_t kb = (uint32_t)(c * kGmKC * 2);
     const uint32_t slot = (uint32_t)(c - c0) % (uint32_t)kGmWSlots;
 #pragma unroll
-    for (int j = 0; j < DW; ++j) gm_dma(rs, wring + slot * WB + wdo[j], wso[j] + kb);
+    for (int j = 0; j < DW; ++j) gm_dma(c < c1 ? wres[j] : wr0, wring + slot * WB + wdo[j], wso[j] + kb);
   };
 
   // operand reads: lane (g, r16) takes row r16 of a subtile, k 8g..8g+7 of the 32-k step s (chunk 4s + g)
@@ -170,6 +179,37 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
   gm_wait_vm<0>();
 
   // lane (g, r16) of tile (a, b): token row 16(im0 + b) + r16, output columns n0 + 16(jn0 + a) + 4g..+3
+  if (gated) {
+    // the up waves (odd: tile rows 32..63) park their values, rounded to bf16 as the GEMM's output would be,
+    // where the rings were; the gate waves (even, same token rows) finish: silu(gate) * up, rounded again
+    __syncthreads();  // every wave is done with the rings
+    uint32_t *park = reinterpret_cast<uint32_t *>(lds) + (wv >> 1) * (2 * MH * 128);
+    if (wv & 1) {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < MH; ++b)
+          *reinterpret_cast<u32x2 *>(park + (a * MH + b) * 128 + 2 * lane) =
+              u32x2{pack_bf16x2(acc[a][b][0], acc[a][b][1]), pack_bf16x2(acc[a][b][2], acc[a][b][3])};
+    }
+    __syncthreads();
+    if (wv & 1) return;
+#pragma unroll
+    for (int b = 0; b < MH; ++b) {
+      const int m = 16 * (im0 + b) + r16;
+      if (m >= M) continue;
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int n = 32 * nt + 16 * a + 4 * g;
+        if (n >= I) continue;
+        const u32x2 u2 = *reinterpret_cast<const u32x2 *>(park + (a * MH + b) * 128 + 2 * lane);
+        st8(out + (int64_t)m * ldo + n,
+            u32x2{silu_mul_bf16x2(pack_bf16x2(acc[a][b][0], acc[a][b][1]), u2[0]),
+                  silu_mul_bf16x2(pack_bf16x2(acc[a][b][2], acc[a][b][3]), u2[1])});
+      }
+    }
+    return;
+  }
   if (!part) {
 #pragma unroll
     for (int b = 0; b < MH; ++b) {
@@ -292,6 +332,34 @@ extern "C" int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t 
   auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
             : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
   hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, st, (const uint16_t *)x, ldx, (const uint16_t *)w, ldw,
-                     (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used);
+                     (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used, 0);
+  return (int)hipGetLastError();
+}
+
+extern "C" int a8_gemm_silu_small(const void *x, int64_t ldx, const void *w13, int64_t ldw, void *out, int64_t ldo,
+                                  int M, int I, int K, int mblocks, void *stream) {
+  using namespace a8;
+  if (M < 0 || I < 0 || K < 0 || mblocks < 1)
+    return set_error(A8_EINVAL, "gemm_silu_small: bad sizes M=%d I=%d K=%d mblocks=%d", M, I, K, mblocks);
+  if (M == 0 || I == 0) return 0;
+  if (M > kGmMaxM || K == 0 || K % kGmKC || I % 8)
+    return set_error(A8_EUNSUP, "gemm_silu_small: M=%d I=%d K=%d outside M <= %d, K a multiple of %d, I of 8", M, I,
+                     K, kGmMaxM, kGmKC);
+  if (!x || !w13 || !out) return set_error(A8_EINVAL, "gemm_silu_small: null pointer");
+  if (!al16g(x) || !al16g(w13) || !al16g(out) || (ldx | ldw | ldo) & 7 || ldx < K || ldw < K || ldo < I)
+    return set_error(A8_EALIGN, "gemm_silu_small: pointers must be 16-byte aligned, leading dims multiples of 8 "
+                     "and >= the row length");
+  if ((int64_t)(M - 1) * ldx * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32) ||
+      (int64_t)(2 * I - 1) * ldw * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32))
+    return set_error(A8_EUNSUP, "gemm_silu_small: operands span more than 4 GiB");
+  const int nch = K / kGmKC;
+  const int MT = std::min(12, ((((M + mblocks - 1) / mblocks) + 31) / 32) * 2);
+  const int nmb = (M + MT * 16 - 1) / (MT * 16);
+  const dim3 grid((unsigned)((I + 31) / 32), 1u, (unsigned)nmb);
+  const bool w8 = MT % 4 == 0;
+  auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
+            : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
+  hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, (hipStream_t)stream, (const uint16_t *)x, ldx,
+                     (const uint16_t *)w13, ldw, (uint16_t *)out, ldo, nullptr, nullptr, M, 2 * I, K, nch, 1, I);
   return (int)hipGetLastError();
 }

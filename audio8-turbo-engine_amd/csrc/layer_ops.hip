@@ -77,11 +77,7 @@ __global__ __launch_bounds__(256) void k_silu_mul(const uint16_t *__restrict__ g
   const u32x4 g = ld16(p), u = ld16(p + I);
   u32x4 o;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float g0 = bf_lo(g[j]), g1 = bf_hi(g[j]);
-    const uint32_t gs = pack_bf16x2(g0 / (1.f + expf(-g0)), g1 / (1.f + expf(-g1)));  // HF: act(gate) in bf16
-    o[j] = pack_bf16x2(bf_lo(gs) * bf_lo(u[j]), bf_hi(gs) * bf_hi(u[j]));
-  }
+  for (int j = 0; j < 4; ++j) o[j] = silu_mul_bf16x2(g[j], u[j]);
   st16(y + (int64_t)r * s_y + 8 * c, o);
 }
 

@@ -512,6 +512,25 @@ def gemm_small(x, w, out=None, splits=1, ws=None, mblocks=1):
     return y
 
 
+def gemm_silu_small(x, w13, out=None, mblocks=1):
+    """out[M, I] = silu_mul(x @ w13^T) in one launch (a8_gemm_silu_small): w13 [2I, K] = [gate; up] rows, the
+    product rounded to bf16 as gemm_small's output, then silu_mul's arithmetic (fast_kernels.py:526-545) in the
+    GEMM's epilogue: the same bits as silu_mul(gemm_small(x, w13)). M <= 192, K a multiple of 64, I of 8."""
+    _check_bf16("x", x, 2)
+    _check_bf16("w13", w13, 2)
+    M, K = x.shape
+    _need(w13.shape[1] == K and w13.shape[0] % 2 == 0, f"w13 shape {tuple(w13.shape)} must be [2I, {K}]")
+    I = w13.shape[0] // 2
+    y = out if out is not None else torch.empty(M, I, dtype=x.dtype, device=x.device)
+    _check_bf16("out", y, 2)
+    _need(y.shape[0] == M and y.shape[1] == I, f"out shape {tuple(y.shape)} does not match [{M}, {I}]")
+    _check_device(x=x, w13=w13, out=y)
+    st = _lib.load().a8_gemm_silu_small(x.data_ptr(), x.stride(0), w13.data_ptr(), w13.stride(0), y.data_ptr(),
+                                        y.stride(0), M, I, K, int(mblocks), _lib.stream_of(x))
+    _lib.check(st, "gemm_silu_small")
+    return y
+
+
 class GemmDispatch:
     """Per-(M, N, K) choice between the library GEMM (torch.matmul -> hipBLASLt) and gemm_small, measured on
     the running GPU at startup, outside graph capture (the reference's GemmDispatch, fast_kernels.py:413-519,
@@ -605,6 +624,15 @@ class GemmDispatch:
         sp, mb = best
         return gemm_small(x, w, splits=sp, ws=self.ws if sp > 1 else None, mblocks=mb)
 
+    def gated(self, x, w13):
+        """silu_mul(self(x, w13)): where the tuned choice for w13 is gemm_small in one pass (no k splits), the
+        activation runs in its epilogue (gemm_silu_small, same bits, one launch and no [M, 2I] round trip);
+        otherwise the product, then silu_mul."""
+        best = self.small.get((x.shape[0], w13.shape[0], w13.shape[1])) if self.enabled and x.dim() == 2 else None
+        if best is not None and best[0] == 1 and x.stride(1) == 1:
+            return gemm_silu_small(x, w13, mblocks=best[1])
+        return silu_mul(self(x, w13))
+
 
 _F16 = torch.float16
 
@@ -660,8 +688,8 @@ def ru_cl(xin, w1, b1, a2, ib2, w2, b2, res, out, TR, taps, dil):
     with xin [B, Tin, C] the activated input ([state | snake1(x)], snake_cat's output), w1 [taps, C, C] and w2
     [C, C] fp16 ([k][n], CLConv's packing without the phase dim), b1 / b2 fp16 [C], a2 / ib2 the second snake's
     fp32 [C] vectors, res the unit's raw input [B, >=TR, C]. The first conv's output h stays in registers in
-    fp32 (h + b1, the snake, one rounding to fp16), as in ru_fused; accumulation is fp32 throughout. C is 96 or
-    192 (one workgroup tile holds a row's channels)."""
+    fp32 (h + b1, the snake, one rounding to fp16), as in ru_fused; accumulation is fp32 throughout. C is 96,
+    192 or 384 (one workgroup tile holds a row's channels)."""
     for name, t, d in (("xin", xin, 3), ("w1", w1, 3), ("w2", w2, 2), ("res", res, 3), ("out", out, 3)):
         _need(isinstance(t, torch.Tensor) and t.dtype == _F16, f"{name} must be a float16 tensor", TypeError)
         _need(t.dim() == d and t.stride(-1) == 1, f"{name} must have {d} dims with a contiguous last dim")

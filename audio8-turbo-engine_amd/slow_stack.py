@@ -72,7 +72,9 @@ class SlowStack:
                             fuse=fuse)
             a = self.mm(o.view(R, -1), L["wo"])
             h, res = rmsnorm(a, L["ln2"], self.eps, residual=res)
-            m = self.mm(silu_mul(self.mm(h, L["w13"])), L["w2"])
+            # a GemmDispatch runs the activation in the w13 product's epilogue where it takes gemm_small
+            act = self.mm.gated(h, L["w13"]) if hasattr(self.mm, "gated") else silu_mul(self.mm(h, L["w13"]))
+            m = self.mm(act, L["w2"])
             nxt = self.layers[i + 1]["ln1"] if i + 1 < nl else self.norm
             h, res = rmsnorm(m, nxt, self.eps, residual=res)
         return h

@@ -13,7 +13,7 @@ builds [state, snake(x)] and conv_cl reads it, and the state keeps the last ctx 
 CLDecoder (fast_engine.py:276-310): conv_in, then per block [snake + transposed conv, 3 residual units
 (snake, dilated conv k, snake, 1x1 conv, + input)], snake + conv_out (one channel), tanh. The reference's
 fused residual unit (_FusedRU, on for the widths TTS_VOC_FUSED_RU names) is FusedRU here, on ru_cl, and
-`fused_ru` names its widths (default 96 and 192, the two ru_cl takes; () keeps every unit as the two convs,
+`fused_ru` names its widths (ru_cl takes 96, 192 and 384; default 96 and 192, where it measured faster; () keeps every unit as the two convs,
 the reference's default). The fused unit keeps the first conv's output in fp32 where the two convs round it
 to fp16, as the reference's does.
 
@@ -100,9 +100,12 @@ class FusedRU:
     (the reference's _FusedRU, fast_engine.py:235-273, on ru_cl): the k-tap conv's output stays in registers
     (fp32, the second snake applied there, one rounding to fp16) and feeds the 1x1 conv in the same workgroup.
     Uses c1's state (activated context) and refreshes it after, as the two-conv path does (any chunk length).
-    Widths 96 and 192 (RU_WIDTHS): one workgroup tile holds a row's channels."""
+    Widths 96, 192 and 384 (RU_WIDTHS): one workgroup tile holds a row's channels."""
 
-    RU_WIDTHS = (96, 192)
+    RU_WIDTHS = (96, 192, 384)
+    # the widths the decoder fuses by default: at 384 channels the fused unit measured slower than the two convs
+    # (201 vs 190 us at block 1's 49152 rows: one row tile and 32-channel slices to fit the row's 384 channels)
+    DEFAULT_WIDTHS = (96, 192)
 
     def __init__(self, c1, c2):
         assert c1.Cin == c1.Cout == c2.Cin == c2.Cout and c2.taps == 1 and c1.ph == c2.ph == 1
@@ -158,7 +161,7 @@ class CLDecoder:
     weights; every conv's state is registered in `states` (per row, for snapshots / row resets). frame: the
     input rows a call takes (sizes each conv's split-K workspace once; the streaming decoder's frame is 4)."""
 
-    def __init__(self, wts, Bmax, dev, states=None, frame=4, fused_ru=FusedRU.RU_WIDTHS):
+    def __init__(self, wts, Bmax, dev, states=None, frame=4, fused_ru=FusedRU.DEFAULT_WIDTHS):
         self.states = states if states is not None else []
         fuse = set(int(c) for c in (fused_ru or ()))
         S = self.states

@@ -358,7 +358,7 @@ def per_config(a8, torch, dev, steps):
                                           "note": "one residual unit, 192 rows x 1024 positions x 192 channels: "
                                                   "snake_cat + ru_cl + state copy vs the k=7 and 1x1 convs"},
                             "note": "one frame of the streaming decoder; synthetic DAC-style weights; residual "
-                                    "units of 96 / 192 channels fused (ru_cl), the others two convs"}
+                                    "units of 96 / 192 channels fused (ru_cl), the 384 / 768-channel ones two convs"}
     del g, dec, dec2, wts, xf, xr
     torch.cuda.empty_cache()
 

@@ -331,6 +331,15 @@ int a8_silu_mul(const void *gu, int64_t s_gu, void *y, int64_t s_y, int rows, in
  */
 int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo,
                   void *ws, int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, void *stream);
+/*
+ * The w13 projection with the gated activation in its epilogue: out[M, I] = silu_mul(x . w13^T), w13 [2I, K]
+ * = [gate; up] rows (row stride ldw), the product rounded to bf16 as a8_gemm_small's, then a8_silu_mul's
+ * arithmetic (serve/fast_kernels.py:526-545): the same bits as a8_gemm_small followed by a8_silu_mul, in one
+ * launch (the reference's SiLU-mul after its w13 GEMM, serve/fast_engine.py:135). M <= 192, K a multiple
+ * of 64, I of 8; mblocks as for a8_gemm_small; no k splits.
+ */
+int a8_gemm_silu_small(const void *x, int64_t ldx, const void *w13, int64_t ldw, void *out, int64_t ldo, int M, int I,
+                       int K, int mblocks, void *stream);
 
 /*
  * The streaming vocoder's channels-last convolutions (the codec decoder's default conv path,
@@ -365,7 +374,7 @@ int a8_snake_cat(const void *x, int64_t s_xb, int64_t s_xt, const void *state, i
  * xin [B, Tin, C] the activated input ([state | snake1(x)]: a8_snake_cat's output, Tin >= TR + (taps-1) dil),
  * w1 [taps, C, C] (tap stride s_wt, row stride s_wc = C) and w2 [C, C] fp16 [k][n] rows, b1 / b2 fp16 [C]
  * (b1 8-byte aligned), a2 / ib2 fp32 [C] (16-byte aligned), res the unit's raw input. fp32 accumulation.
- * C must be 96 or 192 (one workgroup holds a row's channels): else A8_EUNSUP.
+ * C must be 96, 192 or 384 (one workgroup holds a row's channels): else A8_EUNSUP.
  */
 int a8_ru_cl(const void *xin, int64_t s_xb, int64_t s_xt, const void *w1, int64_t s_wt, int64_t s_wc, const void *b1,
              const float *a2, const float *ib2, const void *w2, const void *b2, const void *res, int64_t s_rb,

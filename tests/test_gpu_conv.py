@@ -149,7 +149,7 @@ def test_conv_cl_split_k_equals_one_pass(a8, dev):
 
 
 @pytest.mark.parametrize("B,T,C,dil", [(8, 64, 96, 9), (8, 64, 192, 3), (64, 1024, 192, 1), (65, 1009, 96, 3),
-                                       (3, 5, 96, 9), (2, 130, 192, 9)])
+                                       (3, 5, 96, 9), (2, 130, 192, 9), (64, 256, 384, 3), (5, 70, 384, 9)])
 def test_ru_cl_against_oracle(a8, cref, dev, B, T, C, dil):
     """A whole residual unit in one launch (ru_cl) against the oracle's ru_fused: snake_cat of the state and
     the raw input, then the fused k=7 conv, second snake, 1x1 conv, bias and residual; long inputs (block 2 /
@@ -178,7 +178,7 @@ def test_ru_cl_against_oracle(a8, cref, dev, B, T, C, dil):
 
 def test_ru_cl_refuses_other_widths(a8, dev):
     """Widths whose row does not fit one tile are refused (the caller takes the two convs)."""
-    C = 384
+    C = 768
     xin = torch.zeros(1, 10, C, dtype=F16, device=dev)
     w1, w2 = torch.zeros(7, C, C, dtype=F16, device=dev), torch.zeros(C, C, dtype=F16, device=dev)
     v16, v32 = torch.zeros(C, dtype=F16, device=dev), torch.zeros(C, device=dev)

@@ -111,3 +111,42 @@ def test_gemm_dispatch_graph(a8, dev):
         for o, e in zip(outs, eager):
             assert torch.equal(o, e)
     say(f"  choices {mm.small}")
+
+
+@pytest.mark.parametrize("M,I,K,mblocks", [(192, 4864, 896, 1), (192, 4864, 896, 3), (37, 1000, 640, 1),
+                                           (100, 24, 128, 2), (1, 8, 64, 1)])
+def test_gemm_silu_small(a8, dev, M, I, K, mblocks):
+    """The w13 product with SiLU-mul in its epilogue equals gemm_small then silu_mul bit for bit (the slow AR's
+    4864-wide MLP; ragged I with a partial last tile; row blocks), and that pair matches the oracle's
+    linear + silu_mul (oracle/layer_ref.py) within the GEMM's bar."""
+    say(f"case: gemm_silu M={M} I={I} K={K} mblocks={mblocks}")
+    from oracle import layer_ref
+    g = torch.Generator().manual_seed(M + I + K)
+    x, w13 = randn_bf16(g, M, K), (randn_bf16(g, 2 * I, K) / K ** 0.5).to(BF)
+    xd, wd = x.to(dev), w13.to(dev)
+    got = a8.gemm_silu_small(xd, wd, mblocks=mblocks)
+    pair = a8.silu_mul(a8.gemm_small(xd, wd))
+    torch.cuda.synchronize()
+    assert torch.equal(got, pair)
+    gu = a8.gemm_small(xd, wd).cpu()
+    _check(gu, x, w13)
+    want = layer_ref.silu_mul(gu)
+    assert torch.equal(pair.cpu(), want) or (pair.cpu().float() - want.float()).abs().max().item() <= \
+        2 ** -7 * want.float().abs().max().item()
+
+
+def test_dispatch_gated_takes_the_fused_launch(a8, dev):
+    """GemmDispatch.gated: the fused launch where the tuned w13 choice is gemm_small without k splits (forced
+    here), silu_mul(product) otherwise; both equal silu_mul(dispatch(x, w13))."""
+    say("case: GemmDispatch.gated")
+    g = torch.Generator().manual_seed(3)
+    x, w13 = randn_bf16(g, 192, 896).to(dev), (randn_bf16(g, 2 * 512, 896) / 30.0).to(BF).to(dev)
+    mm = a8.GemmDispatch()
+    mm.small[(192, 1024, 896)] = (1, 1)
+    a = mm.gated(x, w13)
+    b = a8.silu_mul(mm(x, w13))
+    mm.small[(192, 1024, 896)] = None          # the library product, then silu_mul
+    c = mm.gated(x, w13)
+    d = a8.silu_mul(torch.matmul(x, w13.t()))
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(c, d)

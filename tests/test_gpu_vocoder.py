@@ -46,6 +46,38 @@ def test_streaming_decoder_matches_whole_utterance(dev):
     assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
 
 
+def test_streaming_decoder_with_fused_units(dev):
+    """A decoder whose blocks are 192 and 96 channels wide, so every residual unit runs fused (ru_cl): streaming
+    chunks (shorter and longer than the units' contexts) reproduce the oracle's whole-utterance decode, and the
+    two-conv decoder (fused_ru=()) agrees with it as closely."""
+    from oracle import conv_ref
+    say("case: CLDecoder 64->384 ch, rates 2,2 (blocks of 192 / 96 channels: fused units), chunks 1,5,2 x 2 rows")
+    voc = importlib.import_module("audio8-turbo-engine_amd.vocoder")
+    wts = voc.decoder_weights(cin=64, ch=384, rates=(2, 2), k=7, dils=(1, 3, 9), dev="cpu", seed=5)
+    wd = {"conv_in": tuple(t.to(dev) for t in wts["conv_in"]),
+          "blocks": [(a.to(dev), w.to(dev), b.to(dev), s, [tuple(t.to(dev) if torch.is_tensor(t) else t for t in u)
+                                                          for u in us]) for a, w, b, s, us in wts["blocks"]],
+          "final": tuple(t.to(dev) for t in wts["final"])}
+    dec, dec2 = voc.CLDecoder(wd, 2, dev), voc.CLDecoder(wd, 2, dev, fused_ru=())
+    assert all(fu is not None for _, us in dec.blocks for _, _, fu in us)
+    assert all(fu is None for _, us in dec2.blocks for _, _, fu in us)
+    g = torch.Generator().manual_seed(10)
+    B, chunks = 2, (1, 5, 2)
+    x = torch.randn(B, sum(chunks), 64, generator=g)
+    outs, outs2, t0 = [], [], 0
+    for T in chunks:
+        outs.append(dec(x[:, t0:t0 + T].to(dev), B))
+        outs2.append(dec2(x[:, t0:t0 + T].to(dev), B))
+        t0 += T
+    got, got2 = torch.cat(outs, 1).cpu().double(), torch.cat(outs2, 1).cpu().double()
+    want = conv_ref.decoder(wts, x)
+    torch.cuda.synchronize()
+    for name, y in (("fused", got), ("two-conv", got2)):
+        err = (y - want).abs()
+        say(f"{name}: max err {err.max().item():.2e} mean {err.mean().item():.2e}")
+        assert err.max().item() < 2e-2 and err.mean().item() < 2e-3
+
+
 def test_rows_are_independent(dev):
     say("case: CLDecoder row reset, 3 rows")
     voc, wts = _small(dev)
