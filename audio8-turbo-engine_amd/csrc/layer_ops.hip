@@ -27,21 +27,31 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t *__restrict__ x,
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int nch = N >> 3;
-  u32x4 h[kRnMaxChunks];
+  // every load of the row -- x, the residual and the norm weight -- goes out before the first use: one memory
+  // round trip, not one for the row and another for the weight after the reduction
+  // (buffer loads: chunks past the row read zeros through the range check, so no branch splits the batch)
+  const rsrc_t xr = make_rsrc(x + (int64_t)row * sx, (uint32_t)N * 2u), wr = make_rsrc(w, (uint32_t)N * 2u);
+  const rsrc_t rr = make_rsrc(RES ? r + (int64_t)row * sr : x, RES ? (uint32_t)N * 2u : 0u);
+  u32x4 h[kRnMaxChunks], rv[kRnMaxChunks], wv[kRnMaxChunks];
+#pragma unroll
+  for (int c = 0; c < kRnMaxChunks; ++c) {
+    const uint32_t off = (uint32_t)(lane + 64 * c) * 16u;
+    h[c] = bld16(xr, off);
+    rv[c] = RES ? bld16(rr, off) : u32x4{0u, 0u, 0u, 0u};
+    wv[c] = bld16(wr, off);
+  }
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < kRnMaxChunks; ++c) {
     const int ch = lane + 64 * c;
-    h[c] = u32x4{0u, 0u, 0u, 0u};
     if (ch >= nch) continue;
-    u32x4 v = ld16(x + (int64_t)row * sx + 8 * ch);
+    u32x4 v = h[c];
     if (RES) {  // residual add in fp32, rounded once to bf16 (the new residual stream)
-      const u32x4 rv = ld16(r + (int64_t)row * sr + 8 * ch);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = pack_bf16x2(bf_lo(v[j]) + bf_lo(rv[j]), bf_hi(v[j]) + bf_hi(rv[j]));
+      for (int j = 0; j < 4; ++j) v[j] = pack_bf16x2(bf_lo(v[j]) + bf_lo(rv[c][j]), bf_hi(v[j]) + bf_hi(rv[c][j]));
       st16(ro + (int64_t)row * sro + 8 * ch, v);
+      h[c] = v;
     }
-    h[c] = v;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float a = bf_lo(v[j]), b = bf_hi(v[j]);
@@ -55,12 +65,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const uint16_t *__restrict__ x,
   for (int c = 0; c < kRnMaxChunks; ++c) {
     const int ch = lane + 64 * c;
     if (ch >= nch) continue;
-    const u32x4 wv = ld16(w + 8 * ch);
     u32x4 o;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t xn = pack_bf16x2(bf_lo(h[c][j]) * inv, bf_hi(h[c][j]) * inv);  // HF: .to(input dtype)
-      o[j] = pack_bf16x2(bf_lo(wv[j]) * bf_lo(xn), bf_hi(wv[j]) * bf_hi(xn));         // HF: weight * x
+      o[j] = pack_bf16x2(bf_lo(wv[c][j]) * bf_lo(xn), bf_hi(wv[c][j]) * bf_hi(xn));   // HF: weight * x
     }
     st16(y + (int64_t)row * sy + 8 * ch, o);
   }

@@ -49,6 +49,8 @@ def parse():
                    help="only launch the C4 prefill 3x (target of rocprofv3 --pmc passes)")
     p.add_argument("--vocoder-probe", action="store_true",
                    help="only run the streaming decoder for 5 frames at 192 rows (target of rocprofv3)")
+    p.add_argument("--slow-probe", action="store_true",
+                   help="only tune GemmDispatch and replay the 24-layer slow-AR step 3 times (target of rocprofv3)")
     return p.parse_args()
 
 
@@ -473,6 +475,29 @@ def vocoder_probe(a8, torch, dev):
     print("vocoder probe: 5 frames done", flush=True)
 
 
+def slow_probe(a8, torch, dev):
+    """Profile target for the slow-AR step's projections: the 24-layer step at 192 rows x KV 2048 (synthetic
+    weights, as the slow_ar_step leg) with GemmDispatch tuned first, then 3 steps replayed from a graph."""
+    from importlib import import_module
+    ss = import_module(a8.__name__ + ".slow_stack")
+    b, S, layers, hidden, inter = 192, 2048, LAYERS, 896, 4864
+    wts, norm = ss.random_weights(layers, hidden, NQ, NKV, HD, inter, dev, seed=11)
+    st = a8.SlowStack(wts, norm, NQ, NKV, HD, 1e-6, 10000.0, max_rows=max(16 * b, 8192), cache_rows=b + 1,
+                      cache_len=S, max_pos=S, dev=dev)
+    mm = a8.GemmDispatch()
+    mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b])
+    st.mm = mm
+    gen = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(b, hidden, generator=gen, device=dev).to(torch.bfloat16)
+    lens_d = torch.full((b,), S, dtype=torch.int32, device=dev)
+    pos, slot = lens_d - 1, torch.arange(b, dtype=torch.int32, device=dev)
+    g = capture(torch, lambda: st.forward(x, pos, slot, lens_d, rowmap=False, fuse=True))
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    print("slow probe: choices", {f"{N}x{K}": c for (M, N, K), c in mm.small.items()}, flush=True)
+
+
 def prefill_probe(a8, torch, dev):
     """Counter target for the prefill: the C4 workload (64 requests, n ~ U[40, 400] after a 300-position
     prefix, 13,745 packed rows) launched 3 times. Run under rocprofv3 --pmc with one counter group a pass."""
@@ -512,6 +537,9 @@ def main():
         return
     if args.vocoder_probe:
         vocoder_probe(a8, torch, dev)
+        return
+    if args.slow_probe:
+        slow_probe(a8, torch, dev)
         return
     props = torch.cuda.get_device_properties(dev)
     w = build_workload(a8, torch, args.config, dev)
