@@ -254,10 +254,9 @@ def per_config(a8, torch, dev, steps):
     g = capture(torch, lambda: st.forward(xbuf, pos, slot, lens_d, rowmap=False, fuse=True))
     us = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
     wbytes = layers * 2 * (hidden * (NQ + 2 * NKV) * HD + hidden * NQ * HD + hidden * 2 * inter + inter * hidden)
-    res["slow_ar_step"] = {"us_per_step": round(us, 1), "us_per_layer": round(us / layers, 2), "rows": b, "kv_len": S,
-                           "hidden": hidden, "inter": inter, "weight_bytes": wbytes,
-                           "note": "the full slow-AR decode step around the attention path; synthetic weights; "
-                                   "projections through hipBLASLt (the reference's default mm)"}
+    lib_step = {"us_per_step": round(us, 1), "us_per_layer": round(us / layers, 2),
+                "note": "projections through hipBLASLt (torch.matmul, the reference's default mm), silu_mul "
+                        "separate"}
     del g
     # the same step with the projections through GemmDispatch: per shape, hipBLASLt or this package's small-M
     # GEMM (gemm_small, with its split count and row blocks), whichever the timing at startup finds faster --
@@ -268,14 +267,18 @@ def per_config(a8, torch, dev, steps):
     xbuf.copy_(x0)
     g = capture(torch, lambda: st.forward(xbuf, pos, slot, lens_d, rowmap=False, fuse=True))
     us2 = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
-    res["slow_ar_step_dispatch"] = {
-        "us_per_step": round(us2, 1), "us_per_layer": round(us2 / layers, 2),
+    res["slow_ar_step"] = {
+        "us_per_step": round(us2, 1), "us_per_layer": round(us2 / layers, 2), "rows": b, "kv_len": S,
+        "hidden": hidden, "inter": inter, "weight_bytes": wbytes,
         "choices": {f"{N}x{K}": (None if c is None else {"splits": c[0], "mblocks": c[1]})
                     for (M, N, K), c in mm.small.items()},
         "tune_us": {f"{N}x{K}": [round(lt * 1e3, 2), None if bt is None else round(bt * 1e3, 2)]
                     for (M, N, K), lt, _, bt in mm.log},
-        "note": "projections through GemmDispatch (library vs gemm_small per shape, timed at startup); "
-                "tune_us = [library, chosen] per call"}
+        "library": lib_step,
+        "note": "the full slow-AR decode step around the attention path (fused store + decode, rmsnorm, the four "
+                "projections, SiLU-mul); synthetic weights; projections through GemmDispatch (hipBLASLt or "
+                "gemm_small per shape, timed at startup on the layers' weights; w13 with SiLU-mul in its "
+                "epilogue where gemm_small takes it); tune_us = [library, chosen] per call"}
     del g, st, wts, xbuf, mm
     torch.cuda.empty_cache()
 
