@@ -180,3 +180,61 @@ def test_slow_stack_prefill_and_graph(a8, ref, lref, dev):
         outs.append(h.cpu())
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
     assert torch.equal(outs[1].view(torch.int16), outs[2].view(torch.int16))
+
+
+def test_slow_stack_with_gemm_dispatch(a8, ref, lref, dev):
+    """The decode tick with the projections through a tuned GemmDispatch (gemm_small where it times faster,
+    the w13 product with SiLU-mul in its epilogue) at the slow AR's widths and the decode tick's 192 rows,
+    against the oracle (the same bar as the library-GEMM stack), and captured in a graph: replays equal
+    the eager step bit for bit."""
+    say("case: slow stack with GemmDispatch, 192 rows")
+    n_layers, hidden, inter, b, S = 2, 896, 4864, 192, 256
+    st, layers, norm = _stack(a8, dev, n_layers, hidden, inter, b, S, seed=13)
+    mm = a8.GemmDispatch()
+    mm.tune([L[k] for L in layers for k in ("wqkv", "wo", "w13", "w2")], [b])
+    # every projection on gemm_small here, whatever the timing chose (the library path has its own test)
+    for (M, N, K), c in list(mm.small.items()):
+        mm.small[(M, N, K)] = c if c is not None else (1, 1)
+    st.mm = mm
+    g = torch.Generator().manual_seed(14)
+    x = randn_bf16(g, b, hidden)
+    lens = torch.randint(1, S + 1, (b,), generator=g).int()
+    pos, slot = lens - 1, torch.arange(b, dtype=torch.int32)
+    kc0 = [t.clone() for t in st.kc]
+    vc0 = [t.clone() for t in st.vc]
+    kc = [t.cpu() for t in st.kc]
+    vc = [t.cpu() for t in st.vc]
+    want = lref.slow_stack(x.clone(), pos, slot, lens, _cpu(layers), norm.cpu(), NQ, NKV, HD, 1e-6,
+                           st.attn.cos.cpu(), st.attn.sin.cpu(), kc, vc, rowmap=False)
+    xd, posd, slotd, lensd = x.to(dev), pos.to(dev), slot.to(dev), lens.to(dev)
+    got = st.forward(xd.clone(), posd, slotd, lensd, rowmap=False, fuse=True).clone()
+    torch.cuda.synchronize()
+    emax, emean, vmax = _close(got, want)
+    say(f"  max-abs {emax:.3e} mean-abs {emean:.3e} (max |h| {vmax:.2f}); choices {mm.small}")
+    assert emax <= 0.02 * vmax and emean <= 5e-3
+    # graph capture of the same step from the same caches: every replay == the eager result
+    xbuf = torch.empty_like(xd)
+
+    def step():
+        return st.forward(xbuf, posd, slotd, lensd, rowmap=False, fuse=True)
+
+    for i in range(n_layers):
+        st.kc[i].copy_(kc0[i])
+        st.vc[i].copy_(vc0[i])
+    xbuf.copy_(xd)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        yg = step()
+    for rep in range(3):
+        for i in range(n_layers):
+            st.kc[i].copy_(kc0[i])
+            st.vc[i].copy_(vc0[i])
+        xbuf.copy_(xd)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, got), f"replay {rep} differs from the eager step"
