@@ -310,8 +310,9 @@ class DecodeAttention:
         nsplit = max(1, min(int(nsplit), self.nsplit_max))
         assert b * nsplit <= self.cap, (b, nsplit, self.cap)
         _need(bn == 64, f"bn={bn}: only 64-key tiles are implemented", NotImplementedError)
-        _need(q.dtype == _BF16, f"q must be bfloat16 (got {q.dtype}); fp32 queries are not implemented",
-              NotImplementedError if q.dtype == torch.float32 else TypeError)
+        if q.dtype == torch.float32:
+            return self._call_f32q(q, kc, vc, lens, out, rowmap)
+        _need(q.dtype == _BF16, f"q must be bfloat16 or float32 (got {q.dtype})", TypeError)
         _check_bf16("q", q, 3)
         _need(q.shape[1] == self.nq and q.shape[2] == self.hd,
               f"q shape {tuple(q.shape)} does not match [b, {self.nq}, {self.hd}]")
@@ -349,6 +350,33 @@ class DecodeAttention:
         _lib.check(st, "decode_attention")
         return out
 
+
+    def _call_f32q(self, q, kc, vc, lens, out, rowmap):
+        """fp32 queries: the reference's PREC = "ieee" branch (fast_kernels.py:279; fp32 products, bf16 weights in
+        P.V, the output in out's dtype, bf16 or fp32) through a8_decode_attn_f32q, one launch (the engine never
+        decodes an fp32 q; the kernel is exact, not tuned)."""
+        b = q.shape[0]
+        _need(q.dim() == 3 and q.stride(2) == 1 and q.shape[1] == self.nq and q.shape[2] == self.hd,
+              f"q shape {tuple(q.shape)} does not match [b, {self.nq}, {self.hd}] with a contiguous last dim")
+        _check_cache(kc, vc, self.nkv, self.hd)
+        _check_i32("lens", lens, b)
+        if rowmap is not None:
+            _check_i32("rowmap", rowmap, b)
+        _need(isinstance(out, torch.Tensor) and out.dtype in (_BF16, torch.float32) and out.dim() == 3 and
+              out.stride(2) == 1, "out must be a bfloat16 or float32 [b, nq, hd] tensor with a contiguous last dim",
+              TypeError)
+        _need(out.shape[0] >= b and out.shape[1] == self.nq and out.shape[2] == self.hd,
+              f"out shape {tuple(out.shape)} does not match [{b}, {self.nq}, {self.hd}]")
+        _check_device(q=q, kc=kc, vc=vc, lens=lens, rowmap=rowmap, out=out)
+        if b == 0:
+            return out
+        st = _lib.load().a8_decode_attn_f32q(
+            q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1),
+            kc.stride(2), kc.shape[0], kc.shape[2], lens.data_ptr(), rowmap.data_ptr() if rowmap is not None else None,
+            out.data_ptr(), out.stride(0), out.stride(1), 1 if out.dtype == torch.float32 else 0, b, self.nq,
+            self.nkv, self.hd, float(self.scale), _lib.stream_of(q))
+        _lib.check(st, "decode_attention (fp32 q)")
+        return out
 
 def heaviest_first(blocks):
     """(q0, n, slot, pos0) query blocks sorted by their key count pos0 + n, largest first; stable."""

@@ -213,6 +213,18 @@ int a8_decode_attn_flat(const void *q, int64_t s_qb, int64_t s_qh,
                         int b, int nq, int nkv, int hd, int grid, float scale, void *stream);
 
 /*
+ * a8_decode_attn_f32q replaces the PREC = "ieee" branch of serve/fast_kernels.py:271-290 (DecodeAttention
+ * with an fp32 query, 279; kernels 193-253): q fp32 [b, nq, hd] (strides s_qb, s_qh), the caches and lens /
+ * rowmap as a8_decode_attn; fp32 products q . k (k widened exactly), the softmax weights rounded to bf16 for
+ * P.V, fp32 sums; out [b, nq, hd] bf16 (out_f32 = 0) or fp32 (out_f32 = 1), strides s_ob, s_oh. One launch,
+ * no workspace; hd 64 or 128, at most 16 q heads per kv head.
+ */
+int a8_decode_attn_f32q(const float *q, int64_t s_qb, int64_t s_qh, const void *kc, const void *vc, int64_t s_kb,
+                        int64_t s_kh, int64_t s_ks, int cache_rows, int cache_len, const int32_t *lens,
+                        const int32_t *rowmap, void *out, int64_t s_ob, int64_t s_oh, int out_f32, int b, int nq,
+                        int nkv, int hd, float scale, void *stream);
+
+/*
  * Launch shape of a8_decode_attn_flat / a8_store_decode_flat (replaces the split heuristic of
  * serve/fast_engine.py:776): workgroups for b rows over a cache of cache_len positions on n_cu compute
  * units, within a workspace of cap_row_splits row-splits.

@@ -149,20 +149,23 @@ def decode_split(q, kc, vc, lens, nsplit, rowmap=None, scale=None, bn=64):
     return acc, ml
 
 
-def decode_combine(acc, ml):
-    """The combine kernel (fast_kernels.py:238-253): out = bf16(sum(w acc) / sum(w l)), w = exp(m - M)."""
+def decode_combine(acc, ml, out_dtype=BF16):
+    """The combine kernel (fast_kernels.py:238-253): out = sum(w acc) / sum(w l), w = exp(m - M), stored in
+    the output's dtype (bf16, or fp32 for an fp32 output; fast_kernels.py:253)."""
     m, l = ml[..., 0], ml[..., 1]
     M = m.amax(-1, keepdim=True)
     w = torch.where(m == NEG_INF, torch.zeros(()), torch.exp(m - M))
     num = (acc * w[..., None]).sum(-2)
     den = (l * w).sum(-1)
-    return (num / den[..., None]).to(BF16)
+    return (num / den[..., None]).to(out_dtype)
 
 
-def decode_attention(q, kc, vc, lens, nsplit=1, rowmap=None, scale=None, bn=64):
-    """DecodeAttention.__call__ (fast_kernels.py:271-290) on CPU tensors; returns out [b, nq, hd] bf16."""
+def decode_attention(q, kc, vc, lens, nsplit=1, rowmap=None, scale=None, bn=64, out_dtype=BF16):
+    """DecodeAttention.__call__ (fast_kernels.py:271-290) on CPU tensors; returns out [b, nq, hd] (bf16, or
+    out_dtype). q may be bf16 or fp32: the split works on q.float() either way, which is the reference's
+    PREC = "ieee" product for an fp32 q (fast_kernels.py:279) and exact for a bf16 one."""
     acc, ml = decode_split(q, kc, vc, lens, max(1, int(nsplit)), rowmap, scale, bn)
-    return decode_combine(acc, ml)
+    return decode_combine(acc, ml, out_dtype)
 
 
 # ----------------------------------------------------------------------------------------------

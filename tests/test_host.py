@@ -95,8 +95,13 @@ def test_decode_shim_validation(a8):
     lens = torch.ones(3, dtype=torch.int32)
     with pytest.raises(AssertionError):                     # fast_kernels.py:276: b * nsplit <= cap
         att(q, kc, kc, lens, q, nsplit=3)
-    with pytest.raises(NotImplementedError):
+    # an fp32 query takes its own entry point (validated the same way: device tensors only)
+    with pytest.raises(ValueError, match="HIP device"):
         att(q.float(), kc, kc, lens, q, nsplit=1)
+    with pytest.raises(TypeError):                          # out must be bf16 or fp32
+        att(q.float(), kc, kc, lens, q.half(), nsplit=1)
+    with pytest.raises(TypeError):                          # q must be bf16 or fp32
+        att(q.half(), kc, kc, lens, q, nsplit=1)
     with pytest.raises(NotImplementedError):
         att(q, kc, kc, lens, q, nsplit=1, bn=32)
     with pytest.raises(ValueError, match="HIP device"):

@@ -429,6 +429,32 @@ def test_layer_slow_stack_against_float64_unrolled(ref, lref):
     assert (got.double() - wrong).abs().max().item() > 10 * err
 
 
+def test_decode_fp32_query_against_float64(ref):
+    """The oracle's decode with an fp32 query (the reference's PREC = "ieee" branch): against a float64
+    textbook softmax attention over the same fp32 q and bf16 K / V, within the bf16 rounding of the weights
+    that the reference applies before P.V; fp32 and bf16 outputs."""
+    g = torch.Generator().manual_seed(31)
+    b, nq, nkv, hd, S = 5, 6, 2, 64, 150
+    q = torch.randn(b, nq, hd, generator=g)
+    kc = torch.randn(b, nkv, S, hd, generator=g).to(torch.bfloat16)
+    vc = torch.randn(b, nkv, S, hd, generator=g).to(torch.bfloat16)
+    lens = torch.tensor([1, 64, 65, 100, 150], dtype=torch.int32)
+    got = ref.decode_attention(q, kc, vc, lens, nsplit=3, out_dtype=torch.float32).double()
+    got_bf = ref.decode_attention(q, kc, vc, lens, out_dtype=torch.bfloat16)
+    assert got_bf.dtype == torch.bfloat16
+    group = nq // nkv
+    for r in range(b):
+        L = int(lens[r])
+        for h in range(nq):
+            k = kc[r, h // group, :L].double()
+            v = vc[r, h // group, :L].double()
+            s = (k @ q[r, h].double()) * hd ** -0.5
+            p = torch.softmax(s, 0)
+            want = p @ v
+            assert (got[r, h] - want).abs().max().item() <= 1e-2 * max(1.0, want.abs().max().item())
+            assert (got_bf[r, h].double() - want).abs().max().item() <= 2e-2 * max(1.0, want.abs().max().item())
+
+
 # ---- the vocoder's channels-last convolutions (oracle/conv_ref.py) ----
 
 @pytest.fixture(scope="module")
