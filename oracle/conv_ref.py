@@ -18,7 +18,9 @@ Pinned by tests/test_oracle.py against torch.nn.functional.conv1d (causal / dila
 conv_transpose1d (the phase split of a stride-s transposed conv, as fast_engine.py:186-194 builds it), in
 float64, and by a brute-force loop on tiny sizes; ru_fused against the two-conv unit (snake_cat, conv_cl,
 conv_cl with the residual) bit for bit where the second snake is the identity (ib2 = 0: h rounds to fp16
-either way), and against a float64 loop with the snake.
+either way), and against a float64 loop with the snake; decoder's composition (block order, transposed-conv
+crop, unit order and dilations, causal taps) against the closed-form impulse response of structured weights
+(identity snakes, delta taps, sample-repeat transposed convs), and by a causality invariant on random weights.
 """
 from __future__ import annotations
 

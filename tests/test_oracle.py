@@ -603,3 +603,85 @@ def test_vocoder_pack_conv_against_torch_conv():
         assert got.shape == want.shape
         err = (got.double() - want).abs()
         assert (err <= want.abs() * 2 ** -10 + 1e-3).all(), (trans, K, err.max())
+
+
+def _structured_decoder(cin, ch, rates, k, dils, c):
+    """decoder_weights-shaped weights under which the decoder is a known linear filter on channel 0: every snake
+    the identity (alpha 1e-6: x + sin(ax)^2 / a moves a dyadic fp16 value by less than half an ulp), conv_in
+    and the final conv the current tap of channel 0, each transposed conv a sample repeat (taps 0 .. s-1 of
+    channel i -> i), each residual unit x + c * x(t - (k - 1) dil) (its k-conv the oldest tap, its 1x1 conv
+    c times the identity)."""
+    def eye_tap(co, ci, kk, tap):
+        w = torch.zeros(co, ci, kk)
+        for i in range(min(co, ci)):
+            w[i, i, tap] = 1.0
+        return w
+
+    alpha = lambda C: torch.full((C,), 1e-6)
+    wts = {"conv_in": (eye_tap(ch, cin, k, k - 1), torch.zeros(ch)), "blocks": []}
+    C = ch
+    for s in rates:
+        tw = torch.zeros(C, C // 2, 2 * s)
+        for i in range(C // 2):
+            tw[i, i, :s] = 1.0
+        a0 = alpha(C)
+        C //= 2
+        units = [(alpha(C), eye_tap(C, C, k, 0), torch.zeros(C), d, alpha(C), c * eye_tap(C, C, 1, 0), torch.zeros(C))
+                 for d in dils]
+        wts["blocks"].append((a0, tw, torch.zeros(C), s, units))
+    wts["final"] = (alpha(C), eye_tap(1, C, k, k - 1), torch.zeros(1))
+    return wts
+
+
+def test_decoder_composition_closed_form():
+    """The oracle decoder's composition (fast_engine.py:276-310: conv_in, per block snake + causal transposed conv
+    + residual units, snake, conv_out, tanh) against the closed-form impulse response of the structured weights
+    above: an impulse of height h at input time t0 leaves the transposed convs as a box of length s, each unit of
+    dilation d at a block's rate multiplies the z-transform by (1 + c z^-(k-1) d) in that rate's samples, later
+    blocks repeat every sample s times. A wrong block order, dilation, crop side, tap order or a non-causal
+    shift moves or reweights the response."""
+    from oracle import conv_ref
+    cin, ch, rates, k, dils, c, T = 2, 8, (2, 4), 3, (1, 2), 0.5, 5
+    wts = _structured_decoder(cin, ch, rates, k, dils, c)
+    for t0, h in ((0, 0.25), (2, -0.375), (4, 0.5)):
+        x = torch.zeros(1, T, cin, dtype=torch.float64)
+        x[0, t0, 0] = h
+        x[0, t0, 1] = 0.75  # channel 1 never reaches the output (the final conv reads channel 0)
+        got = conv_ref.decoder(wts, x)[0].double()
+        # closed form: the response as a dict time -> value, refined block by block
+        resp = {t0: h}
+        for bi, s in enumerate(rates):
+            resp = {t * s + j: v for t, v in resp.items() for j in range(s)}  # repeat (box of length s)
+            for d in dils:  # x + c x(t - (k - 1) d), in order
+                D = (k - 1) * d
+                nxt = dict(resp)
+                for t, v in resp.items():
+                    nxt[t + D] = nxt.get(t + D, 0.0) + c * v
+                resp = nxt
+        up = int(np.prod(rates))
+        want = torch.zeros(T * up, dtype=torch.float64)
+        for t, v in resp.items():
+            if t < T * up:
+                want[t] = v
+        assert got.shape == want.shape
+        assert torch.allclose(got, torch.tanh(want), rtol=0, atol=1e-12), (t0, (got - torch.tanh(want)).abs().max())
+
+
+def test_decoder_is_causal_in_its_input():
+    """Random weights at small sizes: changing input time t0 leaves every output sample before t0 * up
+    unchanged, and changes the sample at t0 * up (the decoder streams, so a chunked run can equal the whole
+    utterance)."""
+    import importlib
+    voc = importlib.import_module("audio8-turbo-engine_amd.vocoder")
+    from oracle import conv_ref
+    wts = voc.decoder_weights(cin=8, ch=16, rates=(2, 2), k=3, dils=(1, 2), seed=3)
+    g = torch.Generator().manual_seed(4)
+    T, up = 6, 4
+    x = torch.randn(1, T, 8, generator=g).to(torch.float16).double()
+    base = conv_ref.decoder(wts, x)[0]
+    for t0 in (1, 3, 5):
+        x2 = x.clone()
+        x2[0, t0] += 1.0
+        y = conv_ref.decoder(wts, x2)[0]
+        assert torch.equal(y[:t0 * up], base[:t0 * up]), t0
+        assert not torch.equal(y[t0 * up:], base[t0 * up:]), t0
