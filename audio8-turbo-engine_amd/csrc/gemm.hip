@@ -33,6 +33,7 @@ constexpr int kGmKC = 64;   // k per chunk
 constexpr int kGmWSlots = 8;  // W ring slots: 7 chunks of weights in flight (HBM latency), X only 2 (L2)
 constexpr int kGmMaxM = 192;
 constexpr int kGmCntBytes = 4096;  // k splits: the workspace starts with one 32-bit counter per tile (<= 1024)
+constexpr int kGmSsMax = 32;       // norm-fused products: partial sums of squares per row (N / 32 <= 32)
 
 __device__ __forceinline__ void gm_dma(u32x4 rs, uint32_t lds, uint32_t voff) {
   asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" : : "{m0}"(lds), "v"(voff), "s"(rs) : "memory");
@@ -47,12 +48,27 @@ __device__ __forceinline__ void gm_wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// Epilogue options of the norm-fused projections (a8_gemm_small_norm; zero / null: the plain product):
+//   res_add  out is the residual stream: out = bf16(f32(bf16(acc)) + f32(out)) in place (the reference's
+//            o / w2 product rounded to bf16, then rmsnorm's residual add, fast_kernels.py:30-46);
+//   ss_out   with res_add: per token row and 32-column group, the sum of squares of the new residual values
+//            (fp32 [Mall][N / 32]: the next RMSNorm's statistic, summed by its consumer);
+//   ss_in    the token rows are a raw residual stream h whose RMSNorm (weight folded into w by the caller) this
+//            product consumes: acc is scaled by rsqrt(sum_j ss_in[m][j] / K + eps) before the rounding.
+struct GmEpi {
+  int res_add;
+  float *ss_out;
+  const float *ss_in;
+  int ss_n;
+  float eps;
+};
+
 template <int MT, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__restrict__ x, int64_t ldx,
                                                            const uint16_t *__restrict__ w, int64_t ldw,
                                                            uint16_t *__restrict__ out, int64_t ldo,
                                                            float *__restrict__ part, int32_t *__restrict__ cnt,
-                                                           int Mall, int N, int K, int cps, int S, int I) {
+                                                           int Mall, int N, int K, int cps, int S, int I, GmEpi ep) {
   static_assert(NW == 4 || NW == 8, "waves");
   static_assert(MT >= 2 && MT * 16 <= kGmMaxM && (2 * MT) % NW == 0, "token subtiles");
   constexpr int XB = MT * 16 * 128;        // X bytes per ring slot (token rows x 128 bytes)
@@ -128,6 +144,30 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
 #pragma unroll
     for (int b = 0; b < MH; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // ss_in: thread m < M loads row m's partial sums of squares now, ahead of every DMA request (loads complete in
+  // order, so the first chunk's wait covers them), and parks 1 / rms in LDS after that wait
+  __shared__ float inv_s[kGmMaxM];
+  f32x4 ssv[kGmSsMax / 4];
+  const bool has_ss = ep.ss_in != nullptr;
+  if (has_ss && (int)threadIdx.x < M) {
+    const float *sp4 = ep.ss_in + (int64_t)(mb0 + (int)threadIdx.x) * ep.ss_n;
+#pragma unroll
+    for (int j = 0; j < kGmSsMax / 4; ++j)
+      ssv[j] = 4 * j < ep.ss_n ? *reinterpret_cast<const f32x4 *>(sp4 + 4 * j) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // res_add without k splits: this lane's old residual values, requested ahead of the DMA as well
+  u32x2 rold[2][MH];
+  if (ep.res_add && !part) {
+#pragma unroll
+    for (int b = 0; b < MH; ++b)
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int m = 16 * (im0 + b) + r16, n = n0 + 16 * (jn0 + a) + 4 * g;
+        rold[a][b] = (m < M && n < N) ? *reinterpret_cast<const u32x2 *>(out + (int64_t)m * ldo + n) : u32x2{0u, 0u};
+      }
+  }
+
   // W chunks c0 .. c0 + P - 1 (P = kGmWSlots - 1 in flight), then X chunks c0, c0 + 1; per chunk c: the wait,
   // the meeting (everyone is done with chunk c - 1, whose slots the next requests refill), X(c + 2), W(c + P)
   constexpr int P = kGmWSlots - 1;
@@ -177,6 +217,16 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
   }
   // the requests past the range still write (zeros) into LDS: let them land before the workgroup ends
   gm_wait_vm<0>();
+  if (has_ss) {  // 1 / rms of every token row, for the epilogues (the loads above have long returned)
+    if ((int)threadIdx.x < M) {
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < kGmSsMax / 4; ++j)  // in order 0 .. ss_n - 1 (the rest are zeros)
+        t = (((t + ssv[j][0]) + ssv[j][1]) + ssv[j][2]) + ssv[j][3];
+      inv_s[threadIdx.x] = __builtin_amdgcn_rsqf(t / (float)K + ep.eps);
+    }
+    __syncthreads();
+  }
 
   // lane (g, r16) of tile (a, b): token row 16(im0 + b) + r16, output columns n0 + 16(jn0 + a) + 4g..+3
   if (gated) {
@@ -184,6 +234,14 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
     // where the rings were; the gate waves (even, same token rows) finish: silu(gate) * up, rounded again
     __syncthreads();  // every wave is done with the rings
     uint32_t *park = reinterpret_cast<uint32_t *>(lds) + (wv >> 1) * (2 * MH * 128);
+    if (has_ss) {  // the consumed RMSNorm's 1 / rms, on the fp32 products of both halves
+#pragma unroll
+      for (int b = 0; b < MH; ++b) {
+        const float iv = inv_s[min(16 * (im0 + b) + r16, M - 1)];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) acc[a][b] *= iv;
+      }
+    }
     if (wv & 1) {
 #pragma unroll
       for (int a = 0; a < 2; ++a)
@@ -214,13 +272,26 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
 #pragma unroll
     for (int b = 0; b < MH; ++b) {
       const int m = 16 * (im0 + b) + r16;
-      if (m >= M) continue;
+      const float iv = has_ss ? inv_s[min(m, M - 1)] : 1.f;
+      float ss = 0.f;
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int n = n0 + 16 * (jn0 + a) + 4 * g;
-        if (n < N)
-          st8(out + (int64_t)m * ldo + n,
-              u32x2{pack_bf16x2(acc[a][b][0], acc[a][b][1]), pack_bf16x2(acc[a][b][2], acc[a][b][3])});
+        u32x2 o{pack_bf16x2(acc[a][b][0] * iv, acc[a][b][1] * iv), pack_bf16x2(acc[a][b][2] * iv, acc[a][b][3] * iv)};
+        if (ep.res_add) {  // h = bf16(a + res), a the product rounded to bf16 (zeros outside the tile's range)
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            o[e] = pack_bf16x2(bf_lo(o[e]) + bf_lo(rold[a][b][e]), bf_hi(o[e]) + bf_hi(rold[a][b][e]));
+            const float h0 = bf_lo(o[e]), h1 = bf_hi(o[e]);
+            ss += (m < M && n < N) ? h0 * h0 + h1 * h1 : 0.f;
+          }
+        }
+        if (m < M && n < N) st8(out + (int64_t)m * ldo + n, o);
+      }
+      if (ep.res_add && ep.ss_out) {  // this wave's 32 columns of row m: the four lane groups' sums
+        ss = sum_over_groups(ss);
+        const int grp = (n0 + 32 * (wv & 1)) >> 5;
+        if (g == 0 && m < M && n0 + 32 * (wv & 1) < N) ep.ss_out[(int64_t)(mb0 + m) * (N >> 5) + grp] = ss;
       }
     }
     return;
@@ -256,11 +327,15 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
   __syncthreads();
   if (!last) return;
   const int ncol = min(kGmNB, N - n0) >> 3;  // 8-column groups of the tile (N is a multiple of 8)
-  for (int t = threadIdx.x; t < M * 8; t += 64 * NW) {
-    const int m = t >> 3, q = t & 7;
-    if (q >= ncol) continue;
-    const int n = n0 + 8 * q;
+  // (every lane runs the loop to its end: the sums of squares below reduce across lanes)
+  for (int t0 = 0; t0 < M * 8; t0 += 64 * NW) {
+    const int t = t0 + (int)threadIdx.x;
+    const int m = min(t >> 3, M - 1), q = t & 7;
+    const bool live = t < M * 8 && q < ncol;
+    const int n = n0 + 8 * min(q, ncol - 1);
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const u32x4 rv = (ep.res_add && live) ? *reinterpret_cast<const u32x4 *>(out + (int64_t)m * ldo + n)
+                                          : u32x4{0u, 0u, 0u, 0u};
     const uint32_t o0 = (uint32_t)((((int64_t)mb0 + m) * N + n) * 4), os = (uint32_t)((int64_t)Mall * N * 4);
     // four splits' loads in flight at a time (past S: offsets past the range, zeros, not added)
     for (int j = 0; j < S; j += 4) {
@@ -281,8 +356,25 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
         }
       }
     }
-    st16(out + (int64_t)m * ldo + n, u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                                            pack_bf16x2(v[6], v[7])});
+    const float iv = has_ss ? inv_s[m] : 1.f;
+    u32x4 o{pack_bf16x2(v[0] * iv, v[1] * iv), pack_bf16x2(v[2] * iv, v[3] * iv), pack_bf16x2(v[4] * iv, v[5] * iv),
+            pack_bf16x2(v[6] * iv, v[7] * iv)};
+    if (ep.res_add) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = pack_bf16x2(bf_lo(o[e]) + bf_lo(rv[e]), bf_hi(o[e]) + bf_hi(rv[e]));
+        const float h0 = bf_lo(o[e]), h1 = bf_hi(o[e]);
+        ss += h0 * h0 + h1 * h1;
+      }
+      if (ep.ss_out) {  // a 32-column group = four consecutive lanes (q = 4j .. 4j + 3 of row m)
+        ss = live ? ss : 0.f;
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        if (live && (q & 3) == 0) ep.ss_out[(int64_t)(mb0 + m) * (N >> 5) + ((n0 >> 5) + (q >> 2))] = ss;
+      }
+    }
+    if (live) st16(out + (int64_t)m * ldo + n, o);
   }
 }
 
@@ -332,7 +424,7 @@ extern "C" int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t 
   auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
             : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
   hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, st, (const uint16_t *)x, ldx, (const uint16_t *)w, ldw,
-                     (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used, 0);
+                     (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used, 0, GmEpi{});
   return (int)hipGetLastError();
 }
 
@@ -360,6 +452,62 @@ extern "C" int a8_gemm_silu_small(const void *x, int64_t ldx, const void *w13, i
   auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
             : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
   hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, (hipStream_t)stream, (const uint16_t *)x, ldx,
-                     (const uint16_t *)w13, ldw, (uint16_t *)out, ldo, nullptr, nullptr, M, 2 * I, K, nch, 1, I);
+                     (const uint16_t *)w13, ldw, (uint16_t *)out, ldo, nullptr, nullptr, M, 2 * I, K, nch, 1, I,
+                     GmEpi{});
+  return (int)hipGetLastError();
+}
+
+extern "C" int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo,
+                                  void *ws, int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, int gated,
+                                  int res_add, float *ss_out, const float *ss_in, int ss_n, float eps, void *stream) {
+  using namespace a8;
+  if (M < 0 || N < 0 || K < 0 || splits < 1 || mblocks < 1 || ss_n < 0)
+    return set_error(A8_EINVAL, "gemm_small_norm: bad sizes M=%d N=%d K=%d splits=%d mblocks=%d", M, N, K, splits,
+                     mblocks);
+  if (M == 0 || N == 0) return 0;
+  const int I = gated ? N / 2 : 0;  // gated: w = [gate; up] (N = 2 I rows), out [M, I]
+  if (M > kGmMaxM || K == 0 || K % kGmKC || N % 8 || (gated && (N % 16 || splits != 1 || res_add)))
+    return set_error(A8_EUNSUP, "gemm_small_norm: M=%d N=%d K=%d (gated %d, splits %d, res_add %d) outside M <= %d, "
+                     "K a multiple of %d, N of 8 (16 gated; gated: one split, no residual)", M, N, K, gated, splits,
+                     res_add, kGmMaxM, kGmKC);
+  if (ss_out && (!res_add || N % 32))
+    return set_error(A8_EUNSUP, "gemm_small_norm: sums of squares need res_add and N a multiple of 32 (N=%d)", N);
+  if (ss_in && (ss_n < 1 || ss_n > kGmSsMax || ss_n % 4))
+    return set_error(A8_EUNSUP, "gemm_small_norm: %d partial sums per row (1..%d, a multiple of 4)", ss_n, kGmSsMax);
+  if (res_add && ss_in)
+    return set_error(A8_EUNSUP, "gemm_small_norm: a product both adds the residual and consumes a norm");
+  const int ldo_need = gated ? I : N;
+  if (!x || !w || !out) return set_error(A8_EINVAL, "gemm_small_norm: null pointer");
+  if (!al16g(x) || !al16g(w) || !al16g(out) || (ss_in && !al16g(ss_in)) || (ldx | ldw | ldo) & 7 || ldx < K ||
+      ldw < K || ldo < ldo_need)
+    return set_error(A8_EALIGN, "gemm_small_norm: pointers must be 16-byte aligned, leading dims multiples of 8 and "
+                     ">= the row length");
+  if ((int64_t)(M - 1) * ldx * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32) ||
+      (int64_t)(N - 1) * ldw * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32))
+    return set_error(A8_EUNSUP, "gemm_small_norm: operands span more than 4 GiB");
+  const int nch = K / kGmKC;
+  const int S = gated ? 1 : std::min(splits, nch);
+  const int cps = (nch + S - 1) / S;
+  const int S_used = (nch + cps - 1) / cps;
+  if (S_used > 1 && (!ws || ws_bytes < kGmCntBytes + (int64_t)S_used * M * N * 4 || !al16g(ws)))
+    return set_error(A8_EWSPACE, "gemm_small_norm: %d splits need a 16-byte aligned workspace of %lld bytes", S_used,
+                     (long long)(kGmCntBytes + (int64_t)S_used * M * N * 4));
+  if (S_used > 1 && (int64_t)S_used * M * N * 4 >= ((int64_t)1 << 32))
+    return set_error(A8_EUNSUP, "gemm_small_norm: %d splits of %d x %d partials span more than 4 GiB", S_used, M, N);
+  const int MT = std::min(12, ((((M + mblocks - 1) / mblocks) + 31) / 32) * 2);
+  const int nmb = (M + MT * 16 - 1) / (MT * 16);
+  const int ntile = gated ? (I + 31) / 32 : (N + kGmNB - 1) / kGmNB;
+  if (S_used > 1 && (int64_t)ntile * nmb > kGmCntBytes / 4)
+    return set_error(A8_EUNSUP, "gemm_small_norm: %d x %d tiles exceed the %d counters for k splits", ntile, nmb,
+                     kGmCntBytes / 4);
+  int32_t *cnt = S_used > 1 ? (int32_t *)ws : nullptr;
+  float *part = S_used > 1 ? (float *)((char *)ws + kGmCntBytes) : nullptr;
+  const dim3 grid((unsigned)ntile, (unsigned)S_used, (unsigned)nmb);
+  const bool w8 = MT % 4 == 0;
+  auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
+            : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
+  const GmEpi ep{res_add ? 1 : 0, ss_out, ss_in, ss_n, eps};
+  hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, (hipStream_t)stream, (const uint16_t *)x, ldx,
+                     (const uint16_t *)w, ldw, (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used, I, ep);
   return (int)hipGetLastError();
 }

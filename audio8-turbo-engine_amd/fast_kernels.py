@@ -559,6 +559,48 @@ def gemm_silu_small(x, w13, out=None, mblocks=1):
     return y
 
 
+def gemm_small_norm(x, w, out, splits=1, mblocks=1, ws=None, gated=False, res_add=False, ss_out=None, ss_in=None,
+                    eps=1e-6):
+    """The slow-AR projections with the residual RMSNorm between them folded in (a8_gemm_small_norm; the
+    reference runs rmsnorm, fast_kernels.py:30-69, as its own launch between the products):
+      res_add: out is the residual stream, updated in place: out = bf16(bf16(x @ w^T) + out) -- the product
+        rounded to bf16 and rmsnorm's residual add, the same bits; ss_out (fp32 [M, N / 32], optional) gets the
+        new stream's sums of squares per 32-column group, the next norm's statistic;
+      ss_in: x is a raw residual stream h and w a weight with the norm's weight folded in (fold_norm): out =
+        bf16((h @ w^T) * rsqrt(sum(ss_in[m]) / K + eps)) -- the norm's 1 / rms applied to the fp32 products
+        (the reference rounds h * (1 / rms) and its product with the norm weight to bf16 first: within bf16
+        rounding noise of it); with gated, w = [gate; up] and out = silu_mul of the two (gemm_silu_small's
+        epilogue).
+    M <= 192, K a multiple of 64, N of 8 (32 with ss_out, 16 gated); splits / ws / mblocks as gemm_small."""
+    _check_bf16("x", x, 2)
+    _check_bf16("w", w, 2)
+    M, K = x.shape
+    N = w.shape[0]
+    _need(w.shape[1] == K, f"w shape {tuple(w.shape)} does not match K = {K}")
+    _check_bf16("out", out, 2)
+    _need(out.shape[0] == M and out.shape[1] == (N // 2 if gated else N), f"out shape {tuple(out.shape)} mismatch")
+    for name, t in (("ss_out", ss_out), ("ss_in", ss_in)):
+        if t is not None:
+            _need(t.dtype == torch.float32 and t.dim() == 2 and t.is_contiguous() and t.shape[0] >= M,
+                  f"{name} must be a contiguous float32 [>= M, groups] tensor")
+    if ss_out is not None:
+        _need(ss_out.shape[1] == N // 32, f"ss_out must have N / 32 = {N // 32} columns")
+    _check_device(x=x, w=w, out=out, ws=ws, ss_out=ss_out, ss_in=ss_in)
+    st = _lib.load().a8_gemm_small_norm(
+        x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
+        ws.data_ptr() if ws is not None else None, ws.numel() * ws.element_size() if ws is not None else 0,
+        M, N, K, int(splits), int(mblocks), int(bool(gated)), int(bool(res_add)),
+        ss_out.data_ptr() if ss_out is not None else None, ss_in.data_ptr() if ss_in is not None else None,
+        ss_in.shape[1] if ss_in is not None else 0, float(eps), _lib.stream_of(x))
+    _lib.check(st, "gemm_small_norm")
+    return out
+
+
+def fold_norm(w, norm_w):
+    """w [N, K] with the norm weight [K] folded in, for gemm_small_norm(ss_in=...): bf16(w * norm_w)."""
+    return (w.float() * norm_w.float()[None, :]).to(w.dtype).contiguous()
+
+
 class GemmDispatch:
     """Per-(M, N, K) choice between the library GEMM (torch.matmul -> hipBLASLt) and gemm_small, measured on
     the running GPU at startup, outside graph capture (the reference's GemmDispatch, fast_kernels.py:413-519,
@@ -572,6 +614,7 @@ class GemmDispatch:
 
     def __init__(self):
         self.small = {}     # (M, N, K) -> (splits, mblocks) or None (library GEMM)
+        self.small_best = {}  # (M, N, K) -> the fastest gemm_small (splits, mblocks), chosen or not
         self.enabled = True
         self.ws = None
         self.log = []
@@ -622,6 +665,7 @@ class GemmDispatch:
                 n = max(20, len(ws_))
                 best, best_t = None, self._time([lambda w=w: torch.matmul(x, w.t(), out=y) for w in ws_], n)
                 lib_t = best_t
+                small_t = None
                 for sp in self.SPLITS:
                     if sp > K // 64:
                         continue
@@ -632,9 +676,12 @@ class GemmDispatch:
                         t = self._time([lambda w=w: gemm_small(x, w, y, splits=sp, ws=wsp, mblocks=mb) for w in ws_], n)
                         if t < best_t:
                             best, best_t = (sp, mb), t
+                        if small_t is None or t < small_t:
+                            self.small_best[(M, N, K)], small_t = (sp, mb), t
                 self.small[(M, N, K)] = best
-                if best is not None and best[0] > 1:
-                    need = max(need, gemm_ws_bytes(M, N, best[0]))
+                sb = self.small_best.get((M, N, K))
+                if sb is not None and sb[0] > 1:  # the norm-fused products run gemm_small whatever was chosen
+                    need = max(need, gemm_ws_bytes(M, N, sb[0]))
                 self.log.append(((M, N, K), lib_t, best, best_t))
                 if log:
                     log(f"[gemm] M={M} N={N} K={K}: library {lib_t * 1e3:.1f} us, "
@@ -660,6 +707,29 @@ class GemmDispatch:
         if best is not None and best[0] == 1 and x.stride(1) == 1:
             return gemm_silu_small(x, w13, mblocks=best[1])
         return silu_mul(self(x, w13))
+
+    def _shape(self, M, N, K, gated):
+        """(splits, mblocks) of gemm_small for a norm-fused product (which only gemm_small computes): the
+        fastest gemm_small shape tune measured, else one pass over K with row blocks of about 32 rows for narrow
+        N; gated: one pass."""
+        best = self.small_best.get((M, N, K))
+        if best is not None and (not gated or best[0] == 1):
+            return best
+        return 1, (1 if N >= 4096 else max(1, M // 32))
+
+    def residual(self, x, w, res, ss_out=None):
+        """res += x @ w^T in place (the product rounded to bf16, then the residual add: rmsnorm's residual
+        step), with the new stream's per-row sums of squares into ss_out ([M, N / 32] fp32)."""
+        sp, mb = self._shape(x.shape[0], w.shape[0], w.shape[1], False)
+        return gemm_small_norm(x, w, res, splits=sp, mblocks=mb, ws=self.ws if sp > 1 else None, res_add=True,
+                               ss_out=ss_out)
+
+    def normed(self, h, wf, ss_in, eps, out, gated=False):
+        """The product of RMSNorm(h) with a weight whose norm weight is folded in (fold_norm), the norm's
+        statistic from the producer's ss_out; gated: silu_mul of the [gate; up] halves."""
+        sp, mb = self._shape(h.shape[0], wf.shape[0], wf.shape[1], gated)
+        return gemm_small_norm(h, wf, out, splits=sp, mblocks=mb, ws=self.ws if sp > 1 else None, gated=gated,
+                               ss_in=ss_in, eps=eps)
 
 
 _F16 = torch.float16

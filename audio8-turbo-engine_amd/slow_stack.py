@@ -17,7 +17,7 @@ from __future__ import annotations
 import torch
 
 from .attn_stack import AttnStack
-from .fast_kernels import rmsnorm, silu_mul
+from .fast_kernels import GemmDispatch, fold_norm, rmsnorm, silu_mul
 
 
 def random_weights(n_layers, hidden, nq, nkv, hd, inter, dev, seed=0, dt=torch.bfloat16):
@@ -46,6 +46,9 @@ class SlowStack:
     updated in place), as in the reference. fuse=True lets the store and the decode share one launch where
     every row attends its own slot (AttnStack.forward)."""
 
+    # token rows up to which a norm-fused step applies (gemm_small_norm's M limit)
+    FUSE_NORM_ROWS = 192
+
     def __init__(self, layers, norm, nq, nkv, hd, eps, rope_base, max_rows, cache_rows, cache_len, max_pos, dev,
                  nsplit_max=16, ring=None, mm=None):
         self.layers = layers
@@ -58,9 +61,52 @@ class SlowStack:
         # the projections' GEMM: the reference's `mm` argument (fast_engine.py:90) -- torch.matmul by default, or
         # a GemmDispatch (this package's small-M kernel where it measured faster)
         self.mm = mm if mm is not None else (lambda x, w: torch.matmul(x, w.t()))
+        # fuse_norm: with a GemmDispatch as mm, decode steps of at most FUSE_NORM_ROWS rows run the residual
+        # RMSNorms inside the projections (gemm_small_norm): the o / w2 products add the residual in their epilogue
+        # and leave the next norm's sums of squares; the qkv / w13 products take that norm's 1 / rms on their fp32
+        # products, its weight folded into theirs -- two launches fewer per layer, within bf16 rounding noise of
+        # the reference's rmsnorm -> product sequence
+        self.fuse_norm = False
+        self._folded = None
+        self._ss = None
+
+    def _fused_ready(self, R, plan):
+        if not (self.fuse_norm and isinstance(self.mm, GemmDispatch) and plan is None and R <= self.FUSE_NORM_ROWS):
+            return False
+        hidden = self.norm.shape[0]
+        if self._folded is None:
+            self._folded = [(fold_norm(L["wqkv"], L["ln1"]), fold_norm(L["w13"], L["ln2"])) for L in self.layers]
+            dev = self.norm.device
+            self._ss = [torch.zeros(self.FUSE_NORM_ROWS, hidden // 32, dtype=torch.float32, device=dev) for _ in range(2)]
+        return True
+
+    def _forward_fused(self, x, pos, slot, lens, nsplit, rowmap, fuse):
+        """forward() with the residual RMSNorms inside the projections (see fuse_norm)."""
+        R = x.shape[0]
+        mm = self.mm
+        h = rmsnorm(x, self.layers[0]["ln1"], self.eps)
+        res = x
+        q = torch.empty(R, self.nq, self.hd, dtype=x.dtype, device=x.device)
+        o = torch.empty_like(q)
+        ss_a, ss_b = self._ss[0][:R], self._ss[1][:R]
+        for i, L in enumerate(self.layers):
+            wqkv_f, w13_f = self._folded[i]
+            if i == 0:
+                qkv = mm(h, L["wqkv"])
+            else:  # RMSNorm(res, ln1) folded in, its statistic from the previous layer's w2 product
+                qkv = mm.normed(res, wqkv_f, ss_b, self.eps, torch.empty(R, wqkv_f.shape[0], dtype=x.dtype,
+                                                                          device=x.device))
+            self.attn.layer(i, qkv, L["bqkv"], pos, slot, lens, q, o, nsplit=nsplit, rowmap=rowmap, fuse=fuse)
+            mm.residual(o.view(R, -1), L["wo"], res, ss_a)          # res += o @ wo^T
+            act = mm.normed(res, w13_f, ss_a, self.eps, torch.empty(R, w13_f.shape[0] // 2, dtype=x.dtype,
+                                                                    device=x.device), gated=True)
+            mm.residual(act, L["w2"], res, ss_b)                    # res += act @ w2^T
+        return rmsnorm(res, self.norm, self.eps)
 
     def forward(self, x, pos, slot, lens, nsplit=1, rowmap=True, plan=None, fuse=False):
         R = x.shape[0]
+        if self._fused_ready(R, plan):
+            return self._forward_fused(x, pos, slot, lens, nsplit, rowmap, fuse)
         nl = len(self.layers)
         h = rmsnorm(x, self.layers[0]["ln1"], self.eps)
         res = x

@@ -266,19 +266,31 @@ def per_config(a8, torch, dev, steps):
     st.mm = mm
     xbuf.copy_(x0)
     g = capture(torch, lambda: st.forward(xbuf, pos, slot, lens_d, rowmap=False, fuse=True))
+    us_dispatch = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
+    del g
+    # the same step with the residual RMSNorms inside the projections (SlowStack.fuse_norm: gemm_small_norm,
+    # two launches fewer per layer)
+    st.fuse_norm = True
+    xbuf.copy_(x0)
+    g = capture(torch, lambda: st.forward(xbuf, pos, slot, lens_d, rowmap=False, fuse=True))
     us2 = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
     res["slow_ar_step"] = {
         "us_per_step": round(us2, 1), "us_per_layer": round(us2 / layers, 2), "rows": b, "kv_len": S,
         "hidden": hidden, "inter": inter, "weight_bytes": wbytes,
         "choices": {f"{N}x{K}": (None if c is None else {"splits": c[0], "mblocks": c[1]})
                     for (M, N, K), c in mm.small.items()},
+        "gemm_small_shapes": {f"{N}x{K}": {"splits": c[0], "mblocks": c[1]} for (M, N, K), c in mm.small_best.items()},
         "tune_us": {f"{N}x{K}": [round(lt * 1e3, 2), None if bt is None else round(bt * 1e3, 2)]
                     for (M, N, K), lt, _, bt in mm.log},
         "library": lib_step,
-        "note": "the full slow-AR decode step around the attention path (fused store + decode, rmsnorm, the four "
-                "projections, SiLU-mul); synthetic weights; projections through GemmDispatch (hipBLASLt or "
-                "gemm_small per shape, timed at startup on the layers' weights; w13 with SiLU-mul in its "
-                "epilogue where gemm_small takes it); tune_us = [library, chosen] per call"}
+        "norms_separate": {"us_per_step": round(us_dispatch, 1), "us_per_layer": round(us_dispatch / layers, 2),
+                           "note": "GemmDispatch per shape (hipBLASLt or gemm_small), rmsnorm as its own launch"},
+        "note": "the full slow-AR decode step around the attention path (fused store + decode, the four "
+                "projections, the residual RMSNorms, SiLU-mul); synthetic weights; projections on gemm_small "
+                "(its fastest shape per weight, timed at startup on the layers' weights) with the norms inside "
+                "them (SlowStack.fuse_norm: the o / w2 products add the residual and leave the norm's sums of "
+                "squares, the qkv / w13 products apply it, w13 with SiLU-mul in its epilogue); tune_us = "
+                "[library, chosen] per call"}
     del g, st, wts, xbuf, mm
     torch.cuda.empty_cache()
 
@@ -480,7 +492,8 @@ def vocoder_probe(a8, torch, dev):
 
 def slow_probe(a8, torch, dev):
     """Profile target for the slow-AR step's projections: the 24-layer step at 192 rows x KV 2048 (synthetic
-    weights, as the slow_ar_step leg) with GemmDispatch tuned first, then 3 steps replayed from a graph."""
+    weights, as the slow_ar_step leg) with GemmDispatch tuned first and the norms inside the projections, then 3 steps
+    replayed from a graph."""
     from importlib import import_module
     ss = import_module(a8.__name__ + ".slow_stack")
     b, S, layers, hidden, inter = 192, 2048, LAYERS, 896, 4864
@@ -490,6 +503,7 @@ def slow_probe(a8, torch, dev):
     mm = a8.GemmDispatch()
     mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b])
     st.mm = mm
+    st.fuse_norm = True
     gen = torch.Generator(device=dev).manual_seed(5)
     x = torch.randn(b, hidden, generator=gen, device=dev).to(torch.bfloat16)
     lens_d = torch.full((b,), S, dtype=torch.int32, device=dev)

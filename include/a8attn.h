@@ -352,6 +352,22 @@ int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t ldw, void *
  */
 int a8_gemm_silu_small(const void *x, int64_t ldx, const void *w13, int64_t ldw, void *out, int64_t ldo, int M, int I,
                        int K, int mblocks, void *stream);
+/*
+ * The projections with the slow-AR layer's residual RMSNorm folded into them, so that the norm takes no launch of
+ * its own (the reference runs rmsnorm, serve/fast_kernels.py:30-69, between its GEMMs, serve/fast_engine.py:131-137;
+ * no counterpart entry point in the reference). Shapes, splits, ws and mblocks as a8_gemm_small; gated != 0: w =
+ * [gate; up] (N = 2I rows), out [M, I] with a8_gemm_silu_small's epilogue (one split, N a multiple of 16).
+ *   res_add != 0: out [M, N] is the residual stream, updated in place: out = bf16(f32(bf16(x . w^T)) + f32(out))
+ *     -- the product rounded as a8_gemm_small's, then rmsnorm's residual add, the same bits. ss_out (optional,
+ *     N a multiple of 32): fp32 [M][N / 32], the sums of squares of the new stream per 32-column group.
+ *   ss_in (optional; not with res_add): x is a raw residual stream h and w carries the norm weight (w[n][k] =
+ *     bf16(w[n][k] norm_w[k])); the fp32 products are scaled by rsqrt(sum_{j < ss_n} ss_in[m][j] / K + eps)
+ *     before the rounding (ss_n a multiple of 4, <= 32; ss_in 16-byte aligned, row stride ss_n): the RMSNorm's
+ *     1 / rms without the reference's two intermediate bf16 roundings, within their rounding noise.
+ */
+int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo, void *ws,
+                       int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, int gated, int res_add,
+                       float *ss_out, const float *ss_in, int ss_n, float eps, void *stream);
 
 /*
  * The streaming vocoder's channels-last convolutions (the codec decoder's default conv path,

@@ -1,0 +1,157 @@
+"""The norm-fused projections (gemm_small_norm) and the slow stack that uses them (SlowStack.fuse_norm), on the
+GPU through the C ABI: the residual add bit for bit against gemm_small's rounded product plus torch's bf16 add,
+its per-row sums of squares against torch; the RMSNorm consumer (the norm weight folded into the weight, the
+norm's 1 / rms on the fp32 products) against a float64 evaluation, plain and with the gated SiLU epilogue; the
+fused 24-layer-shaped step against the oracle's _Stack.forward restatement, and its graph replays against the
+eager step."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import randn_bf16
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def lref():
+    from oracle import layer_ref
+    return layer_ref
+
+
+def _ulps(a, b):
+    return (a.view(torch.int16).int() - b.view(torch.int16).int()).abs()
+
+
+@pytest.mark.parametrize("M,N,K,splits,mblocks", [(192, 896, 896, 1, 6), (192, 896, 4864, 4, 3), (64, 896, 896, 1, 1),
+                                                  (192, 896, 4864, 1, 1), (40, 256, 512, 2, 1)])
+def test_residual_add_and_sums_of_squares(a8, dev, M, N, K, splits, mblocks):
+    say(f"case: gemm_small_norm res_add M={M} N={N} K={K} splits={splits} mblocks={mblocks}")
+    g = torch.Generator().manual_seed(M + N + K)
+    x = randn_bf16(g, M, K).to(dev)
+    w = (randn_bf16(g, N, K) * (K ** -0.5)).to(BF).to(dev)
+    res0 = randn_bf16(g, M, N).to(dev)
+    ws = torch.zeros(a8.gemm_ws_bytes(M, N, splits), dtype=torch.uint8, device=dev) if splits > 1 else None
+    a = a8.gemm_small(x, w, splits=splits, ws=ws, mblocks=mblocks)
+    want = (a.float() + res0.float()).to(BF)
+    res = res0.clone()
+    ss = torch.full((M, N // 32), -1.0, dtype=torch.float32, device=dev)
+    for rep in range(2):  # the workspace counters are left at zero: a second call is the same
+        res.copy_(res0)
+        a8.gemm_small_norm(x, w, res, splits=splits, mblocks=mblocks, ws=ws, res_add=True, ss_out=ss)
+        torch.cuda.synchronize()
+        assert torch.equal(res, want), (rep, _ulps(res, want).max().item())
+    ss_want = (want.float() ** 2).view(M, N // 32, 32).sum(-1)
+    assert torch.allclose(ss, ss_want, rtol=1e-5, atol=1e-5), (ss - ss_want).abs().max().item()
+
+
+@pytest.mark.parametrize("M,N,K,splits,mblocks,gated", [(192, 1152, 896, 1, 6, False), (192, 9728, 896, 1, 1, True),
+                                                        (64, 1152, 896, 3, 1, False), (33, 256, 512, 1, 1, True)])
+def test_norm_consumer_against_float64(a8, lref, dev, M, N, K, splits, mblocks, gated):
+    """out = bf16(h @ fold_norm(w, ln)^T * rsqrt(mean(h^2) + eps)), the statistic from 32-column sums of
+    squares as a producer leaves them; within 2 bf16 ulps of float64 (the gated one: of silu_mul of the two
+    float64 halves rounded to bf16, within one more ulp where the halves' roundings differ)."""
+    say(f"case: gemm_small_norm consumer M={M} N={N} K={K} splits={splits} mblocks={mblocks} gated={gated}")
+    g = torch.Generator().manual_seed(7 * M + N)
+    h = (randn_bf16(g, M, K) * 3).to(BF)
+    w = (randn_bf16(g, N, K) * (K ** -0.5)).to(BF)
+    ln = (1 + 0.05 * torch.randn(K, generator=g)).to(BF)
+    eps = 1e-6
+    wf = a8.fold_norm(w, ln)
+    ss = (h.float() ** 2).view(M, K // 32, 32).sum(-1).contiguous()
+    inv = torch.rsqrt((h.double() ** 2).mean(-1, keepdim=True) + eps)
+    prod = (h.double() @ wf.double().t()) * inv
+    ws = torch.zeros(a8.gemm_ws_bytes(M, N, splits), dtype=torch.uint8, device=dev) if splits > 1 else None
+    out = torch.empty(M, N // 2 if gated else N, dtype=BF, device=dev)
+    a8.gemm_small_norm(h.to(dev), wf.to(dev), out, splits=splits, mblocks=mblocks, ws=ws, gated=gated,
+                       ss_in=ss.to(dev), eps=eps)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    # the bar of gemm_small's own tests: 2 bf16 ulps of the value plus 1e-3 of the largest (fp32 sums cancel
+    # on near-zero outputs); gated: of silu_mul over the float64 halves rounded to bf16, one ulp more
+    want = lref.silu_mul(prod.to(BF)).double() if gated else prod
+    bar = 3 if gated else 2
+    err = (got.double() - want).abs()
+    tol = bar * 2.0 ** -8 * want.abs() + 1e-3 * want.abs().max()
+    u = _ulps(got, want.to(BF))
+    say(f"  max ulps {u.max().item()}, exact {(u == 0).float().mean().item():.4f}, worst err / tol "
+        f"{(err / tol).max().item():.3f}")
+    assert (err <= tol).all()
+
+
+def test_slow_stack_fused_norm(a8, ref, lref, dev):
+    """The decode tick with fuse_norm (every projection on gemm_small, the norms inside them) at the slow AR's
+    widths and 192 rows against the oracle, with the same bar as the unfused stack, and its graph replays
+    against the eager step bit for bit."""
+    import importlib
+    tl = importlib.import_module("test_gpu_layer")
+    say("case: slow stack, norm-fused projections, 192 rows")
+    n_layers, hidden, inter, b, S = 3, 896, 4864, 192, 256
+    st, layers, norm = tl._stack(a8, dev, n_layers, hidden, inter, b, S, seed=23)
+    mm = a8.GemmDispatch()
+    mm.tune([L[k] for L in layers for k in ("wqkv", "wo", "w13", "w2")], [b])
+    st.mm = mm
+    st.fuse_norm = True
+    g = torch.Generator().manual_seed(24)
+    x = randn_bf16(g, b, hidden)
+    lens = torch.randint(1, S + 1, (b,), generator=g).int()
+    pos, slot = lens - 1, torch.arange(b, dtype=torch.int32)
+    kc0 = [t.clone() for t in st.kc]
+    vc0 = [t.clone() for t in st.vc]
+    kc = [t.cpu() for t in st.kc]
+    vc = [t.cpu() for t in st.vc]
+    want = lref.slow_stack(x.clone(), pos, slot, lens, tl._cpu(layers), norm.cpu(), tl.NQ, tl.NKV, tl.HD, 1e-6,
+                           st.attn.cos.cpu(), st.attn.sin.cpu(), kc, vc, rowmap=False)
+    xd, posd, slotd, lensd = x.to(dev), pos.to(dev), slot.to(dev), lens.to(dev)
+    # the same step unfused (the reference's rmsnorm -> product sequence, bit for bit but for GEMM summation
+    # order): its distance to the oracle is the rounding noise the fused step is held to
+    st.fuse_norm = False
+    ref_step = st.forward(xd.clone(), posd, slotd, lensd, rowmap=False, fuse=True).clone()
+    for i in range(n_layers):
+        st.kc[i].copy_(kc0[i])
+        st.vc[i].copy_(vc0[i])
+    st.fuse_norm = True
+    got = st.forward(xd.clone(), posd, slotd, lensd, rowmap=False, fuse=True).clone()
+    torch.cuda.synchronize()
+    emax, emean, vmax = tl._close(got, want)
+    umax, umean, _ = tl._close(ref_step, want)
+    say(f"  fused: max-abs {emax:.3e} mean-abs {emean:.3e}; unfused: max-abs {umax:.3e} mean-abs {umean:.3e} "
+        f"(max |h| {vmax:.2f}); choices {mm.small}")
+    # the unfused stack's bar for the largest error; the mean error within 2x the unfused step's: the fused step
+    # rounds at other points (the folded weight instead of each norm's two bf16 outputs), perturbations of the
+    # same size that add to the unfused step's GEMM-order noise (about sqrt(2) x expected)
+    assert emax <= 0.02 * vmax and emean <= max(5e-3, 2.0 * umean)
+    for i in range(n_layers):
+        dk = (st.kc[i].cpu().float() - kc[i].float()).abs().max().item()
+        assert dk <= 0.05, dk
+    xbuf = torch.empty_like(xd)
+
+    def step():
+        return st.forward(xbuf, posd, slotd, lensd, rowmap=False, fuse=True)
+
+    for i in range(n_layers):
+        st.kc[i].copy_(kc0[i])
+        st.vc[i].copy_(vc0[i])
+    xbuf.copy_(xd)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        yg = step()
+    for rep in range(3):
+        for i in range(n_layers):
+            st.kc[i].copy_(kc0[i])
+            st.vc[i].copy_(vc0[i])
+        xbuf.copy_(xd)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, got), f"replay {rep} differs from the eager step"
