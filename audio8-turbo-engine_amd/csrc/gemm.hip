@@ -71,6 +71,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
                                                            int Mall, int N, int K, int cps, int S, int I, GmEpi ep) {
   static_assert(NW == 4 || NW == 8, "waves");
   static_assert(MT >= 2 && MT * 16 <= kGmMaxM && (2 * MT) % NW == 0, "token subtiles");
+  warm_kernargs<120>();  // the explicit arguments above span 0x00-0x77
   constexpr int XB = MT * 16 * 128;        // X bytes per ring slot (token rows x 128 bytes)
   constexpr int WB = kGmNB * 128;          // W bytes per ring slot
   constexpr int DX = 2 * MT / NW;          // X requests per wave per chunk (2 MT of 1 KB)
