@@ -50,9 +50,11 @@ SIGNATURES = {
                         _I, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
     "a8_conv_cl_ws_bytes": (_L, [_I, _I, _I, _I, _I, _I]),
     "a8_snake_cat": (_I, [_P, _L, _L, _P, _L, _L, _P, _P, _P, _L, _L, _I, _I, _I, _I, _P]),
+    "a8_snake_cat_refresh": (_I, [_P, _L, _L, _P, _L, _L, _P, _P, _P, _L, _L, _I, _I, _I, _I, _P]),
     "a8_decode_attn_f32q": (_I, [_P, _L, _L, _P, _P, _L, _L, _L, _I, _I, _P, _P, _P, _L, _L, _I, _I, _I, _I, _I,
                                  _F, _P]),
     "a8_gemm_silu_small": (_I, [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
+    "a8_conv_out_tanh": (_I, [_P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
     "a8_gemm_small_norm": (_I, [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P]),
     "a8_ru_cl": (_I, [_P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _P, _L, _L, _I, _I, _I, _I, _I, _I,
                       _P]),

@@ -56,8 +56,11 @@ __device__ __forceinline__ float sin_hw(float x) {
   return __builtin_amdgcn_sinf(r);
 }
 __device__ __forceinline__ u32x2 ld8(const void *p) { return *reinterpret_cast<const u32x2 *>(p); }
-// the snake x + ib sin(a x)^2 on 8 channels (fp32, one rounding to fp16)
+// the snake x + ib sin(a x)^2 on 8 channels (fp32, one rounding to fp16). No contraction: left free, the compiler
+// fuses the last add and the fp16 conversion into one v_fma_mix at some call sites and not at others (one
+// rounding against two), and the same row would get different bits in snake_cat, the conv loads and the state.
 __device__ __forceinline__ u32x4 snake8(u32x4 v, const float *a, const float *ib) {
+#pragma clang fp contract(off)
   u32x4 o;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -371,35 +374,117 @@ __global__ __launch_bounds__(256) void k_conv_fin(const float *__restrict__ part
   }
 }
 
-template <bool SNAKE>
+template <bool SNAKE, bool REFRESH>
 __global__ __launch_bounds__(256) void k_snake_cat(const uint16_t *__restrict__ x, int64_t s_xb, int64_t s_xt,
-                                                   const uint16_t *__restrict__ st, int64_t s_sb, int64_t s_st,
+                                                   uint16_t *st, int64_t s_sb, int64_t s_st,
                                                    const float *__restrict__ sa, const float *__restrict__ sib,
                                                    uint16_t *__restrict__ y, int64_t s_yb, int64_t s_yt, int B,
                                                    int T, int CTX, int C) {
   warm_kernargs<104>();  // the explicit arguments above span 0x00-0x67
-  const int nch = C >> 3, rows = CTX + T;
+  const int nch = C >> 3;
+  // REFRESH (T >= CTX): one item per x row j; item j < CTX also moves state row j into y and writes the new
+  // state row j (y's row T + j = snake(x[T - CTX + j])) after reading the old one -- the only reader of that row
+  const int rows = REFRESH ? T : CTX + T;
   const uint32_t id = blockIdx.x * 256u + threadIdx.x;
   if (id >= (uint32_t)B * (uint32_t)rows * (uint32_t)nch) return;
   const int c = (int)(id % (uint32_t)nch);
   const uint32_t rt = id / (uint32_t)nch;
   const int tt = (int)(rt % (uint32_t)rows), b = (int)(rt / (uint32_t)rows);
-  u32x4 v;
-  if (tt < CTX) {
-    v = ld16(st + (int64_t)b * s_sb + (int64_t)tt * s_st + 8 * c);
-  } else {
-    v = ld16(x + (int64_t)b * s_xb + (int64_t)(tt - CTX) * s_xt + 8 * c);
-    if (SNAKE) {
-      float a[8], ib[8];
+  float a[8], ib[8];
+  if (SNAKE) {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        a[q] = sa[8 * c + q];
-        ib[q] = sib[8 * c + q];
-      }
-      v = snake8(v, a, ib);
+    for (int q = 0; q < 8; ++q) {
+      a[q] = sa[8 * c + q];
+      ib[q] = sib[8 * c + q];
     }
   }
+  auto act = [&](int j) {
+    u32x4 v = ld16(x + (int64_t)b * s_xb + (int64_t)j * s_xt + 8 * c);
+    return SNAKE ? snake8(v, a, ib) : v;
+  };
+  if (REFRESH) {
+    st16(y + (int64_t)b * s_yb + (int64_t)(CTX + tt) * s_yt + 8 * c, act(tt));
+    if (tt < CTX) {
+      uint16_t *sp = st + (int64_t)b * s_sb + (int64_t)tt * s_st + 8 * c;
+      const u32x4 old = ld16(sp);
+      st16(y + (int64_t)b * s_yb + (int64_t)tt * s_yt + 8 * c, old);
+      st16(sp, act(T - CTX + tt));
+    }
+    return;
+  }
+  const u32x4 v = tt < CTX ? ld16(st + (int64_t)b * s_sb + (int64_t)tt * s_st + 8 * c) : act(tt - CTX);
   st16(y + (int64_t)b * s_yb + (int64_t)tt * s_yt + 8 * c, v);
+}
+
+// The decoder's last conv (one output channel) with everything around it (a8_conv_out_tanh): snake_cat's
+// [state | snake(x)], the causal conv of `taps` taps (dilation 1) into one channel with fp32 sums, the fp16
+// rounding conv_cl would store, then tanh in fp32 (serve/fast_engine.py:228-233 and 310: snake_cat, conv_cl,
+// the state refresh, y[..., 0].float().tanh()). Workgroup (b, tb) computes outputs t = 256 tb .. + 255 of row
+// b from the activated rows t .. t + taps - 1 of [state | snake(x)] staged in LDS; workgroup (b, 0), the only
+// one reading row b's old state, also writes the new state (the last CTX activated rows, T >= CTX) after its
+// staging has read the old one. A dot product per output: the implicit GEMM pads the one column to 16.
+constexpr int kCoT = 256;        // outputs per workgroup
+constexpr int kCoMaxCin = 128;   // input channels (the decoder's last block has 96)
+constexpr int kCoMaxTaps = 8;
+constexpr int kCoPitch = kCoMaxCin + 8;  // LDS row pitch (elements): consecutive rows start 4 banks apart
+
+__global__ __launch_bounds__(256) void k_conv_out(const uint16_t *__restrict__ x, int64_t s_xb, int64_t s_xt,
+                                                  uint16_t *st, int64_t s_sb, int64_t s_st,
+                                                  const float *__restrict__ sa, const float *__restrict__ sib,
+                                                  const uint16_t *__restrict__ w, const uint16_t *__restrict__ bias,
+                                                  float *__restrict__ y, int64_t s_yb, int T, int CTX, int Cin,
+                                                  int taps) {
+  warm_kernargs<104>();  // the explicit arguments above span 0x00-0x67
+  __shared__ __attribute__((aligned(16))) uint16_t xs[(kCoT + kCoMaxTaps) * kCoPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t ws[kCoMaxTaps * kCoMaxCin];
+  __shared__ float a_s[kCoMaxCin], ib_s[kCoMaxCin];
+  const int nt = (T + kCoT - 1) / kCoT;
+  const int b = blockIdx.x / nt, tb = blockIdx.x - b * nt;
+  const int t0 = tb * kCoT, tid = threadIdx.x;
+  const int nch = Cin >> 3;
+  for (int i = tid; i < taps * nch; i += 256) st16(ws + 8 * i, ld16(w + 8 * i));
+  for (int i = tid; i < Cin; i += 256) {
+    a_s[i] = sa[i];
+    ib_s[i] = sib[i];
+  }
+  __syncthreads();
+  // rows q = t0 .. t0 + kCoT + taps - 2 of [state | snake(x)] (q < CTX: the state's row q, else x's row q - CTX)
+  const int nrow = min(kCoT, T - t0) + taps - 1;
+  const uint16_t *xb = x + (int64_t)b * s_xb;
+  uint16_t *sb = st + (int64_t)b * s_sb;
+  for (int i = tid; i < nrow * nch; i += 256) {
+    const int r = i / nch, c = i - r * nch, q = t0 + r;
+    u32x4 v;
+    if (q < CTX) {
+      v = ld16(sb + (int64_t)q * s_st + 8 * c);
+    } else {
+      v = snake8(ld16(xb + (int64_t)(q - CTX) * s_xt + 8 * c), a_s + 8 * c, ib_s + 8 * c);
+    }
+    st16(xs + r * kCoPitch + 8 * c, v);
+  }
+  __syncthreads();
+  if (tb == 0) {  // the new state: the last CTX activated rows (this workgroup has read the old state above)
+    for (int i = tid; i < CTX * nch; i += 256) {
+      const int r = i / nch, c = i - r * nch;
+      st16(sb + (int64_t)r * s_st + 8 * c,
+           snake8(ld16(xb + (int64_t)(T - CTX + r) * s_xt + 8 * c), a_s + 8 * c, ib_s + 8 * c));
+    }
+  }
+  const int t = t0 + tid;
+  if (t >= T) return;
+  float acc = 0.f;
+  for (int j = 0; j < taps; ++j) {
+    const uint16_t *xr = xs + (tid + j) * kCoPitch;
+    const uint16_t *wr = ws + j * Cin;
+    for (int c = 0; c < nch; ++c) {
+      const u32x4 xv = ld16(xr + 8 * c), wv = ld16(wr + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = __builtin_fmaf(h_hi(xv[e]), h_hi(wv[e]), __builtin_fmaf(h_lo(xv[e]), h_lo(wv[e]), acc));
+    }
+  }
+  acc += bias ? h_lo((uint32_t)bias[0]) : 0.f;
+  const float yh = h_lo(pack_f16x2(acc, 0.f));  // the fp16 conv output
+  y[(int64_t)b * s_yb + t] = tanhf(yh);
 }
 
 static inline bool al16(const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
@@ -643,26 +728,61 @@ extern "C" int a8_ru_cl(const void *xin, int64_t s_xb, int64_t s_xt, const void 
   return (int)hipGetLastError();
 }
 
+static int snake_cat_entry(const char *fn, const void *x, int64_t s_xb, int64_t s_xt, const void *state, int64_t s_sb,
+                           int64_t s_st, const float *a, const float *ib, void *y, int64_t s_yb, int64_t s_yt, int B,
+                           int T, int CTX, int C, bool refresh, void *stream) {
+  using namespace a8;
+  if (B < 0 || T < 0 || CTX < 0 || C <= 0) return set_error(A8_EINVAL, "%s: bad sizes B=%d T=%d CTX=%d C=%d", fn, B, T, CTX, C);
+  if (C % 8) return set_error(A8_EUNSUP, "%s: C %d not a multiple of 8", fn, C);
+  if (refresh && T < CTX)
+    return set_error(A8_EUNSUP, "%s: the state refresh needs T >= CTX (T %d, CTX %d)", fn, T, CTX);
+  if (B == 0 || T + CTX == 0) return 0;
+  if ((T > 0 && !x) || (CTX > 0 && !state) || !y || (a != nullptr) != (ib != nullptr))
+    return set_error(A8_EINVAL, "%s: null pointer", fn);
+  if ((x && !al16(x)) || (state && !al16(state)) || !al16(y) || (a && (!al16(a) || !al16(ib))) ||
+      (s_xb | s_xt | s_sb | s_st | s_yb | s_yt) & 7)
+    return set_error(A8_EALIGN, "%s: pointers 16-byte aligned, strides multiples of 8", fn);
+  const int64_t n = (int64_t)B * (refresh ? T : CTX + T) * (C / 8);
+  if (n >= (int64_t)1 << 31) return set_error(A8_EUNSUP, "%s: too large", fn);
+  const unsigned grid = (unsigned)((n + 255) / 256);
+  auto kern = a ? (refresh ? k_snake_cat<true, true> : k_snake_cat<true, false>)
+                : (refresh ? k_snake_cat<false, true> : k_snake_cat<false, false>);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x, s_xb, s_xt,
+                     (uint16_t *)const_cast<void *>(state), s_sb, s_st, a, ib, (uint16_t *)y, s_yb, s_yt, B, T, CTX, C);
+  return (int)hipGetLastError();
+}
+
 extern "C" int a8_snake_cat(const void *x, int64_t s_xb, int64_t s_xt, const void *state, int64_t s_sb, int64_t s_st,
                             const float *a, const float *ib, void *y, int64_t s_yb, int64_t s_yt, int B, int T, int CTX,
                             int C, void *stream) {
+  return snake_cat_entry("snake_cat", x, s_xb, s_xt, state, s_sb, s_st, a, ib, y, s_yb, s_yt, B, T, CTX, C, false,
+                         stream);
+}
+
+extern "C" int a8_snake_cat_refresh(const void *x, int64_t s_xb, int64_t s_xt, void *state, int64_t s_sb, int64_t s_st,
+                                    const float *a, const float *ib, void *y, int64_t s_yb, int64_t s_yt, int B, int T,
+                                    int CTX, int C, void *stream) {
+  return snake_cat_entry("snake_cat_refresh", x, s_xb, s_xt, state, s_sb, s_st, a, ib, y, s_yb, s_yt, B, T, CTX, C,
+                         true, stream);
+}
+
+extern "C" int a8_conv_out_tanh(const void *x, int64_t s_xb, int64_t s_xt, void *state, int64_t s_sb, int64_t s_st,
+                                const float *a, const float *ib, const void *w, const void *bias, float *y, int64_t s_yb,
+                                int B, int T, int CTX, int Cin, int taps, void *stream) {
   using namespace a8;
-  if (B < 0 || T < 0 || CTX < 0 || C <= 0) return set_error(A8_EINVAL, "snake_cat: bad sizes B=%d T=%d CTX=%d C=%d", B, T, CTX, C);
-  if (C % 8) return set_error(A8_EUNSUP, "snake_cat: C %d not a multiple of 8", C);
-  if (B == 0 || T + CTX == 0) return 0;
-  if ((T > 0 && !x) || (CTX > 0 && !state) || !y || (a != nullptr) != (ib != nullptr))
-    return set_error(A8_EINVAL, "snake_cat: null pointer");
-  if ((x && !al16(x)) || (state && !al16(state)) || !al16(y) || (a && (!al16(a) || !al16(ib))) ||
-      (s_xb | s_xt | s_sb | s_st | s_yb | s_yt) & 7)
-    return set_error(A8_EALIGN, "snake_cat: pointers 16-byte aligned, strides multiples of 8");
-  const int64_t n = (int64_t)B * (CTX + T) * (C / 8);
-  if (n >= (int64_t)1 << 31) return set_error(A8_EUNSUP, "snake_cat: too large");
-  const unsigned grid = (unsigned)((n + 255) / 256);
-  if (a)
-    hipLaunchKernelGGL(k_snake_cat<true>, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x, s_xb, s_xt,
-                       (const uint16_t *)state, s_sb, s_st, a, ib, (uint16_t *)y, s_yb, s_yt, B, T, CTX, C);
-  else
-    hipLaunchKernelGGL(k_snake_cat<false>, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x, s_xb,
-                       s_xt, (const uint16_t *)state, s_sb, s_st, a, ib, (uint16_t *)y, s_yb, s_yt, B, T, CTX, C);
+  if (B < 0 || T < 0 || CTX < 0 || Cin <= 0 || taps <= 0)
+    return set_error(A8_EINVAL, "conv_out_tanh: bad sizes B=%d T=%d CTX=%d Cin=%d taps=%d", B, T, CTX, Cin, taps);
+  if (Cin % 8 || Cin > kCoMaxCin || taps > kCoMaxTaps || CTX != taps - 1 || T < CTX)
+    return set_error(A8_EUNSUP, "conv_out_tanh: Cin %d (a multiple of 8 up to %d), taps %d (up to %d), context %d (taps - 1), "
+                     "T %d >= context", Cin, kCoMaxCin, taps, kCoMaxTaps, CTX, T);
+  if (B == 0 || T == 0) return 0;
+  if (!x || (CTX > 0 && !state) || !a || !ib || !w || !y) return set_error(A8_EINVAL, "conv_out_tanh: null pointer");
+  if (!al16(x) || (state && !al16(state)) || !al16(a) || !al16(ib) || !al16(w) || (s_xb | s_xt | s_sb | s_st) & 7)
+    return set_error(A8_EALIGN, "conv_out_tanh: pointers 16-byte aligned, strides multiples of 8");
+  const int64_t grid = (int64_t)B * ((T + kCoT - 1) / kCoT);
+  if (grid >= (int64_t)1 << 31) return set_error(A8_EUNSUP, "conv_out_tanh: too large");
+  hipLaunchKernelGGL(k_conv_out, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, (const uint16_t *)x, s_xb, s_xt,
+                     (uint16_t *)state, s_sb, s_st, a, ib, (const uint16_t *)w, (const uint16_t *)bias, y, s_yb, T, CTX,
+                     Cin, taps);
   return (int)hipGetLastError();
 }

@@ -813,9 +813,38 @@ def conv_cl_ws_bytes(B, TR, Cin, Cout, taps, ph):
     return int(_lib.load().a8_conv_cl_ws_bytes(B, TR, Cin, Cout, taps, ph))
 
 
-def snake_cat(x, state, a, ib, out):
+def conv_out_tanh(x, state, a, ib, w, bias, out):
+    """The decoder's last conv with what surrounds it, in one launch (a8_conv_out_tanh): out[b, t] =
+    tanh(fp16(bias + sum_j [state | snake(x)][b, t + j] . w[j])) in fp32, and state <- the last CTX rows of
+    [state | snake(x)] (serve/fast_engine.py:228-233 and 310: snake_cat, conv_cl into one channel, the state
+    refresh, y[..., 0].float().tanh()). x [B, T, Cin] raw fp16; state [>=B, CTX, Cin] activated, CTX = taps - 1
+    <= T; a / ib fp32 [Cin]; w [taps, Cin] fp16 (the one output channel); bias fp16 [1] or None; out [B, T] fp32
+    (row stride free). Cin a multiple of 8 up to 128, taps up to 8."""
+    _need(isinstance(x, torch.Tensor) and x.dim() == 3 and x.stride(-1) == 1 and x.dtype == _F16,
+          "x must be float16 [B, T, Cin], last dim contiguous")
+    B, T, Cin = x.shape
+    taps = w.shape[0]
+    _need(w.dtype == _F16 and w.dim() == 2 and w.shape[1] == Cin and w.is_contiguous(), "w must be float16 [taps, Cin]")
+    _need(state is not None and state.dtype == _F16 and state.shape[0] >= B and state.shape[1] == taps - 1 and
+          state.shape[2] == Cin and state.stride(-1) == 1, "state must be float16 [>=B, taps - 1, Cin]")
+    _need(out.dtype == torch.float32 and out.dim() == 2 and out.shape[0] == B and out.shape[1] == T and
+          out.stride(-1) == 1, "out must be float32 [B, T]")
+    _need(a.dtype == torch.float32 and ib.dtype == torch.float32 and a.is_contiguous() and ib.is_contiguous(),
+          "a / ib must be contiguous float32 vectors")
+    _check_device(x=x, state=state, w=w, out=out, a=a, ib=ib, bias=bias)
+    st = _lib.load().a8_conv_out_tanh(
+        x.data_ptr(), x.stride(0), x.stride(1), state.data_ptr(), state.stride(0), state.stride(1), a.data_ptr(),
+        ib.data_ptr(), w.data_ptr(), bias.data_ptr() if bias is not None else None, out.data_ptr(), out.stride(0),
+        B, T, state.shape[1], Cin, taps, _lib.stream_of(x))
+    _lib.check(st, "conv_out_tanh")
+    return out
+
+
+def snake_cat(x, state, a, ib, out, refresh=False):
     """x [B, T, C] (raw) and state [>=B, CTX, C] (activated context, or None) -> out [B, CTX+T, C] =
-    concat(state, snake(x)) along time (fast_kernels.py:718-729, kernel 695-715); a / ib None: no snake."""
+    concat(state, snake(x)) along time (fast_kernels.py:718-729, kernel 695-715); a / ib None: no snake.
+    refresh=True (T >= CTX) also writes the next context into state, state[:B] = out[:, T:], in the same
+    launch (a8_snake_cat_refresh; the reference copies it after the conv, fast_engine.py:232)."""
     _need(isinstance(x, torch.Tensor) and x.dim() == 3 and x.stride(-1) == 1, "x must be [B, T, C], last dim contiguous")
     B, T, C = x.shape
     CTX = state.shape[1] if state is not None else 0
@@ -829,7 +858,10 @@ def snake_cat(x, state, a, ib, out):
               and a.numel() >= C and ib.numel() >= C, "a / ib must be contiguous float32 [C] vectors")
     _need(x.dtype == _F16, "x must be float16", TypeError)
     _check_device(x=x, state=state, out=out, a=a, ib=ib)
-    st = _lib.load().a8_snake_cat(
+    if refresh:
+        _need(state is not None and T >= CTX, "refresh needs a state and T >= CTX")
+    fn = _lib.load().a8_snake_cat_refresh if refresh else _lib.load().a8_snake_cat
+    st = fn(
         x.data_ptr(), x.stride(0), x.stride(1), state.data_ptr() if state is not None else None,
         state.stride(0) if state is not None else 0, state.stride(1) if state is not None else 0,
         a.data_ptr() if a is not None else None, ib.data_ptr() if ib is not None else None, out.data_ptr(),

@@ -24,7 +24,7 @@ from __future__ import annotations
 
 import torch
 
-from .fast_kernels import conv_cl, conv_cl_ws_bytes, ru_cl, snake_cat
+from .fast_kernels import conv_cl, conv_cl_ws_bytes, conv_out_tanh, ru_cl, snake_cat
 
 F16 = torch.float16
 
@@ -89,9 +89,11 @@ class CLConv:
                     ws=self.ws)
             return y
         xin = torch.empty(b, self.ctx + T, self.Cin, dtype=F16, device=x.device)
-        snake_cat(x, self.state[:b], self.a, self.ib, xin)
+        refresh = T >= self.ctx  # the next context written by snake_cat itself (no copy after the conv)
+        snake_cat(x, self.state[:b], self.a, self.ib, xin, refresh=refresh)
         conv_cl(xin, self.W, self.bias, T, self.taps, self.dil, self.ph, y, res=res, ws=self.ws)
-        self.state[:b].copy_(xin[:, T:])
+        if not refresh:
+            self.state[:b].copy_(xin[:, T:])
         return y
 
 
@@ -119,10 +121,12 @@ class FusedRU:
         c1, c2 = self.c1, self.c2
         T = x.shape[1]
         xin = torch.empty(b, c1.ctx + T, c1.Cin, dtype=F16, device=x.device)
-        snake_cat(x, c1.state[:b], c1.a, c1.ib, xin)
+        refresh = T >= c1.ctx
+        snake_cat(x, c1.state[:b], c1.a, c1.ib, xin, refresh=refresh)
         y = torch.empty(b, T, c1.Cout, dtype=F16, device=x.device)
         ru_cl(xin, self.w1, c1.bias, c2.a, c2.ib, self.w2, c2.bias, x, y, T, c1.taps, c1.dil)
-        c1.state[:b].copy_(xin[:, T:])
+        if not refresh:
+            c1.state[:b].copy_(xin[:, T:])
         return y
 
 
@@ -182,6 +186,12 @@ class CLDecoder:
             self.blocks.append((tc, us))
         af, wf, bf = wts["final"]
         self.final = CLConv(wf, bf, Bmax, dev, S, alpha=af, tmax=t)
+        # fused_out: the last conv (one channel) as one launch with its snake_cat, state refresh and tanh
+        # (conv_out_tanh), where its shape allows; else snake_cat + conv_cl + the state copy + tanh
+        f = self.final
+        self.wout = f.W[0, :, :, 0].contiguous()  # [taps, Cin]: the one output channel's weights
+        self.fused_out = (f.Cout == 1 and f.ph == 1 and f.dil == 1 and f.state is not None and f.Cin % 8 == 0
+                          and f.Cin <= 128 and f.taps <= 8)
         self.up = 1
         for _, _, _, s, _ in wts["blocks"]:
             self.up *= s
@@ -198,4 +208,8 @@ class CLDecoder:
             x = tc(x, b)
             for c1, c2, fu in units:
                 x = fu(x, b) if fu is not None else c2(c1(x, b), b, res=x)
-        return self.final(x, b)[..., 0].float().tanh()
+        f = self.final
+        if self.fused_out and x.shape[1] >= f.ctx:
+            y = torch.empty(b, x.shape[1], dtype=torch.float32, device=x.device)
+            return conv_out_tanh(x.contiguous(), f.state[:b], f.a, f.ib, self.wout, f.bias, y)
+        return f(x, b)[..., 0].float().tanh()

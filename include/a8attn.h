@@ -393,6 +393,26 @@ int64_t a8_conv_cl_ws_bytes(int B, int TR, int Cin, int Cout, int taps, int ph);
 int a8_snake_cat(const void *x, int64_t s_xb, int64_t s_xt, const void *state, int64_t s_sb, int64_t s_st,
                  const float *a, const float *ib, void *y, int64_t s_yb, int64_t s_yt, int B, int T, int CTX, int C,
                  void *stream);
+/*
+ * a8_snake_cat that also writes the next context (no counterpart entry point in the reference, which copies
+ * it after the conv, serve/fast_engine.py:232): y as a8_snake_cat, and state[b] <- y[b, T .. T + CTX) in the same
+ * launch (each old state row is read, then rewritten, by the same thread). Needs T >= CTX (else A8_EUNSUP).
+ */
+int a8_snake_cat_refresh(const void *x, int64_t s_xb, int64_t s_xt, void *state, int64_t s_sb, int64_t s_st,
+                         const float *a, const float *ib, void *y, int64_t s_yb, int64_t s_yt, int B, int T, int CTX,
+                         int C, void *stream);
+/*
+ * The codec decoder's last conv with what surrounds it, in one launch (no counterpart entry point in the
+ * reference, which runs serve/fast_engine.py:228-233 -- snake_cat, conv_cl into one output channel, the state
+ * copy -- and then y[..., 0].float().tanh() at 310): y[b, t] = tanh(f32(fp16(bias[0] + sum_{j < taps} sum_k
+ * xin[b, t + j, k] w[j, k]))) with xin = [state[b] | snake(x[b])] (snake as a8_snake_cat's, fp32 sums), and
+ * state[b] <- xin[b, T .. T + CTX). x [B, T, Cin] fp16 (row strides s_xb, s_xt); state [>=B, CTX, Cin] fp16,
+ * activated, CTX = taps - 1 <= T; a / ib fp32 [Cin]; w [taps, Cin] fp16 contiguous; bias fp16 [1] or NULL;
+ * y [B, T] fp32, row stride s_yb. Cin a multiple of 8 up to 128, taps up to 8; else A8_EUNSUP.
+ */
+int a8_conv_out_tanh(const void *x, int64_t s_xb, int64_t s_xt, void *state, int64_t s_sb, int64_t s_st,
+                     const float *a, const float *ib, const void *w, const void *bias, float *y, int64_t s_yb,
+                     int B, int T, int CTX, int Cin, int taps, void *stream);
 
 /*
  * a8_ru_cl replaces serve/fast_kernels.py:679-692 (ru_fused, kernel 626-676; used by _FusedRU,

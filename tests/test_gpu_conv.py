@@ -184,3 +184,88 @@ def test_ru_cl_refuses_other_widths(a8, dev):
     v16, v32 = torch.zeros(C, dtype=F16, device=dev), torch.zeros(C, device=dev)
     with pytest.raises(RuntimeError, match="ru_cl"):
         a8.ru_cl(xin, w1, v16, v32, v32, w2, v16, xin, torch.empty(1, 4, C, dtype=F16, device=dev), 4, 7, 1)
+
+
+@pytest.mark.parametrize("B,T,C,taps", [(4, 2048, 96, 7), (3, 300, 96, 7), (2, 7, 32, 7), (5, 513, 128, 3)])
+def test_conv_out_tanh_against_the_call_it_replaces(a8, cref, dev, B, T, C, taps):
+    """conv_out_tanh (the decoder's last conv, one launch) against what it replaces, frame after frame: snake_cat,
+    conv_cl into one channel (padded weights), the state copy and tanh -- on the device (the state bit for bit,
+    the fp16 conv output within one ulp: another summation order; tanh of it within 2e-3) and the oracle."""
+    say(f"case: conv_out_tanh B={B} T={T} C={C} taps={taps}")
+    g = torch.Generator().manual_seed(B * T + C)
+    ctx = taps - 1
+    w = (torch.randn(taps, C, generator=g) / (taps * C) ** 0.5).to(F16)
+    W = torch.zeros(1, taps, C, 16, dtype=F16)
+    W[0, :, :, 0] = w
+    bias = torch.randn(1, generator=g).to(F16)
+    a = torch.rand(C, generator=g) + 0.5
+    ib = 1.0 / (a + 1e-9)
+    wd, Wd, bd, ad, ibd = w.to(dev), W.to(dev), bias.to(dev), a.to(dev), ib.to(dev)
+    st1 = torch.zeros(B, ctx, C, dtype=F16, device=dev)
+    st2 = st1.clone()
+    for rep in range(3):
+        x = (torch.randn(B, T, C, generator=g) * 2).to(F16).to(dev)
+        st_h = st2.cpu()
+        y = torch.empty(B, T, dtype=torch.float32, device=dev)
+        a8.conv_out_tanh(x, st1, ad, ibd, wd, bd, y)
+        xin = torch.empty(B, ctx + T, C, dtype=F16, device=dev)
+        a8.snake_cat(x, st2, ad, ibd, xin)
+        y16 = torch.empty(B, T, 1, dtype=F16, device=dev)
+        a8.conv_cl(xin, Wd, bd, T, taps, 1, 1, y16)
+        st2.copy_(xin[:, T:])
+        torch.cuda.synchronize()
+        assert torch.equal(st1, st2), rep                                      # the new state, bit for bit
+        want16 = cref.conv_cl(xin.cpu(), W, bias, T, taps, 1, 1, 1)[..., 0]    # the oracle on the same input
+        assert _close(torch.atanh(y.cpu().clamp(-0.9999, 0.9999)).to(F16).unsqueeze(-1), y16.cpu()) or \
+            (y.cpu() - torch.tanh(y16.cpu()[..., 0].float())).abs().max().item() <= 2e-3
+        assert (y.cpu() - torch.tanh(want16.float())).abs().max().item() <= 2e-3, rep
+        xin_h = cref.snake_cat(x.cpu(), st_h, a, ib)
+        want_h = torch.tanh(cref.conv_cl(xin_h, W, bias, T, taps, 1, 1, 1)[..., 0].float())
+        assert (y.cpu() - want_h).abs().max().item() <= 2e-3, rep
+
+
+def test_decoder_fused_output_conv(dev):
+    """The decoder with its last conv fused (the default) against the same decoder with snake_cat + conv_cl +
+    state copy + tanh: waveforms within 2e-3, every state bit for bit, over several frames."""
+    import importlib
+    voc = importlib.import_module("audio8-turbo-engine_amd.vocoder")
+    say("case: decoder, fused output conv vs the four-step call")
+    wd = voc.decoder_weights(dev=dev, seed=31)
+    d1, d2 = voc.CLDecoder(wd, 4, dev), voc.CLDecoder(wd, 4, dev)
+    d2.fused_out = False
+    assert d1.fused_out
+    g = torch.Generator(device=dev).manual_seed(32)
+    for rep in range(3):
+        x = torch.randn(4, 4, 1024, generator=g, device=dev).to(F16)
+        y1, y2 = d1(x, 4), d2(x, 4)
+        torch.cuda.synchronize()
+        assert (y1 - y2).abs().max().item() <= 2e-3, rep
+        for s1, s2 in zip(d1.states, d2.states):
+            assert torch.equal(s1, s2), rep
+
+
+@pytest.mark.parametrize("snake", [True, False])
+def test_snake_cat_refresh_equals_copy(a8, dev, snake):
+    """snake_cat(..., refresh=True) against snake_cat then the state copy the reference makes after the conv
+    (fast_engine.py:232): the concatenated rows and the next state bit for bit, frame after frame, including
+    frames exactly as long as the context."""
+    say(f"case: snake_cat refresh, snake {snake}")
+    g = torch.Generator().manual_seed(93)
+    B, C, ctx = 5, 96, 18
+    a = (torch.rand(C, generator=g) + 0.5).to(dev) if snake else None
+    ib = (1.0 / (a + 1e-9)) if snake else None
+    s1 = torch.randn(B, ctx, C, generator=g).to(F16).to(dev)
+    s2 = s1.clone()
+    for T in (18, 64, 19, 1024):
+        x = torch.randn(B, T, C, generator=g).to(F16).to(dev)
+        y1 = torch.empty(B, ctx + T, C, dtype=F16, device=dev)
+        y2 = torch.empty_like(y1)
+        a8.snake_cat(x, s1, a, ib, y1, refresh=True)
+        a8.snake_cat(x, s2, a, ib, y2)
+        s2.copy_(y2[:, T:])
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), T
+        assert torch.equal(s1, s2), T
+    with pytest.raises(Exception):  # shorter than the context: refused (the caller copies instead)
+        a8.snake_cat(torch.zeros(B, 4, C, dtype=F16, device=dev), s1, a, ib,
+                     torch.empty(B, ctx + 4, C, dtype=F16, device=dev), refresh=True)
