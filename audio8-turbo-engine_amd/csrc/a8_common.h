@@ -40,10 +40,18 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 // The gated MLP activation on two bf16 pairs (serve/fast_kernels.py:526-545, _silu_mul_kernel): the gate's
 // SiLU rounded to bf16 first (act(gate) in bf16, as the model's MLP), then times up, rounded again. Shared by
-// k_silu_mul and the w13 GEMM's gated epilogue, so the fused and separate paths give the same bits.
+// k_silu_mul and the w13 GEMM's gated epilogue, so the fused and separate paths give the same bits. The SiLU is
+// g * rcp(1 + 2^(-g log2 e)) on the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each; the
+// reference's tl.exp is an approximate exp as well): its result is rounded to bf16 at once, which these errors
+// move only where a value lies within ~2^-16 of a bf16 rounding boundary. Large negative g: 2^(...) = inf,
+// rcp(inf) = 0, g * 0 = -0, as g / inf. (A full-precision expf and an IEEE divide cost ~4x the VALU
+// instructions, about 1.8 us of the w13 epilogue at 192 x 4864.)
+__device__ __forceinline__ float silu_f32(float g) {
+  return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
+}
 __device__ __forceinline__ uint32_t silu_mul_bf16x2(uint32_t g2, uint32_t u2) {
   const float g0 = bf_lo(g2), g1 = bf_hi(g2);
-  const uint32_t gs = pack_bf16x2(g0 / (1.f + expf(-g0)), g1 / (1.f + expf(-g1)));
+  const uint32_t gs = pack_bf16x2(silu_f32(g0), silu_f32(g1));
   return pack_bf16x2(bf_lo(gs) * bf_lo(u2), bf_hi(gs) * bf_hi(u2));
 }
 
