@@ -620,9 +620,10 @@ class GemmDispatch:
         self.log = []
 
     @staticmethod
-    def _time(fns, n=20):
-        """Mean time of one call, from a graph of n calls cycling through `fns` (one per weight of the shape,
-        so that with a model's layers the weights are not all served from cache)."""
+    def _time(fns, n=20, reps=7):
+        """Time of one call, from a graph of n calls cycling through `fns` (one per weight of the shape, so that
+        with a model's layers the weights are not all served from cache): the median over `reps` timed replays
+        (one timed replay pair left the choice between shapes within ~1 us of each other to noise)."""
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -634,14 +635,16 @@ class GemmDispatch:
             for i in range(n):
                 fns[i % len(fns)]()
         g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
         g.replay()
-        g.replay()
-        e1.record()
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / (2 * n)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        ev[0].record()
+        for i in range(reps):
+            g.replay()
+            ev[i + 1].record()
+        torch.cuda.synchronize()
+        ts = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+        return ts[reps // 2] / n
 
     @staticmethod
     def applies(M, N, K):
