@@ -8,12 +8,14 @@
 // workgroup tile is all M rows x 64 weight rows, and K is split across workgroups only for narrow N.
 //
 // One workgroup = 64 weight rows (four 16-row n-subtiles) x all token rows (MT 16-row m-subtiles, MT even)
-// x a range of 64-wide k chunks. The chunk's X rows and W rows go from HBM / L2 into LDS by DMA (16-byte
-// pieces, row r's chunks permuted by chunk ^= r & 7 through the source offsets so the operand reads of
-// consecutive rows spread over the banks): the weights through a ring of 8 slots with 7 chunks in flight (they
-// come from HBM: ~1.5 us away), the token rows through a ring of 3 with 2 in flight (L2). Wave w computes
-// n-subtiles 2(w&1), 2(w&1)+1 x m-subtiles (w>>1) MT/2.. : per 32-k step two W operands and MT/2 X operands from
-// LDS, MT MFMAs (v_mfma_f32_16x16x32_bf16: A = W rows, B = X^T, so the C layout holds 4 consecutive output
+// x a range of KC-wide k chunks (KC = 128 for token tiles of up to 64 rows where K allows, else 64: each wait
+// and meeting then covers twice the bytes, measured 0.2-1.3 us faster per product at the slow AR's shapes). The
+// chunk's X rows and W rows go from HBM / L2 into LDS by DMA (16-byte pieces, row r's KC / 8 pieces permuted by
+// piece ^= r mod KC / 8 through the source offsets so the operand reads of consecutive rows spread over the
+// banks): the weights through a ring of 8 slots with 7 chunks in flight at KC = 64 (5 and 4 at KC = 128, the
+// same bytes; they come from HBM: ~1.5 us away), the token rows through a ring of 3 with 2 in flight (L2).
+// Wave w computes n-subtiles 2(w&1), 2(w&1)+1 x m-subtiles (w>>1) MT/2.. : per 32-k step two W operands and
+// MT/2 X operands from LDS, MT MFMAs (v_mfma_f32_16x16x32_bf16: A = W rows, B = X^T, so the C layout holds 4 consecutive output
 // columns of one token row per lane). The DMA is inline asm the compiler does not track; the kernel waits for
 // it with vmcnt counts (every wave issues the same number of requests per chunk, and loads complete in order).
 // The token rows may also be split into row blocks (blockIdx.z), for more workgroups where N is narrow. With
@@ -29,8 +31,8 @@ namespace a8 {
 namespace {
 
 constexpr int kGmNB = 64;   // weight rows per workgroup
-constexpr int kGmKC = 64;   // k per chunk
-constexpr int kGmWSlots = 8;  // W ring slots: 7 chunks of weights in flight (HBM latency), X only 2 (L2)
+constexpr int kGmKC = 64;   // k granularity (the narrower chunk; K must be a multiple of it)
+constexpr int kGmWSlots = 8;  // W ring slots at 64-wide chunks: 7 chunks of weights in flight (HBM latency), X 2 (L2)
 constexpr int kGmMaxM = 192;
 constexpr int kGmCntBytes = 4096;  // k splits: the workspace starts with one 32-bit counter per tile (<= 1024)
 constexpr int kGmSsMax = 32;       // norm-fused products: partial sums of squares per row (N / 32 <= 32)
@@ -63,7 +65,7 @@ struct GmEpi {
   float eps;
 };
 
-template <int MT, int NW>
+template <int MT, int NW, int KC>
 __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__restrict__ x, int64_t ldx,
                                                            const uint16_t *__restrict__ w, int64_t ldw,
                                                            uint16_t *__restrict__ out, int64_t ldo,
@@ -72,12 +74,19 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
   static_assert(NW == 4 || NW == 8, "waves");
   static_assert(MT >= 2 && MT * 16 <= kGmMaxM && (2 * MT) % NW == 0, "token subtiles");
   warm_kernargs<120>();  // the explicit arguments above span 0x00-0x77
-  constexpr int XB = MT * 16 * 128;        // X bytes per ring slot (token rows x 128 bytes)
-  constexpr int WB = kGmNB * 128;          // W bytes per ring slot
-  constexpr int DX = 2 * MT / NW;          // X requests per wave per chunk (2 MT of 1 KB)
-  constexpr int DW = 8 / NW;               // W requests per wave per chunk (8 of 1 KB)
+  static_assert(KC == 64 || KC == 128, "k chunk");
+  constexpr int CPR = KC / 8;              // 16-byte pieces of a row's chunk
+  constexpr int RB = 2 * KC;               // bytes of a row's chunk
+  constexpr int RPI = 64 / CPR;            // rows per 1 KB request
+  constexpr int XB = MT * 16 * RB;         // X bytes per ring slot
+  constexpr int WB = kGmNB * RB;           // W bytes per ring slot
+  constexpr int DX = MT * 16 / RPI / NW;   // X requests per wave per chunk
+  constexpr int DW = kGmNB / RPI / NW;     // W requests per wave per chunk
+  constexpr int KS = KC / 32;              // 32-k MFMA steps per chunk
+  constexpr int WSL = KC == 64 ? kGmWSlots : 5;  // W ring slots (the same bytes in flight)
   constexpr int MH = 2 * MT / NW;          // m-subtiles per wave (waves: 2 along n x NW / 2 along m)
-  __shared__ __attribute__((aligned(16))) char lds[3 * XB + kGmWSlots * WB];
+  static_assert(DX * NW * RPI == MT * 16 && DW * NW * RPI == kGmNB, "requests");
+  __shared__ __attribute__((aligned(16))) char lds[3 * XB + WSL * WB];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int r16 = lane & 15, g = lane >> 4;
   const int nt = blockIdx.x, sp = blockIdx.y;
@@ -85,7 +94,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
   const int mb0 = (int)blockIdx.z * MT * 16, M = min(MT * 16, Mall - mb0);
   x += (int64_t)mb0 * ldx;
   out += (int64_t)mb0 * ldo;
-  const int nch = K / kGmKC;
+  const int nch = K / KC;
   const int c0 = sp * cps, c1 = min(c0 + cps, nch);
   if (c0 >= c1) return;  // (the host sizes the grid so that this does not happen)
   const int n0 = nt * kGmNB;
@@ -104,35 +113,35 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
   u32x4 xr0 = xr, wr0 = wr;
   xr0[2] = 0u;
   wr0[2] = 0u;
-  const uint32_t prow = (uint32_t)(lane >> 3), pch = (uint32_t)(lane & 7);
+  const uint32_t prow = (uint32_t)lane / (uint32_t)CPR, pch = (uint32_t)lane % (uint32_t)CPR;
   uint32_t xso[DX], xdo[DX], wso[DW], wdo[DW];
   u32x4 wres[DW];
 #pragma unroll
   for (int j = 0; j < DX; ++j) {  // X instruction i = wv + NW j: token rows 8i..8i+7
-    const uint32_t i = (uint32_t)(wv + NW * j), row = 8u * i + prow;
-    xso[j] = row * (uint32_t)(ldx * 2) + ((pch ^ (row & 7u)) << 4);
+    const uint32_t i = (uint32_t)(wv + NW * j), row = (uint32_t)RPI * i + prow;
+    xso[j] = row * (uint32_t)(ldx * 2) + ((pch ^ (row & (uint32_t)(CPR - 1))) << 4);
     xdo[j] = i * 1024u;
   }
 #pragma unroll
   for (int j = 0; j < DW; ++j) {  // W instruction i = wv + NW j: weight rows 8i..8i+7 of the tile
-    const uint32_t i = (uint32_t)(wv + NW * j), row = 8u * i + prow;
-    const bool up = gated && i >= 4u;  // (wave-uniform) the up half of a gated tile, from its own source
+    const uint32_t i = (uint32_t)(wv + NW * j), row = (uint32_t)RPI * i + prow;
+    const bool up = gated && i >= (uint32_t)(32 / RPI);  // (wave-uniform) the up half of a gated tile, from its own source
     wres[j] = up ? wu : wr;
     const uint32_t srow = up ? row - 32u : row;
-    wso[j] = srow * (uint32_t)(ldw * 2) + ((pch ^ (row & 7u)) << 4);
+    wso[j] = srow * (uint32_t)(ldw * 2) + ((pch ^ (row & (uint32_t)(CPR - 1))) << 4);
     wdo[j] = i * 1024u;
   }
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>(lds);
   const uint32_t wring = lds0 + 3u * XB;
   auto issue_x = [&](int c, int slot) __attribute__((always_inline)) {
     const u32x4 rs = c < c1 ? xr : xr0;
-    const uint32_t kb = (uint32_t)(c * kGmKC * 2);
+    const uint32_t kb = (uint32_t)(c * KC * 2);
 #pragma unroll
     for (int j = 0; j < DX; ++j) gm_dma(rs, lds0 + (uint32_t)(slot * XB) + xdo[j], xso[j] + kb);
   };
   auto issue_w = [&](int c) __attribute__((always_inline)) {
-    const uint32_t kb = (uint32_t)(c * kGmKC * 2);
-    const uint32_t slot = (uint32_t)(c - c0) % (uint32_t)kGmWSlots;
+    const uint32_t kb = (uint32_t)(c * KC * 2);
+    const uint32_t slot = (uint32_t)(c - c0) % (uint32_t)WSL;
 #pragma unroll
     for (int j = 0; j < DW; ++j) gm_dma(c < c1 ? wres[j] : wr0, wring + slot * WB + wdo[j], wso[j] + kb);
   };
@@ -171,7 +180,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
 
   // W chunks c0 .. c0 + P - 1 (P = kGmWSlots - 1 in flight), then X chunks c0, c0 + 1; per chunk c: the wait,
   // the meeting (everyone is done with chunk c - 1, whose slots the next requests refill), X(c + 2), W(c + P)
-  constexpr int P = kGmWSlots - 1;
+  constexpr int P = WSL - 1;
 #pragma unroll
   for (int c = 0; c < P; ++c) issue_w(c0 + c);
   issue_x(c0, 0);
@@ -189,27 +198,27 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
     issue_x(c + 2, xs == 0 ? 2 : xs - 1);
     issue_w(c + P);
     const char *sx = lds + xs * XB;
-    const char *sw = lds + 3 * XB + ((c - c0) % kGmWSlots) * WB;
+    const char *sw = lds + 3 * XB + ((c - c0) % WSL) * WB;
     // every operand of the chunk is read before its first product: one LDS round trip per chunk, not one per
     // pair of products (the scheduler otherwise places each read just before its use)
-    u32x4 A[2][2], B[2][MH];
+    u32x4 A[KS][2], B[KS][MH];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < KS; ++s) {
       const uint32_t ch = (uint32_t)(4 * s + g);
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const uint32_t row = (uint32_t)(16 * (jn0 + a) + r16);
-        A[s][a] = ld16(sw + row * 128u + ((ch ^ (row & 7u)) << 4));
+        A[s][a] = ld16(sw + row * (uint32_t)RB + ((ch ^ (row & (uint32_t)(CPR - 1))) << 4));
       }
 #pragma unroll
       for (int b = 0; b < MH; ++b) {
         const uint32_t row = (uint32_t)(16 * (im0 + b) + r16);
-        B[s][b] = ld16(sx + row * 128u + ((ch ^ (row & 7u)) << 4));
+        B[s][b] = ld16(sx + row * (uint32_t)RB + ((ch ^ (row & (uint32_t)(CPR - 1))) << 4));
       }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int b = 0; b < MH; ++b)
 #pragma unroll
@@ -381,6 +390,17 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
 
 bool al16g(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// 128-wide k chunks where the token tile is small (MT <= 4: twice the bytes per wait and meeting, at the same
+// LDS bytes in flight) and K allows; else 64
+int gm_kc(int MT, int K) { return (MT <= 4 && K % 128 == 0) ? 128 : 64; }
+using GmKern = void (*)(const uint16_t *, int64_t, const uint16_t *, int64_t, uint16_t *, int64_t, float *, int32_t *,
+                        int, int, int, int, int, int, GmEpi);
+GmKern gm_kernel(int MT, int KC) {
+  if (KC == 128) return MT == 2 ? k_gemm_small<2, 4, 128> : k_gemm_small<4, 8, 128>;
+  return MT == 2 ? k_gemm_small<2, 4, 64> : MT == 4 ? k_gemm_small<4, 8, 64> : MT == 6 ? k_gemm_small<6, 4, 64>
+       : MT == 8 ? k_gemm_small<8, 8, 64> : MT == 10 ? k_gemm_small<10, 4, 64> : k_gemm_small<12, 8, 64>;
+}
+
 }  // namespace
 }  // namespace a8
 
@@ -400,7 +420,9 @@ extern "C" int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t 
   if ((int64_t)(M - 1) * ldx * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32) ||
       (int64_t)(N - 1) * ldw * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "gemm_small: operands span more than 4 GiB");
-  const int nch = K / kGmKC;
+  const int MT = std::min(12, ((((M + mblocks - 1) / mblocks) + 31) / 32) * 2);
+  const int KC = gm_kc(MT, K);
+  const int nch = K / KC;
   const int S = std::min(splits, nch);
   const int cps = (nch + S - 1) / S;
   const int S_used = (nch + cps - 1) / cps;  // every split has at least one chunk
@@ -409,8 +431,7 @@ extern "C" int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t 
                      (long long)(kGmCntBytes + (int64_t)S_used * M * N * 4));
   if (S_used > 1 && (int64_t)S_used * M * N * 4 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "gemm_small: %d splits of %d x %d partials span more than 4 GiB", S_used, M, N);
-  // rows per block: an even number of 16-row subtiles covering M / mblocks; blocks that would be empty are dropped
-  const int MT = std::min(12, ((((M + mblocks - 1) / mblocks) + 31) / 32) * 2);
+  // rows per block: an even number of 16-row subtiles covering M / mblocks (MT above); empty blocks are dropped
   const int nmb = (M + MT * 16 - 1) / (MT * 16);
   const int ntile = (N + kGmNB - 1) / kGmNB;
   if (S_used > 1 && (int64_t)ntile * nmb > kGmCntBytes / 4)
@@ -422,8 +443,7 @@ extern "C" int a8_gemm_small(const void *x, int64_t ldx, const void *w, int64_t 
   const hipStream_t st = (hipStream_t)stream;
   // 8 waves (two per SIMD, one covering the other's LDS round trips) where the token subtiles split four ways
   const bool w8 = MT % 4 == 0;
-  auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
-            : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
+  auto kern = gm_kernel(MT, KC);
   hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, st, (const uint16_t *)x, ldx, (const uint16_t *)w, ldw,
                      (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used, 0, GmEpi{});
   return (int)hipGetLastError();
@@ -445,13 +465,13 @@ extern "C" int a8_gemm_silu_small(const void *x, int64_t ldx, const void *w13, i
   if ((int64_t)(M - 1) * ldx * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32) ||
       (int64_t)(2 * I - 1) * ldw * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "gemm_silu_small: operands span more than 4 GiB");
-  const int nch = K / kGmKC;
   const int MT = std::min(12, ((((M + mblocks - 1) / mblocks) + 31) / 32) * 2);
+  const int KC = gm_kc(MT, K);
+  const int nch = K / KC;
   const int nmb = (M + MT * 16 - 1) / (MT * 16);
   const dim3 grid((unsigned)((I + 31) / 32), 1u, (unsigned)nmb);
   const bool w8 = MT % 4 == 0;
-  auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
-            : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
+  auto kern = gm_kernel(MT, KC);
   hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, (hipStream_t)stream, (const uint16_t *)x, ldx,
                      (const uint16_t *)w13, ldw, (uint16_t *)out, ldo, nullptr, nullptr, M, 2 * I, K, nch, 1, I,
                      GmEpi{});
@@ -486,7 +506,9 @@ extern "C" int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int
   if ((int64_t)(M - 1) * ldx * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32) ||
       (int64_t)(N - 1) * ldw * 2 + (int64_t)K * 2 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "gemm_small_norm: operands span more than 4 GiB");
-  const int nch = K / kGmKC;
+  const int MT = std::min(12, ((((M + mblocks - 1) / mblocks) + 31) / 32) * 2);
+  const int KC = gm_kc(MT, K);
+  const int nch = K / KC;
   const int S = gated ? 1 : std::min(splits, nch);
   const int cps = (nch + S - 1) / S;
   const int S_used = (nch + cps - 1) / cps;
@@ -495,7 +517,6 @@ extern "C" int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int
                      (long long)(kGmCntBytes + (int64_t)S_used * M * N * 4));
   if (S_used > 1 && (int64_t)S_used * M * N * 4 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "gemm_small_norm: %d splits of %d x %d partials span more than 4 GiB", S_used, M, N);
-  const int MT = std::min(12, ((((M + mblocks - 1) / mblocks) + 31) / 32) * 2);
   const int nmb = (M + MT * 16 - 1) / (MT * 16);
   const int ntile = gated ? (I + 31) / 32 : (N + kGmNB - 1) / kGmNB;
   if (S_used > 1 && (int64_t)ntile * nmb > kGmCntBytes / 4)
@@ -505,8 +526,7 @@ extern "C" int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int
   float *part = S_used > 1 ? (float *)((char *)ws + kGmCntBytes) : nullptr;
   const dim3 grid((unsigned)ntile, (unsigned)S_used, (unsigned)nmb);
   const bool w8 = MT % 4 == 0;
-  auto kern = MT == 2 ? k_gemm_small<2, 4> : MT == 4 ? k_gemm_small<4, 8> : MT == 6 ? k_gemm_small<6, 4>
-            : MT == 8 ? k_gemm_small<8, 8> : MT == 10 ? k_gemm_small<10, 4> : k_gemm_small<12, 8>;
+  auto kern = gm_kernel(MT, KC);
   const GmEpi ep{res_add ? 1 : 0, ss_out, ss_in, ss_n, eps};
   hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, (hipStream_t)stream, (const uint16_t *)x, ldx,
                      (const uint16_t *)w, ldw, (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used, I, ep);

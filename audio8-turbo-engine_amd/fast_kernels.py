@@ -615,6 +615,7 @@ class GemmDispatch:
     def __init__(self):
         self.small = {}     # (M, N, K) -> (splits, mblocks) or None (library GEMM)
         self.small_best = {}  # (M, N, K) -> the fastest gemm_small (splits, mblocks), chosen or not
+        self.gated_best = {}  # (M, N, K) -> the fastest gemm_silu_small (1, mblocks) for the gated weights
         self.enabled = True
         self.ws = None
         self.log = []
@@ -651,12 +652,18 @@ class GemmDispatch:
         return 0 < M <= 192 and K % 64 == 0 and N % 8 == 0
 
     @torch.inference_mode()
-    def tune(self, weights, Ms, log=None):
+    def tune(self, weights, Ms, log=None, gated=()):
         """weights: iterable of [N, K] bf16 tensors (a model's projections: the calls are timed cycling through
-        every weight of a shape, as the model's layers would); Ms: token counts."""
+        every weight of a shape, as the model's layers would); Ms: token counts. gated: those of the weights that
+        are [gate; up] products (w13): their shape is also timed through the launch that runs it with the
+        activation in its epilogue (gemm_silu_small), whose best row-block count `gated` and the norm-fused
+        products then take."""
         shapes = {}
         for w in weights:
             shapes.setdefault((w.shape[0], w.shape[1]), []).append(w)
+        gshapes = {}
+        for w in gated:
+            gshapes.setdefault((w.shape[0], w.shape[1]), []).append(w)
         need = 0
         for (N, K), ws_ in shapes.items():
             for M in sorted(set(int(m) for m in Ms)):
@@ -685,6 +692,17 @@ class GemmDispatch:
                 sb = self.small_best.get((M, N, K))
                 if sb is not None and sb[0] > 1:  # the norm-fused products run gemm_small whatever was chosen
                     need = max(need, gemm_ws_bytes(M, N, sb[0]))
+                if (N, K) in gshapes and N % 16 == 0:
+                    gws = gshapes[(N, K)]
+                    yg = torch.empty(M, N // 2, device=x.device, dtype=x.dtype)
+                    gt = None
+                    for mb in self.MBLOCKS:
+                        if mb > 1 and (M + mb - 1) // mb < 32:
+                            continue
+                        t = self._time([lambda w=w: gemm_silu_small(x, w, yg, mblocks=mb) for w in gws],
+                                       max(20, len(gws)))
+                        if gt is None or t < gt:
+                            self.gated_best[(M, N, K)], gt = (1, mb), t
                 self.log.append(((M, N, K), lib_t, best, best_t))
                 if log:
                     log(f"[gemm] M={M} N={N} K={K}: library {lib_t * 1e3:.1f} us, "
@@ -706,15 +724,18 @@ class GemmDispatch:
         """silu_mul(self(x, w13)): where the tuned choice for w13 is gemm_small in one pass (no k splits), the
         activation runs in its epilogue (gemm_silu_small, same bits, one launch and no [M, 2I] round trip);
         otherwise the product, then silu_mul."""
-        best = self.small.get((x.shape[0], w13.shape[0], w13.shape[1])) if self.enabled and x.dim() == 2 else None
+        key = (x.shape[0], w13.shape[0], w13.shape[1])
+        best = self.small.get(key) if self.enabled and x.dim() == 2 else None
         if best is not None and best[0] == 1 and x.stride(1) == 1:
-            return gemm_silu_small(x, w13, mblocks=best[1])
+            return gemm_silu_small(x, w13, mblocks=self.gated_best.get(key, best)[1])
         return silu_mul(self(x, w13))
 
     def _shape(self, M, N, K, gated):
         """(splits, mblocks) of gemm_small for a norm-fused product (which only gemm_small computes): the
-        fastest gemm_small shape tune measured, else one pass over K with row blocks of about 32 rows for narrow
-        N; gated: one pass."""
+        fastest gemm_small shape tune measured (gated: the fastest gated launch, where tune timed one), else one
+        pass over K with row blocks of about 32 rows for narrow N; gated: one pass."""
+        if gated and (M, N, K) in self.gated_best:
+            return self.gated_best[(M, N, K)]
         best = self.small_best.get((M, N, K))
         if best is not None and (not gated or best[0] == 1):
             return best

@@ -262,7 +262,7 @@ def per_config(a8, torch, dev, steps):
     # GEMM (gemm_small, with its split count and row blocks), whichever the timing at startup finds faster --
     # timed cycling through the 24 layers' weights, as the step reads them
     mm = a8.GemmDispatch()
-    mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b])
+    mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b], gated=[L["w13"] for L in wts])
     st.mm = mm
     xbuf.copy_(x0)
     g = capture(torch, lambda: st.forward(xbuf, pos, slot, lens_d, rowmap=False, fuse=True))
@@ -280,6 +280,7 @@ def per_config(a8, torch, dev, steps):
         "choices": {f"{N}x{K}": (None if c is None else {"splits": c[0], "mblocks": c[1]})
                     for (M, N, K), c in mm.small.items()},
         "gemm_small_shapes": {f"{N}x{K}": {"splits": c[0], "mblocks": c[1]} for (M, N, K), c in mm.small_best.items()},
+        "gated_shapes": {f"{N}x{K}": {"mblocks": c[1]} for (M, N, K), c in mm.gated_best.items()},
         "tune_us": {f"{N}x{K}": [round(lt * 1e3, 2), None if bt is None else round(bt * 1e3, 2)]
                     for (M, N, K), lt, _, bt in mm.log},
         "library": lib_step,
@@ -501,7 +502,7 @@ def slow_probe(a8, torch, dev):
     st = a8.SlowStack(wts, norm, NQ, NKV, HD, 1e-6, 10000.0, max_rows=max(16 * b, 8192), cache_rows=b + 1,
                       cache_len=S, max_pos=S, dev=dev)
     mm = a8.GemmDispatch()
-    mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b])
+    mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b], gated=[L["w13"] for L in wts])
     st.mm = mm
     st.fuse_norm = True
     gen = torch.Generator(device=dev).manual_seed(5)

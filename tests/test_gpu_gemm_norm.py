@@ -95,7 +95,7 @@ def test_slow_stack_fused_norm(a8, ref, lref, dev):
     n_layers, hidden, inter, b, S = 3, 896, 4864, 192, 256
     st, layers, norm = tl._stack(a8, dev, n_layers, hidden, inter, b, S, seed=23)
     mm = a8.GemmDispatch()
-    mm.tune([L[k] for L in layers for k in ("wqkv", "wo", "w13", "w2")], [b])
+    mm.tune([L[k] for L in layers for k in ("wqkv", "wo", "w13", "w2")], [b], gated=[L["w13"] for L in layers])
     st.mm = mm
     st.fuse_norm = True
     g = torch.Generator().manual_seed(24)

@@ -194,7 +194,7 @@ def test_slow_stack_with_gemm_dispatch(a8, ref, lref, dev):
     n_layers, hidden, inter, b, S = 2, 896, 4864, 192, 256
     st, layers, norm = _stack(a8, dev, n_layers, hidden, inter, b, S, seed=13)
     mm = a8.GemmDispatch()
-    mm.tune([L[k] for L in layers for k in ("wqkv", "wo", "w13", "w2")], [b])
+    mm.tune([L[k] for L in layers for k in ("wqkv", "wo", "w13", "w2")], [b], gated=[L["w13"] for L in layers])
     # every projection on gemm_small here, whatever the timing chose (the library path has its own test)
     for (M, N, K), c in list(mm.small.items()):
         mm.small[(M, N, K)] = c if c is not None else (1, 1)
