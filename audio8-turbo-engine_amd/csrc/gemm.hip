@@ -24,6 +24,7 @@
 // the same launch (no device-scope fence: that would write back and invalidate the whole XCD L2 under the
 // other workgroups' loads, measured 5-20x slower than the GEMM).
 #include <algorithm>
+#include <type_traits>
 
 #include "a8_common.h"
 
@@ -240,8 +241,10 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
 
   // lane (g, r16) of tile (a, b): token row 16(im0 + b) + r16, output columns n0 + 16(jn0 + a) + 4g..+3
   if (gated) {
-    // the up waves (odd: tile rows 32..63) park their values, rounded to bf16 as the GEMM's output would be,
-    // where the rings were; the gate waves (even, same token rows) finish: silu(gate) * up, rounded again
+    // a gate wave (even: tile rows 0..31) and the up wave beside it (odd: rows 32..63, same token rows) hold the
+    // two halves of the same output columns; each finishes one of its two 16-column subtiles -- the gate wave
+    // a = 0, the up wave a = 1 -- taking the other half's values (rounded to bf16, as the GEMM's output would
+    // be) from its partner through LDS where the rings were: silu(gate) * up, rounded again
     __syncthreads();  // every wave is done with the rings
     uint32_t *park = reinterpret_cast<uint32_t *>(lds) + (wv >> 1) * (2 * MH * 128);
     if (has_ss) {  // the consumed RMSNorm's 1 / rms, on the fp32 products of both halves
@@ -252,30 +255,38 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
         for (int a = 0; a < 2; ++a) acc[a][b] *= iv;
       }
     }
-    if (wv & 1) {
+    // (acc indexed by constants only: a subtile picked at run time makes the compiler keep acc in LDS, its
+    // stores then run inside the k loop)
+    auto park_half = [&](auto ap_tag) __attribute__((always_inline)) {
+      constexpr int ap = decltype(ap_tag)::value;  // the subtile handed to the partner: slot (ap, b)
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int b = 0; b < MH; ++b)
+        *reinterpret_cast<u32x2 *>(park + (ap * MH + b) * 128 + 2 * lane) =
+            u32x2{pack_bf16x2(acc[ap][b][0], acc[ap][b][1]), pack_bf16x2(acc[ap][b][2], acc[ap][b][3])};
+    };
+    auto finish_half = [&](auto a_tag) __attribute__((always_inline)) {
+      constexpr int a = decltype(a_tag)::value;  // the subtile this wave finishes (its partner parked slot (a, b))
+      const int n = 32 * nt + 16 * a + 4 * g;
 #pragma unroll
-        for (int b = 0; b < MH; ++b)
-          *reinterpret_cast<u32x2 *>(park + (a * MH + b) * 128 + 2 * lane) =
-              u32x2{pack_bf16x2(acc[a][b][0], acc[a][b][1]), pack_bf16x2(acc[a][b][2], acc[a][b][3])};
-    }
-    __syncthreads();
-    if (wv & 1) return;
-#pragma unroll
-    for (int b = 0; b < MH; ++b) {
-      const int m = 16 * (im0 + b) + r16;
-      if (m >= M) continue;
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const int n = 32 * nt + 16 * a + 4 * g;
-        if (n >= I) continue;
-        const u32x2 u2 = *reinterpret_cast<const u32x2 *>(park + (a * MH + b) * 128 + 2 * lane);
-        st8(out + (int64_t)m * ldo + n,
-            u32x2{silu_mul_bf16x2(pack_bf16x2(acc[a][b][0], acc[a][b][1]), u2[0]),
-                  silu_mul_bf16x2(pack_bf16x2(acc[a][b][2], acc[a][b][3]), u2[1])});
+      for (int b = 0; b < MH; ++b) {
+        const int m = 16 * (im0 + b) + r16;
+        if (m >= M || n >= I) continue;
+        const u32x2 mine{pack_bf16x2(acc[a][b][0], acc[a][b][1]), pack_bf16x2(acc[a][b][2], acc[a][b][3])};
+        const u32x2 other = *reinterpret_cast<const u32x2 *>(park + (a * MH + b) * 128 + 2 * lane);
+        const u32x2 gt = a == 0 ? mine : other, up = a == 0 ? other : mine;
+        st8(out + (int64_t)m * ldo + n, u32x2{silu_mul_bf16x2(gt[0], up[0]), silu_mul_bf16x2(gt[1], up[1])});
       }
-    }
+    };
+    const bool upw = wv & 1;  // wave-uniform
+    if (upw)
+      park_half(std::integral_constant<int, 0>{});
+    else
+      park_half(std::integral_constant<int, 1>{});
+    __syncthreads();
+    if (upw)
+      finish_half(std::integral_constant<int, 1>{});
+    else
+      finish_half(std::integral_constant<int, 0>{});
     return;
   }
   if (!part) {
