@@ -186,7 +186,8 @@ def test_ru_cl_refuses_other_widths(a8, dev):
         a8.ru_cl(xin, w1, v16, v32, v32, w2, v16, xin, torch.empty(1, 4, C, dtype=F16, device=dev), 4, 7, 1)
 
 
-@pytest.mark.parametrize("B,T,C,taps", [(4, 2048, 96, 7), (3, 300, 96, 7), (2, 7, 32, 7), (5, 513, 128, 3)])
+@pytest.mark.parametrize("B,T,C,taps", [(4, 2048, 96, 7), (3, 300, 96, 7), (2, 7, 32, 7), (5, 513, 128, 3),
+                                      (3, 200, 40, 8), (2, 129, 8, 1)])
 def test_conv_out_tanh_against_the_call_it_replaces(a8, cref, dev, B, T, C, taps):
     """conv_out_tanh (the decoder's last conv, one launch) against what it replaces, frame after frame: snake_cat,
     conv_cl into one channel (padded weights), the state copy and tanh -- on the device (the state bit for bit,
