@@ -56,6 +56,8 @@ SIGNATURES = {
     "a8_gemm_silu_small": (_I, [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P]),
     "a8_conv_out_tanh": (_I, [_P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P, _L, _I, _I, _I, _I, _I, _P]),
     "a8_gemm_small_norm": (_I, [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P]),
+    "a8_gemm_small_norm_pf": (_I, [_P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _F,
+                                   _P, _L, _P, _I, _P]),
     "a8_ru_cl": (_I, [_P, _L, _L, _P, _L, _L, _P, _P, _P, _P, _P, _P, _L, _L, _P, _L, _L, _I, _I, _I, _I, _I, _I,
                       _P]),
     "a8_prefix_copy": (_I, [_P, _P, _L, _L, _L, _P, _P, _L, _L, _L, _L, _P, _I, _I, _I, _I, _I, _I, _I, _P]),

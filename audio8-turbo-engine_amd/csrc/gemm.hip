@@ -58,12 +58,19 @@ __device__ __forceinline__ void gm_wait_vm() {
 //            (fp32 [Mall][N / 32]: the next RMSNorm's statistic, summed by its consumer);
 //   ss_in    the token rows are a raw residual stream h whose RMSNorm (weight folded into w by the caller) this
 //            product consumes: acc is scaled by rsqrt(sum_j ss_in[m][j] / K + eps) before the rounding.
+//   pf       workgroups z >= pf_z0 of the grid only read [pf, pf + pf_n16 16-byte pieces) once and end: the next
+//            product's weights into the memory-side cache while this product's own workgroups (fewer than the
+//            chip's compute units) leave the bandwidth idle; pf_sink takes a word in a case that never happens.
 struct GmEpi {
   int res_add;
   float *ss_out;
   const float *ss_in;
   int ss_n;
   float eps;
+  const u32x4 *pf;
+  int64_t pf_n16;
+  uint32_t *pf_sink;
+  int pf_z0;
 };
 
 template <int MT, int NW, int KC>
@@ -74,7 +81,22 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm_small(const uint16_t *__res
                                                            int Mall, int N, int K, int cps, int S, int I, GmEpi ep) {
   static_assert(NW == 4 || NW == 8, "waves");
   static_assert(MT >= 2 && MT * 16 <= kGmMaxM && (2 * MT) % NW == 0, "token subtiles");
-  warm_kernargs<120>();  // the explicit arguments above span 0x00-0x77
+  warm_kernargs<152>();  // the explicit arguments above span 0x00-0x97
+  if (ep.pf && (int)blockIdx.z >= ep.pf_z0) {  // a prefetch workgroup (uniform: no barrier below is reached)
+    const int64_t tpw = 64 * NW;
+    const int64_t id = ((int64_t)(blockIdx.z - ep.pf_z0) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * gridDim.y * (gridDim.z - ep.pf_z0) * tpw;
+    uint32_t acc = 0;
+    for (int64_t i = id * tpw + threadIdx.x; i < ep.pf_n16; i += 8 * stride) {
+      u32x4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = i + u * stride < ep.pf_n16 ? ep.pf[i + u * stride] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    if (acc == 0x9E3779B9u) ep.pf_sink[threadIdx.x & 3] = acc;
+    return;
+  }
   static_assert(KC == 64 || KC == 128, "k chunk");
   constexpr int CPR = KC / 8;              // 16-byte pieces of a row's chunk
   constexpr int RB = 2 * KC;               // bytes of a row's chunk
@@ -489,9 +511,10 @@ extern "C" int a8_gemm_silu_small(const void *x, int64_t ldx, const void *w13, i
   return (int)hipGetLastError();
 }
 
-extern "C" int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo,
-                                  void *ws, int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, int gated,
-                                  int res_add, float *ss_out, const float *ss_in, int ss_n, float eps, void *stream) {
+static int gemm_small_norm_impl(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo,
+                                void *ws, int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, int gated,
+                                int res_add, float *ss_out, const float *ss_in, int ss_n, float eps, const void *pf,
+                                int64_t pf_bytes, void *pf_sink, int pf_slices, void *stream) {
   using namespace a8;
   if (M < 0 || N < 0 || K < 0 || splits < 1 || mblocks < 1 || ss_n < 0)
     return set_error(A8_EINVAL, "gemm_small_norm: bad sizes M=%d N=%d K=%d splits=%d mblocks=%d", M, N, K, splits,
@@ -535,11 +558,30 @@ extern "C" int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int
                      kGmCntBytes / 4);
   int32_t *cnt = S_used > 1 ? (int32_t *)ws : nullptr;
   float *part = S_used > 1 ? (float *)((char *)ws + kGmCntBytes) : nullptr;
-  const dim3 grid((unsigned)ntile, (unsigned)S_used, (unsigned)nmb);
+  const bool do_pf = pf && pf_bytes >= 16 && pf_slices > 0;
+  if (do_pf && (!pf_sink || !al16g(pf) || !al16g(pf_sink) || pf_slices > 64))
+    return set_error(A8_EINVAL, "gemm_small_norm: prefetch needs 16-byte aligned pointers and 1..64 slices");
+  const dim3 grid((unsigned)ntile, (unsigned)S_used, (unsigned)(nmb + (do_pf ? pf_slices : 0)));
   const bool w8 = MT % 4 == 0;
   auto kern = gm_kernel(MT, KC);
-  const GmEpi ep{res_add ? 1 : 0, ss_out, ss_in, ss_n, eps};
+  const GmEpi ep{res_add ? 1 : 0, ss_out, ss_in, ss_n, eps, do_pf ? (const u32x4 *)pf : nullptr,
+                 do_pf ? pf_bytes / 16 : 0, (uint32_t *)pf_sink, nmb};
   hipLaunchKernelGGL(kern, grid, dim3(w8 ? 512 : 256), 0, (hipStream_t)stream, (const uint16_t *)x, ldx,
                      (const uint16_t *)w, ldw, (uint16_t *)out, ldo, part, cnt, M, N, K, cps, S_used, I, ep);
   return (int)hipGetLastError();
+}
+
+extern "C" int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo,
+                                  void *ws, int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, int gated,
+                                  int res_add, float *ss_out, const float *ss_in, int ss_n, float eps, void *stream) {
+  return gemm_small_norm_impl(x, ldx, w, ldw, out, ldo, ws, ws_bytes, M, N, K, splits, mblocks, gated, res_add, ss_out,
+                              ss_in, ss_n, eps, nullptr, 0, nullptr, 0, stream);
+}
+
+extern "C" int a8_gemm_small_norm_pf(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo,
+                                     void *ws, int64_t ws_bytes, int M, int N, int K, int splits, int mblocks,
+                                     int gated, int res_add, float *ss_out, const float *ss_in, int ss_n, float eps,
+                                     const void *pf, int64_t pf_bytes, void *pf_sink, int pf_slices, void *stream) {
+  return gemm_small_norm_impl(x, ldx, w, ldw, out, ldo, ws, ws_bytes, M, N, K, splits, mblocks, gated, res_add, ss_out,
+                              ss_in, ss_n, eps, pf, pf_bytes, pf_sink, pf_slices, stream);
 }

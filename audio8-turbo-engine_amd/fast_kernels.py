@@ -560,7 +560,7 @@ def gemm_silu_small(x, w13, out=None, mblocks=1):
 
 
 def gemm_small_norm(x, w, out, splits=1, mblocks=1, ws=None, gated=False, res_add=False, ss_out=None, ss_in=None,
-                    eps=1e-6):
+                    eps=1e-6, prefetch=None, pf_sink=None, pf_slices=8):
     """The slow-AR projections with the residual RMSNorm between them folded in (a8_gemm_small_norm; the
     reference runs rmsnorm, fast_kernels.py:30-69, as its own launch between the products):
       res_add: out is the residual stream, updated in place: out = bf16(bf16(x @ w^T) + out) -- the product
@@ -571,7 +571,10 @@ def gemm_small_norm(x, w, out, splits=1, mblocks=1, ws=None, gated=False, res_ad
         (the reference rounds h * (1 / rms) and its product with the norm weight to bf16 first: within bf16
         rounding noise of it); with gated, w = [gate; up] and out = silu_mul of the two (gemm_silu_small's
         epilogue).
-    M <= 192, K a multiple of 64, N of 8 (32 with ss_out, 16 gated); splits / ws / mblocks as gemm_small."""
+    M <= 192, K a multiple of 64, N of 8 (32 with ss_out, 16 gated); splits / ws / mblocks as gemm_small.
+    prefetch (a contiguous device tensor, with pf_sink: 16 device bytes): pf_slices more grid slices of
+    workgroups read it once while the product runs (a8_gemm_small_norm_pf: the next product's weights into the
+    memory-side cache); the result is the same."""
     _check_bf16("x", x, 2)
     _check_bf16("w", w, 2)
     M, K = x.shape
@@ -585,13 +588,19 @@ def gemm_small_norm(x, w, out, splits=1, mblocks=1, ws=None, gated=False, res_ad
                   f"{name} must be a contiguous float32 [>= M, groups] tensor")
     if ss_out is not None:
         _need(ss_out.shape[1] == N // 32, f"ss_out must have N / 32 = {N // 32} columns")
-    _check_device(x=x, w=w, out=out, ws=ws, ss_out=ss_out, ss_in=ss_in)
-    st = _lib.load().a8_gemm_small_norm(
-        x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
-        ws.data_ptr() if ws is not None else None, ws.numel() * ws.element_size() if ws is not None else 0,
-        M, N, K, int(splits), int(mblocks), int(bool(gated)), int(bool(res_add)),
-        ss_out.data_ptr() if ss_out is not None else None, ss_in.data_ptr() if ss_in is not None else None,
-        ss_in.shape[1] if ss_in is not None else 0, float(eps), _lib.stream_of(x))
+    _check_device(x=x, w=w, out=out, ws=ws, ss_out=ss_out, ss_in=ss_in, prefetch=prefetch, pf_sink=pf_sink)
+    args = [x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
+            ws.data_ptr() if ws is not None else None, ws.numel() * ws.element_size() if ws is not None else 0,
+            M, N, K, int(splits), int(mblocks), int(bool(gated)), int(bool(res_add)),
+            ss_out.data_ptr() if ss_out is not None else None, ss_in.data_ptr() if ss_in is not None else None,
+            ss_in.shape[1] if ss_in is not None else 0, float(eps)]
+    if prefetch is not None:
+        _need(prefetch.is_contiguous() and pf_sink is not None and pf_sink.numel() * pf_sink.element_size() >= 16,
+              "prefetch must be contiguous, with a 16-byte pf_sink")
+        st = _lib.load().a8_gemm_small_norm_pf(*args, prefetch.data_ptr(), prefetch.numel() * prefetch.element_size(),
+                                               pf_sink.data_ptr(), int(pf_slices), _lib.stream_of(x))
+    else:
+        st = _lib.load().a8_gemm_small_norm(*args, _lib.stream_of(x))
     _lib.check(st, "gemm_small_norm")
     return out
 
@@ -741,12 +750,13 @@ class GemmDispatch:
             return best
         return 1, (1 if N >= 4096 else max(1, M // 32))
 
-    def residual(self, x, w, res, ss_out=None):
+    def residual(self, x, w, res, ss_out=None, prefetch=None, pf_sink=None, pf_slices=8):
         """res += x @ w^T in place (the product rounded to bf16, then the residual add: rmsnorm's residual
-        step), with the new stream's per-row sums of squares into ss_out ([M, N / 32] fp32)."""
+        step), with the new stream's per-row sums of squares into ss_out ([M, N / 32] fp32); prefetch / pf_sink
+        as gemm_small_norm's."""
         sp, mb = self._shape(x.shape[0], w.shape[0], w.shape[1], False)
         return gemm_small_norm(x, w, res, splits=sp, mblocks=mb, ws=self.ws if sp > 1 else None, res_add=True,
-                               ss_out=ss_out)
+                               ss_out=ss_out, prefetch=prefetch, pf_sink=pf_sink, pf_slices=pf_slices)
 
     def normed(self, h, wf, ss_in, eps, out, gated=False):
         """The product of RMSNorm(h) with a weight whose norm weight is folded in (fold_norm), the norm's

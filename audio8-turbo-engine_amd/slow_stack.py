@@ -69,6 +69,11 @@ class SlowStack:
         self.fuse_norm = False
         self._folded = None
         self._ss = None
+        # prefetch_w13 (norm-fused steps): the o projection's launch carries extra workgroups that read the layer's
+        # w13 weights once (gemm_small_norm prefetch), so the w13 product finds them in the memory-side cache
+        self.prefetch_w13 = True
+        self.pf_slices = 8  # grid slices of prefetch workgroups (each as many as the o product's weight tiles)
+        self._sink = None
 
     def _fused_ready(self, R, plan):
         if not (self.fuse_norm and isinstance(self.mm, GemmDispatch) and plan is None and R <= self.FUSE_NORM_ROWS):
@@ -78,6 +83,7 @@ class SlowStack:
             self._folded = [(fold_norm(L["wqkv"], L["ln1"]), fold_norm(L["w13"], L["ln2"])) for L in self.layers]
             dev = self.norm.device
             self._ss = [torch.zeros(self.FUSE_NORM_ROWS, hidden // 32, dtype=torch.float32, device=dev) for _ in range(2)]
+            self._sink = torch.zeros(4, dtype=torch.int32, device=dev)
         return True
 
     def _forward_fused(self, x, pos, slot, lens, nsplit, rowmap, fuse):
@@ -97,7 +103,8 @@ class SlowStack:
                 qkv = mm.normed(res, wqkv_f, ss_b, self.eps, torch.empty(R, wqkv_f.shape[0], dtype=x.dtype,
                                                                           device=x.device))
             self.attn.layer(i, qkv, L["bqkv"], pos, slot, lens, q, o, nsplit=nsplit, rowmap=rowmap, fuse=fuse)
-            mm.residual(o.view(R, -1), L["wo"], res, ss_a)          # res += o @ wo^T
+            mm.residual(o.view(R, -1), L["wo"], res, ss_a,          # res += o @ wo^T
+                        prefetch=w13_f if self.prefetch_w13 else None, pf_sink=self._sink, pf_slices=self.pf_slices)
             act = mm.normed(res, w13_f, ss_a, self.eps, torch.empty(R, w13_f.shape[0] // 2, dtype=x.dtype,
                                                                     device=x.device), gated=True)
             mm.residual(act, L["w2"], res, ss_b)                    # res += act @ w2^T

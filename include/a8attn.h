@@ -368,6 +368,15 @@ int a8_gemm_silu_small(const void *x, int64_t ldx, const void *w13, int64_t ldw,
 int a8_gemm_small_norm(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo, void *ws,
                        int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, int gated, int res_add,
                        float *ss_out, const float *ss_in, int ss_n, float eps, void *stream);
+/*
+ * a8_gemm_small_norm with `pf_slices` more grid slices of workgroups that only read [pf, pf + pf_bytes) once and
+ * end (no counterpart in the reference): the next product's weights go into the memory-side cache while this
+ * product runs; pf_sink a 16-byte device word the read may write in a case that practically never happens.
+ */
+int a8_gemm_small_norm_pf(const void *x, int64_t ldx, const void *w, int64_t ldw, void *out, int64_t ldo, void *ws,
+                          int64_t ws_bytes, int M, int N, int K, int splits, int mblocks, int gated, int res_add,
+                          float *ss_out, const float *ss_in, int ss_n, float eps, const void *pf, int64_t pf_bytes,
+                          void *pf_sink, int pf_slices, void *stream);
 
 /*
  * The streaming vocoder's channels-last convolutions (the codec decoder's default conv path,

@@ -25,7 +25,7 @@ def test_header_declares_the_entry_points():
                                          "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn",
                                          "a8_decode_attn_flat", "a8_decode_choose_flat", "a8_store_decode_flat",
                                          "a8_store_decode_split", "a8_prefix_copy", "a8_rmsnorm", "a8_silu_mul", "a8_gemm_small", "a8_gemm_silu_small", "a8_gemm_small_norm", "a8_ru_cl", "a8_decode_attn_f32q",
-                                         "a8_conv_cl", "a8_conv_cl_ws_bytes", "a8_snake_cat", "a8_conv_out_tanh", "a8_snake_cat_refresh"}
+                                         "a8_conv_cl", "a8_conv_cl_ws_bytes", "a8_snake_cat", "a8_conv_out_tanh", "a8_snake_cat_refresh", "a8_gemm_small_norm_pf"}
 
 
 def test_library_is_built_from_these_sources(a8):

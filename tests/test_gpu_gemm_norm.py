@@ -155,3 +155,53 @@ def test_slow_stack_fused_norm(a8, ref, lref, dev):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(yg, got), f"replay {rep} differs from the eager step"
+
+
+def test_prefetch_workgroups_change_nothing(a8, dev):
+    """gemm_small_norm with prefetch workgroups in its grid (the next product's weights read beside it) gives the
+    same residual stream and sums of squares as without, bit for bit, at one and four k splits; and a prefetch
+    that covers a ragged byte count (not a multiple of the grid's stride) reads within its tensor."""
+    say("case: gemm_small_norm with prefetch workgroups vs without")
+    g = torch.Generator().manual_seed(91)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    nxt = randn_bf16(g, 9728 * 896 + 40, 1).view(-1).to(dev)   # 17.4 MB + 80 bytes
+    for M, N, K, splits, mblocks in ((192, 896, 896, 1, 6), (192, 896, 4864, 4, 3)):
+        x = randn_bf16(g, M, K).to(dev)
+        w = (randn_bf16(g, N, K) * (K ** -0.5)).to(BF).to(dev)
+        res0 = randn_bf16(g, M, N).to(dev)
+        ws = torch.zeros(a8.gemm_ws_bytes(M, N, splits), dtype=torch.uint8, device=dev) if splits > 1 else None
+        outs = []
+        for pf in (None, nxt):
+            res = res0.clone()
+            ss = torch.zeros(M, N // 32, dtype=torch.float32, device=dev)
+            a8.gemm_small_norm(x, w, res, splits=splits, mblocks=mblocks, ws=ws, res_add=True, ss_out=ss,
+                               prefetch=pf, pf_sink=sink)
+            torch.cuda.synchronize()
+            outs.append((res, ss))
+        assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), (M, N, K)
+
+
+def test_slow_stack_prefetch_is_the_same_step(a8, dev):
+    """The norm-fused slow-AR step with the w13 prefetch (the default) against the same step without: the final
+    hidden state and the caches bit for bit."""
+    say("case: slow stack fused step, w13 prefetch on / off")
+    from importlib import import_module
+    ss_mod = import_module(a8.__name__ + ".slow_stack")
+    layers, norm = ss_mod.random_weights(2, 896, 14, 2, 64, 1024, dev, seed=13)
+    outs = []
+    for pf in (True, False):
+        st = a8.SlowStack(layers, norm, 14, 2, 64, 1e-6, 10000.0, max_rows=64, cache_rows=17, cache_len=256,
+                          max_pos=256, dev=dev)
+        mm = a8.GemmDispatch()
+        mm.tune([L[k] for L in layers for k in ("wqkv", "wo", "w13", "w2")], [16], gated=[L["w13"] for L in layers])
+        st.mm, st.fuse_norm, st.prefetch_w13 = mm, True, pf
+        gen = torch.Generator(device=dev).manual_seed(14)
+        st.kc_all.normal_(generator=gen)
+        st.vc_all.normal_(generator=gen)
+        x = torch.randn(16, 896, generator=gen, device=dev).to(BF)
+        lens = torch.full((16,), 200, dtype=torch.int32, device=dev)
+        h = st.forward(x, lens - 1, torch.arange(16, dtype=torch.int32, device=dev), lens, rowmap=False, fuse=True)
+        torch.cuda.synchronize()
+        outs.append((h.clone(), st.kc_all.clone(), st.vc_all.clone()))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
