@@ -758,12 +758,12 @@ class GemmDispatch:
         return gemm_small_norm(x, w, res, splits=sp, mblocks=mb, ws=self.ws if sp > 1 else None, res_add=True,
                                ss_out=ss_out, prefetch=prefetch, pf_sink=pf_sink, pf_slices=pf_slices)
 
-    def normed(self, h, wf, ss_in, eps, out, gated=False):
+    def normed(self, h, wf, ss_in, eps, out, gated=False, prefetch=None, pf_sink=None, pf_slices=8):
         """The product of RMSNorm(h) with a weight whose norm weight is folded in (fold_norm), the norm's
         statistic from the producer's ss_out; gated: silu_mul of the [gate; up] halves."""
         sp, mb = self._shape(h.shape[0], wf.shape[0], wf.shape[1], gated)
         return gemm_small_norm(h, wf, out, splits=sp, mblocks=mb, ws=self.ws if sp > 1 else None, gated=gated,
-                               ss_in=ss_in, eps=eps)
+                               ss_in=ss_in, eps=eps, prefetch=prefetch, pf_sink=pf_sink, pf_slices=pf_slices)
 
 
 _F16 = torch.float16

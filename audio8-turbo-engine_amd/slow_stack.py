@@ -73,6 +73,12 @@ class SlowStack:
         # w13 weights once (gemm_small_norm prefetch), so the w13 product finds them in the memory-side cache
         self.prefetch_w13 = True
         self.pf_slices = 8  # grid slices of prefetch workgroups (each as many as the o product's weight tiles)
+        # prefetch_kv_bytes: the qkv product's launch (layers after the first) also reads about this many bytes of
+        # the layer's K cache -- the last rows of the tick, which the whole-row decode reaches in its second pass --
+        # into the memory-side cache, at most a sixth of the rows (measured at 192 rows x 2048: 32 rows, 16.8 MB,
+        # -0.55 us per layer; 64 rows outlast the qkv product and cost +3 us). 0: none.
+        self.prefetch_kv_bytes = 16 << 20
+        self.kv_slices = 8
         self._sink = None
 
     def _fused_ready(self, R, plan):
@@ -100,8 +106,15 @@ class SlowStack:
             if i == 0:
                 qkv = mm(h, L["wqkv"])
             else:  # RMSNorm(res, ln1) folded in, its statistic from the previous layer's w2 product
+                pk = None
+                row_bytes = self.kc[i][0].numel() * self.kc[i].element_size()
+                n = min(R // 6, self.prefetch_kv_bytes // row_bytes) if self.prefetch_w13 else 0
+                if n > 0 and self.kc[i].is_contiguous():
+                    r0 = max(0, min(R, self.kc[i].shape[0]) - n)
+                    pk = self.kc[i][r0:r0 + n]
                 qkv = mm.normed(res, wqkv_f, ss_b, self.eps, torch.empty(R, wqkv_f.shape[0], dtype=x.dtype,
-                                                                          device=x.device))
+                                                                          device=x.device),
+                                prefetch=pk, pf_sink=self._sink, pf_slices=self.kv_slices)
             self.attn.layer(i, qkv, L["bqkv"], pos, slot, lens, q, o, nsplit=nsplit, rowmap=rowmap, fuse=fuse)
             mm.residual(o.view(R, -1), L["wo"], res, ss_a,          # res += o @ wo^T
                         prefetch=w13_f if self.prefetch_w13 else None, pf_sink=self._sink, pf_slices=self.pf_slices)
