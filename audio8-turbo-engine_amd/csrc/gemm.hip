@@ -561,7 +561,9 @@ static int gemm_small_norm_impl(const void *x, int64_t ldx, const void *w, int64
   const bool do_pf = pf && pf_bytes >= 16 && pf_slices > 0;
   if (do_pf && (!pf_sink || !al16g(pf) || !al16g(pf_sink) || pf_slices > 64))
     return set_error(A8_EINVAL, "gemm_small_norm: prefetch needs 16-byte aligned pointers and 1..64 slices");
-  const dim3 grid((unsigned)ntile, (unsigned)S_used, (unsigned)(nmb + (do_pf ? pf_slices : 0)));
+  // pf_slices counts slices of ntile prefetch workgroups: with k splits each grid slice holds S_used times that
+  const int pf_z = do_pf ? (pf_slices + S_used - 1) / S_used : 0;
+  const dim3 grid((unsigned)ntile, (unsigned)S_used, (unsigned)(nmb + pf_z));
   const bool w8 = MT % 4 == 0;
   auto kern = gm_kernel(MT, KC);
   const GmEpi ep{res_add ? 1 : 0, ss_out, ss_in, ss_n, eps, do_pf ? (const u32x4 *)pf : nullptr,

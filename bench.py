@@ -51,6 +51,9 @@ def parse():
                    help="only run the streaming decoder for 5 frames at 192 rows (target of rocprofv3)")
     p.add_argument("--slow-probe", action="store_true",
                    help="only tune GemmDispatch and replay the 24-layer slow-AR step 3 times (target of rocprofv3)")
+    p.add_argument("--gemm-shapes", default=None,
+                   help="with --slow-probe: these gemm_small shapes (NxK:splits:mblocks,...) instead of the tuned ones "
+                        "(the tuning's timings under a profiler differ from the bench's)")
     return p.parse_args()
 
 
@@ -491,7 +494,7 @@ def vocoder_probe(a8, torch, dev):
     print("vocoder probe: 5 frames done", flush=True)
 
 
-def slow_probe(a8, torch, dev):
+def slow_probe(a8, torch, dev, shapes=None):
     """Profile target for the slow-AR step's projections: the 24-layer step at 192 rows x KV 2048 (synthetic
     weights, as the slow_ar_step leg) with GemmDispatch tuned first and the norms inside the projections, then 3 steps
     replayed from a graph."""
@@ -503,6 +506,12 @@ def slow_probe(a8, torch, dev):
                       cache_len=S, max_pos=S, dev=dev)
     mm = a8.GemmDispatch()
     mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b], gated=[L["w13"] for L in wts])
+    for item in (shapes.split(",") if shapes else []):
+        nk, sp, mb = item.split(":")
+        N, K = (int(v) for v in nk.split("x"))
+        mm.small_best[(b, N, K)] = (int(sp), int(mb))
+        if (b, N, K) in mm.gated_best:
+            mm.gated_best[(b, N, K)] = (1, int(mb))
     st.mm = mm
     st.fuse_norm = True
     gen = torch.Generator(device=dev).manual_seed(5)
@@ -513,7 +522,8 @@ def slow_probe(a8, torch, dev):
     for _ in range(3):
         g.replay()
     torch.cuda.synchronize()
-    print("slow probe: choices", {f"{N}x{K}": c for (M, N, K), c in mm.small.items()}, flush=True)
+    print("slow probe: gemm_small shapes", {f"{N}x{K}": c for (M, N, K), c in mm.small_best.items()},
+          "gated", {f"{N}x{K}": c for (M, N, K), c in mm.gated_best.items()}, flush=True)
 
 
 def prefill_probe(a8, torch, dev):
@@ -557,7 +567,7 @@ def main():
         vocoder_probe(a8, torch, dev)
         return
     if args.slow_probe:
-        slow_probe(a8, torch, dev)
+        slow_probe(a8, torch, dev, args.gemm_shapes)
         return
     props = torch.cuda.get_device_properties(dev)
     w = build_workload(a8, torch, args.config, dev)
