@@ -1,31 +1,38 @@
 // Whole-row decode: the launch a8_decode_attn_stream / a8_store_decode_stream make when one chunk holds a
-// whole row at 4 waves and one tile per step (the peak-load shape, 192 rows x 2048 keys). Same work per
-// wave as k_decode_stream with one chunk per unit -- wave w of the workgroup consumes tiles w, w + 4, ...
-// of the unit (row, kv head) with decode_tile.h's step, and the last wave to finish merges the four
-// partials with the same arithmetic -- so the results are the same bits. Semantics are those of
-// serve/fast_kernels.py:193-290 (and, fused, bias_rope_store of 139-187 first).
+// whole row at 4 waves and one tile per step (the peak-load shape, 192 rows x 2048 keys). Wave w of the
+// workgroup consumes tiles w, w + 4, ... of the unit (row, kv head) with decode_tile.h's step; the four
+// partials are merged with k_decode_combine's arithmetic. Semantics are those of serve/fast_kernels.py:193-290
+// (and, fused, bias_rope_store of 139-187 first).
 //
-// What differs is the timeline around each unit (measured with per-wave clock stamps on MI355X: a unit
-// transition cost every wave ~1.3 us, the last unit's merge ~1.4 us, and the first q was ready ~2.9 us
-// after the first tile request, its RoPE-table loads queued behind every wave's first tiles):
+// The timeline around each unit (measured with per-wave clock stamps and with copies that skip parts of the
+// work, on MI355X at 192 rows x 2048 keys):
 //   * Workgroup g takes units g, g + G, ...; a unit's SPW steps are unrolled, so every load, store and
 //     wait sits at a fixed point and the compiler's wait counts are exact (no branch joins paths with
 //     different numbers of memory operations in flight). Stores that only some lanes or waves make are
 //     buffer stores whose range check drops the others' (no branch around them either).
+//   * Unit u starts at step u % SPW (its waves take their tiles in the same rotated order). Units whose
+//     streams all start at the same offset and advance in step meet the same memory channels at the same
+//     time: a plain read of the peak-load bytes in this kernel's pattern took 35.2 us with every unit starting
+//     at key 0 and 33.6-33.8 us with the rotation; the decode itself gained 0.2-0.4 us.
 //   * The inputs of unit i + 1 (q, or its qkv / bias / RoPE-table rows) are requested at unit i's first
-//     step and, fused, rotated at its fourth, when they have long arrived; the k / v / q store of unit
-//     i + 1 goes out then too. The metadata of unit i + 2 follows at unit i's first step. At the
-//     transition no wave waits for anything but its next tile.
+//     step and, fused, rotated at its third, when they have long arrived. The metadata of unit i + 2
+//     follows at unit i's first step. At the transition no wave waits for anything but its next tile.
 //   * The first unit's metadata and qkv / bias rows go out before any tile, its table rows as soon as the
 //     position returns and before the tiles, so q is ready about when the first tiles land.
-//   * The merge reads every parked partial it needs with one batch of LDS reads.
+//   * A unit's k / v / q writes go out after its last step (at its first step, in the middle of the tile
+//     requests, they cost ~0.45 us per layer at the peak load).
+//   * A finished unit is only parked (each wave's m, l, O in LDS); after every second unit and after the last
+//     the workgroup waits for its slowest wave and all four waves merge the parked units, a slice of the
+//     outputs each, with the hardware reciprocal for the division. Merging each unit as it finished, on the
+//     last wave to arrive, cost ~0.7 us per layer more (the merging wave falls behind, the last merge runs
+//     on one wave).
 //   * Nothing is requested past the last tile (the pipeline's last two steps issue no load).
-// Measured at 192 rows x 2048 keys, 24 layers in a graph: 36.2-36.9 us per layer unfused and 37.5-38.1
-// fused (store included), against 37.2-37.8 and 39.3-39.7 for k_decode_stream on the same boxes. Tried and
-// slower: four tiles in flight per wave (+1 us), the first tiles requested before the position (+0.9 to
-// +2.3 us: the table rows then return behind them, also when read through the scalar cache), the unit
-// park deferred behind the next unit's first request (+0.3 us); the order of the tiles within a unit and
-// of the units over the workgroups changed nothing beyond box-to-box noise.
+// Measured at 192 rows x 2048 keys, 24 layers in a graph: 35.0-35.4 us per layer unfused and 36.2-36.5
+// fused (store included). Tried and slower: four tiles in flight per wave (+1 us), the first tiles requested
+// before the position (+0.9 to +2.3 us: the table rows then return behind them), the table rows read through
+// the scalar cache after the first tiles (+1.8 us), each step's refill requested in two halves inside the
+// step (K after the score products, V after the P.V operand reads: +0.8 us), one unit per workgroup over all
+// compute units (k_decode_unit at grid 384: +2 us).
 #include "fused_qkv.h"
 
 namespace a8 {
@@ -50,10 +57,66 @@ struct RowMeta {
 struct RowUnit {
   int row, kh, hi;  // keys [0, hi) of cache row crow are attended
   int crow;
+  int rot;  // the unit's first step (units start at different offsets; see k_decode_rows)
   rsrc_t kr, vr;
 };
 
 }  // namespace
+
+// Per-wave partial of a finished unit as parked in LDS: m[16], l[16] (row sum over the lane groups), then O in
+// rows of kOb floats (q head r16 of the group, 64 dims).
+constexpr int kParkFloats = 32 + 16 * kOb;
+
+__device__ __forceinline__ void park_partial(float *r, const SoftmaxState &S, const TileLane &tl) {
+  const float lsum = sum_over_groups(S.lsum);
+  if (tl.g == 0) {
+    r[tl.r16] = S.m;
+    r[16 + tl.r16] = lsum;
+  }
+  lds_store_4x16(r + 32 + tl.r16 * kOb + 4 * tl.g, S.o[0], S.o[1], S.o[2], S.o[3]);
+}
+
+// Merges the NW parked partials of each of cnt (<= 2) units and writes the units' outputs. Wave partial v of
+// unit s is at rs + v * rstride (rs = r0 or r1). The items (unit, q head, 4 dims) are shared out over the NW
+// waves (item w * 64 + lane, then + NW * 64), so every wave of the workgroup merges a slice. Arithmetic of
+// k_decode_combine's merge with a running maximum taken over the NW partials at once, the division as a
+// multiplication by the hardware reciprocal.
+template <int NW>
+__device__ __forceinline__ void merge_units(const float *r0, const float *r1, int rstride, int cnt, int row0, int kh0,
+                                            int row1, int kh1, uint16_t *out, int64_t s_ob, int64_t s_oh, int group,
+                                            float sl2, int w, int lane) {
+  const int per = group * 16, total = cnt * per;
+  for (int t = w * 64 + lane; t < total; t += NW * 64) {
+    const bool second = t >= per;
+    const int rem = second ? t - per : t;
+    const int head = rem >> 4, d4 = (rem & 15) * 4;
+    const float *rb = second ? r1 : r0;
+    float mv[NW], lv[NW];
+    f32x4 ov[NW];
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float *rv = rb + v * rstride;
+      mv[v] = rv[head];
+      lv[v] = rv[16 + head];
+      ov[v] = *reinterpret_cast<const f32x4 *>(rv + 32 + head * kOb + d4);
+    }
+    float M = kNegInf;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) M = fmaxf(M, mv[v]);
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float wt = (mv[v] == kNegInf) ? 0.f : fast_exp2((mv[v] - M) * sl2);
+      num += wt * ov[v];
+      den += wt * lv[v];
+    }
+    const float rd = __builtin_amdgcn_rcpf(den);
+    const u32x2 res{pack_bf16x2(num[0] * rd, num[1] * rd), pack_bf16x2(num[2] * rd, num[3] * rd)};
+    const int row = second ? row1 : row0, kh = second ? kh1 : kh0;
+    st8(out + (int64_t)row * s_ob + (int64_t)(kh * group + head) * s_oh + d4, res);
+  }
+}
 
 template <bool FUSED, int SPW>
 __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
@@ -72,10 +135,9 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
   // waits only for the buffer it reads
   __shared__ __attribute__((aligned(16))) uint16_t vb0[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vb1[NW * kVTile];
-  // per-wave m, l, O of a finished unit, two areas (a unit's merge may still read one while the next parks)
+  // per-wave m, l, O of finished units, parked until MB of them are merged together
   constexpr int MB = 2;
-  __shared__ __attribute__((aligned(16))) float mrg[MB][NW * (32 + 16 * kOb)];
-  __shared__ int marr[MB], mseq[MB];
+  __shared__ __attribute__((aligned(16))) float mrg[MB][NW * kParkFloats];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -83,11 +145,6 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
   const int U = b * nkv;
   const int nmine = ((int)blockIdx.x < U) ? (U - 1 - (int)blockIdx.x) / G + 1 : 0;
   if (nmine == 0) return;
-  if (tid < MB) {
-    marr[tid] = 0;
-    mseq[tid] = tid - MB;
-  }
-  lds_barrier();
 
   TileLane tl;
   tl.init(lane);
@@ -99,7 +156,8 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
   const rsrc_t pos_r = make_rsrc(si.pos, FUSED ? (uint32_t)b * 4u : 0u);
   const rsrc_t slot_r = make_rsrc(si.slot, FUSED ? (uint32_t)b * 4u : 0u);
   auto unit_of = [&](int i) { return (int)blockIdx.x + i * G; };
-  auto tile_of = [&](int j) { return w + NW * j; };  // wave w: tiles w, w + NW, ... of the unit
+  // wave w: tiles w, w + NW, ... of the unit, starting at step rot
+  auto tile_of = [&](int rot, int j) { return w + NW * ((j + rot) & (SPW - 1)); };
   auto row_of = [&](int i) { return unit_of(i) / nkv; };
   auto meta_load = [&](int i) {
     const bool live = i < nmine;
@@ -117,6 +175,7 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
     const int u = unit_of(i);
     un.row = u / nkv;
     un.kh = u - un.row * nkv;
+    un.rot = u & (SPW - 1);
     int crow = un.row;
     if (rowmap) crow = __builtin_amdgcn_readfirstlane(m.craw);  // waits for the row map only when there is one
     const bool ok = i < nmine && crow >= 0 && crow < cache_rows;
@@ -215,86 +274,39 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
   ptc.col = -1;
   ptn.col = -1;
   QkvRaw rn;      // fused: raw chunks of the next unit, between its request and its rotation
-  StoreDst sdn;   // fused: where unit 0's / the next unit's k / v / q go
+  StoreDst sdc, sdn;  // fused: where the current / next unit's k / v / q go
   int mcur_p = 0, mcur_s = 0;  // fused: position / slot of unit i + 1 while it is prepared
 
-  // ---- unit finish: park, count in; the last of the NW waves merges and writes out ----
-  int nfin = 0;
+  // ---- unit finish: park the wave's partial; every MB units (and after the last) the workgroup waits for its
+  // slowest wave and all waves merge the parked units together, a slice each ----
+  int nfin = 0, prow0 = 0, pkh0 = 0;
   auto finish = [&](const RowUnit &un) {
     const int n = nfin++;
-    const int bsel = MB > 1 ? (n & 1) : 0;
-    float *mb = mrg[bsel], *lb = mb + NW * 16, *ob = mb + NW * 32;
-    const float lsum = sum_over_groups(S.lsum);
-    // the merge of unit n - MB out of this area is complete (it waits for nothing, so this ends; bounded all
-    // the same)
-    for (int spin = 0; spin < (1 << 22) && lds_read_word(&mseq[bsel]) < n - MB; ++spin) __builtin_amdgcn_s_sleep(1);
-    if (tl.g == 0) {
-      mb[w * 16 + tl.r16] = S.m;
-      lb[w * 16 + tl.r16] = lsum;
-    }
-    lds_store_4x16(ob + (w * 16 + tl.r16) * kOb + 4 * tl.g, S.o[0], S.o[1], S.o[2], S.o[3]);
+    const int slot = n % MB;
+    park_partial(mrg[slot] + w * kParkFloats, S, tl);
     S.reset();
-    const bool last = lds_add_word(&marr[bsel], 1) == NW - 1;
-    // the output row of the unit: lanes (head, 4 dims), item t = lane and lane + 64 (t < group * 16)
-    const rsrc_t orr = make_rsrc_wave(out + (int64_t)un.row * s_ob + (int64_t)un.kh * group * s_oh,
-                                      (uint32_t)(((group - 1) * s_oh + 64) * 2));
-    u32x2 res[2];
-    uint32_t ooff[2];
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      res[it] = u32x2{0u, 0u};
-      ooff[it] = kOOR;
+    if (slot == 0) {
+      prow0 = un.row;
+      pkh0 = un.kh;
     }
-    if (last) {
-      lds_write_word(&marr[bsel], 0);  // the buffer's next arrivals come after mseq says n is merged
-      float mv[2][NW], lv[2][NW];
-      f32x4 ov[2][NW];
-#pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int t = min(lane + 64 * it, group * 16 - 1);
-        const int head = t >> 4, d4 = (t & 15) * 4;
-#pragma unroll
-        for (int v = 0; v < NW; ++v) {
-          mv[it][v] = mb[v * 16 + head];
-          lv[it][v] = lb[v * 16 + head];
-          ov[it][v] = *reinterpret_cast<const f32x4 *>(ob + (v * 16 + head) * kOb + d4);
-        }
-      }
-#pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int t = lane + 64 * it;
-        const int head = t >> 4, d4 = (t & 15) * 4;
-        float M = kNegInf;
-#pragma unroll
-        for (int v = 0; v < NW; ++v) M = fmaxf(M, mv[it][v]);
-        f32x4 num = {0.f, 0.f, 0.f, 0.f};
-        float den = 0.f;
-#pragma unroll
-        for (int v = 0; v < NW; ++v) {
-          const float wt = (mv[it][v] == kNegInf) ? 0.f : fast_exp2((mv[it][v] - M) * sl2);
-          num += wt * ov[it][v];
-          den += wt * lv[it][v];
-        }
-        res[it][0] = pack_bf16x2(num[0] / den, num[1] / den);
-        res[it][1] = pack_bf16x2(num[2] / den, num[3] / den);
-        if (t < group * 16) ooff[it] = (uint32_t)(head * s_oh * 2 + d4 * 2);
-      }
+    if (slot == MB - 1 || n == nmine - 1) {
+      lds_barrier();  // every wave has parked (loads of the next unit stay in flight)
+      merge_units<NW>(mrg[0], mrg[1], kParkFloats, slot + 1, prow0, pkh0, un.row, un.kh, out, s_ob, s_oh, group,
+                      sl2, w, lane);
+      if (n < nmine - 1) lds_barrier();  // the area is read before the next unit parks into it
     }
-#pragma unroll
-    for (int it = 0; it < 2; ++it) bst8(orr, ooff[it], res[it]);
-    if (last) lds_write_word(&mseq[bsel], n);  // after the reads above: the buffer may be reused
   };
 
   // ---- steps: compute tile j of the current unit from buffer j % D, then request into it tile j + D of the
   // unit, or tile j + D - SPW of the next (one load sequence, sources selected) ----
   auto step = [&](KTile(&X)[1], uint16_t *xv, int j, bool reload) __attribute__((always_inline)) {
-    const int t0 = 64 * tile_of(j);
+    const int t0 = 64 * tile_of(cur.rot, j);
     if (t0 < cur.hi) compute_step<1, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
     if (reload) {
       const bool in_cur = j + D < SPW;
       const rsrc_t kr = in_cur ? cur.kr : nxt.kr, vr = in_cur ? cur.vr : nxt.vr;
-      const int jj = in_cur ? j + D : j + D - SPW;
-      load_step<1>(X, xv, kr, vr, (uint32_t)(64 * tile_of(jj)), tl);
+      const int tt = in_cur ? tile_of(cur.rot, j + D) : tile_of(nxt.rot, j + D - SPW);
+      load_step<1>(X, xv, kr, vr, (uint32_t)(64 * tt), tl);
     }
   };
   auto step_k = [&](int j, bool reload) __attribute__((always_inline)) {
@@ -304,7 +316,7 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
       step(T0, vbw[0], j, reload);
   };
   auto first_load = [&](int j) __attribute__((always_inline)) {
-    const uint32_t t0 = (uint32_t)(64 * tile_of(j));
+    const uint32_t t0 = (uint32_t)(64 * tile_of(cur.rot, j));
     if (j & 1)
       load_step<1>(T1, vbw[1], cur.kr, cur.vr, t0, tl);
     else
@@ -323,14 +335,14 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
     if (FUSED) {
       // the table rows go out as soon as the position is in, ahead of every tile (their data would return
       // behind the tiles' otherwise: measured slower with the first tile, or all, requested before the
-      // position); the range is exact
+      // position, and slower again with the table rows read through the scalar cache); the range is exact
       load_xb(u0, true, r0);
       load_tab(true, __builtin_amdgcn_readfirstlane(m0.praw), r0);
       resolve(0, m0, cur, true);
       first_load(0);
-      // unit 0's rotation, once its table rows are in; its stores follow the first step
+      // unit 0's rotation, once its table rows are in
       rope_unit(cur, true, __builtin_amdgcn_readfirstlane(m0.praw), __builtin_amdgcn_readfirstlane(m0.sraw), r0, qc0,
-                qc1, ptc, sdn);
+                qc1, ptc, sdc);
 #pragma unroll
       for (int j = 1; j < D; ++j) first_load(j);
     } else {
@@ -362,25 +374,196 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
         mn = meta_load(i + 2);
       }
       step_k(j, true);
-      if (FUSED && j == 0 && i == 0) rope_store(ptc, sdn);  // unit 0's k / v / q
-      if (FUSED && j == kRopeStep) {
-        rope_unit(nxt, true, mcur_p, mcur_s, rn, qn0, qn1, ptn, sdn);
-        rope_store(ptn, sdn);
-      }
+      if (FUSED && j == kRopeStep) rope_unit(nxt, true, mcur_p, mcur_s, rn, qn0, qn1, ptn, sdn);
     }
+    // the unit's k / v / q go out after its last step (stored at its first step they cost ~0.45 us per layer at
+    // the peak load); no row of the launch reads them back
+    if (FUSED) rope_store(ptc, sdc);
     finish(cur);
     cur = nxt;
     qc0 = qn0;
     qc1 = qn1;
-    if (FUSED) ptc = ptn;
+    if (FUSED) {
+      ptc = ptn;
+      sdc = sdn;
+    }
   }
   // ---- the last unit: no request past its last tile ----
 #pragma unroll
-  for (int j = 0; j < SPW; ++j) {
-    step_k(j, j + D < SPW);
-    if (FUSED && j == 0 && nmine == 1) rope_store(ptc, sdn);
-  }
+  for (int j = 0; j < SPW; ++j) step_k(j, j + D < SPW);
+  if (FUSED) rope_store(ptc, sdc);
   finish(cur);
+}
+
+// One unit (row, kv head) per workgroup, two workgroups per compute unit: the launch for grids of at least one
+// workgroup per unit (short rows, and row counts whose units do not fill the compute units twice over). Every
+// unit streams at once and a unit's four waves can share their SIMDs with another workgroup's. The work per
+// wave, the order of its tiles (rotated as in k_decode_rows) and the merge are those of k_decode_rows, so the
+// results are the same bits; each wave parks its partial in its first V buffer (free by then), which keeps the
+// LDS at 64 KB, and the four waves merge a slice of the outputs each.
+template <bool FUSED, int SPW>
+__global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
+    const uint16_t *__restrict__ q, int64_t s_qb, int64_t s_qh,
+    uint16_t *kc, uint16_t *vc, int64_t s_kb, int64_t s_kh,
+    int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
+    uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, int b, int nq, int nkv, int group,
+    float sl2, StoreIn si) {
+  constexpr int NW = kRowsNW;
+  constexpr int D = 2;  // tiles in flight per wave
+  warm_kernargs<232>();
+  static_assert(SPW % D == 0 && SPW >= 4, "steps per unit");
+  __shared__ __attribute__((aligned(16))) uint16_t vb0[NW * kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t vb1[NW * kVTile];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int u = blockIdx.x;
+  if (u >= b * nkv) return;
+  const int row = u / nkv, kh = u - row * nkv;
+
+  TileLane tl;
+  tl.init(lane);
+  uint16_t *const vbw[2] = {vb0 + w * kVTile, vb1 + w * kVTile};
+
+  // ---- metadata: row map, length, position, slot (vector loads, in order with the tiles) ----
+  const rsrc_t lens_r = make_rsrc(lens, (uint32_t)b * 4u);
+  const rsrc_t map_r = make_rsrc(rowmap, rowmap ? (uint32_t)b * 4u : 0u);
+  const rsrc_t pos_r = make_rsrc(si.pos, FUSED ? (uint32_t)b * 4u : 0u);
+  const rsrc_t slot_r = make_rsrc(si.slot, FUSED ? (uint32_t)b * 4u : 0u);
+  const uint32_t mo = (uint32_t)row * 4u;
+  const int craw = bld4(map_r, mo);
+  const int lraw = bld4(lens_r, mo);
+  const int praw = FUSED ? bld4(pos_r, mo) : 0;
+  const int sraw = FUSED ? bld4(slot_r, mo) : 0;
+
+  int crow = -1, hi = 0;
+  rsrc_t kr, vr;
+  // exact = false: the range is the whole cache row (the length is not waited for; hi is set later)
+  auto resolve = [&](bool exact) {
+    int c = row;
+    if (rowmap) c = __builtin_amdgcn_readfirstlane(craw);
+    const bool ok = c >= 0 && c < cache_rows;
+    crow = ok ? c : -1;
+    hi = (ok && exact) ? min(max(__builtin_amdgcn_readfirstlane(lraw), 0), cache_len) : 0;
+    const int64_t cb = (int64_t)(ok ? c : 0) * s_kb + (int64_t)kh * s_kh;
+    const uint32_t bound = ok ? (uint32_t)(exact ? hi : cache_len) * kRow : 0u;
+    kr = make_rsrc_wave(kc + cb, bound);
+    vr = make_rsrc_wave(vc + cb, bound);
+  };
+  // wave w: tiles w, w + NW, ... of the unit, starting at step u % SPW (as k_decode_rows)
+  const int rot = u & (SPW - 1);
+  auto tile_of = [&](int j) { return w + NW * ((j + rot) & (SPW - 1)); };
+  KTile T0[1], T1[1];
+  auto first_load = [&](int j) __attribute__((always_inline)) {
+    const uint32_t t0 = (uint32_t)(64 * tile_of(j));
+    if (j & 1)
+      load_step<1>(T1, vbw[1], kr, vr, t0, tl);
+    else
+      load_step<1>(T0, vbw[0], kr, vr, t0, tl);
+  };
+
+  u32x4 q0, q1;
+  KVPatch pt;
+  pt.col = -1;
+  // fused: the k / v / q writes of bias_rope_store, from wave 0 (every lane of every wave issues them; the
+  // range check drops the others')
+  rsrc_t skr, svr, sqr;
+  uint32_t sko = kOOR, svo = kOOR, sqo = kOOR;
+  if (FUSED) {
+    // qkv / bias chunks (lane head: fused_lane_head), then the position's table rows as soon as it returns,
+    // ahead of every tile
+    const int H = nq + 2 * nkv;
+    const rsrc_t xr = make_rsrc_wave(si.qkv + (int64_t)row * si.s_qkv, (uint32_t)H * 128u);
+    const rsrc_t br = make_rsrc(si.bias, si.bias ? (uint32_t)H * 128u : 0u);
+    const uint32_t ho = (uint32_t)fused_lane_head(tl.r16, kh, group, nq, nkv) * 128u + 16u * tl.g;
+    QkvRaw r;
+    r.w[0] = bld16(xr, ho);
+    r.w[1] = bld16(xr, ho + 64u);
+    r.bb[0] = bld16(br, ho);
+    r.bb[1] = bld16(br, ho + 64u);
+    const int p = __builtin_amdgcn_readfirstlane(praw);
+    const bool pv = p >= 0 && p < si.n_tab;
+    const rsrc_t cr = make_rsrc_wave(si.cos_tab + (int64_t)(pv ? p : 0) * si.s_cs, pv ? 128u : 0u);
+    const rsrc_t sr = make_rsrc_wave(si.sin_tab + (int64_t)(pv ? p : 0) * si.s_cs, pv ? 128u : 0u);
+    const uint32_t og = 16u * tl.g;
+    r.cs[0] = bld16(cr, og);
+    r.cs[1] = bld16(cr, og + 64u);
+    r.sn[0] = bld16(sr, og);
+    r.sn[1] = bld16(sr, og + 64u);
+    resolve(true);
+    first_load(0);
+    // the rotation (rope.h arithmetic), once the table rows are in
+    const int srow = __builtin_amdgcn_readfirstlane(sraw);
+    const int sidx = pv ? p % si.ring : 0;
+    const bool store_ok = pv && srow >= 0 && srow < cache_rows && sidx < cache_len;
+    float xl[8], xh[8], ol[8], oh[8];
+    rope_x(r.w[0], r.w[1], r.bb[0], r.bb[1], si.bias != nullptr, xl, xh);
+    rope_rotate_f(xl, xh, r.cs[0], r.cs[1], r.sn[0], r.sn[1], ol, oh);
+    const bool vlane = tl.r16 == kLaneV, klane = tl.r16 == kLaneK;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ol[j] = vlane ? xl[j] : ol[j];
+      oh[j] = vlane ? xh[j] : oh[j];
+    }
+    rope_narrow(ol, oh, pt.lo, pt.hi);
+    const bool qlive = pv && tl.r16 < group;
+    const u32x4 z{0u, 0u, 0u, 0u};
+    q0 = qlive ? pt.lo : z;
+    q1 = qlive ? pt.hi : z;
+    pt.col = (store_ok && srow == crow) ? sidx : -1;
+    const bool w0 = w == 0;
+    const int64_t kvo = (int64_t)(store_ok ? srow : 0) * s_kb + (int64_t)kh * s_kh + (int64_t)sidx * 64;
+    skr = make_rsrc_wave(kc + kvo, store_ok ? 128u : 0u);
+    svr = make_rsrc_wave(vc + kvo, store_ok ? 128u : 0u);
+    const bool qw = si.qo != nullptr && pv;
+    sqr = make_rsrc_wave(si.qo + (int64_t)(qw ? row : 0) * si.s_qo_r + (int64_t)kh * group * si.s_qo_h,
+                         qw ? (uint32_t)((group - 1) * si.s_qo_h * 2 + 128) : 0u);
+    sko = (w0 && klane) ? og : kOOR;
+    svo = (w0 && vlane) ? og : kOOR;
+    sqo = (w0 && tl.r16 < group) ? (uint32_t)(tl.r16 * si.s_qo_h * 2) + og : kOOR;
+#pragma unroll
+    for (int j = 1; j < D; ++j) first_load(j);
+  } else {
+    // unfused: the first tiles go out over the whole cache row before the length returns; the range is
+    // narrowed after them
+    const rsrc_t qr = make_rsrc(q + (int64_t)row * s_qb + (int64_t)kh * group * s_qh, (uint32_t)(group * s_qh * 2));
+    const uint32_t qo = (uint32_t)(tl.r16 * s_qh * 2) + 16u * tl.g;
+    q0 = bld16(qr, qo);
+    q1 = bld16(qr, qo + 64u);
+    resolve(false);
+#pragma unroll
+    for (int j = 0; j < D; ++j) first_load(j);
+    resolve(true);
+  }
+
+  SoftmaxState S;
+  S.reset();
+  auto step = [&](KTile(&X)[1], uint16_t *xv, int j) __attribute__((always_inline)) {
+    const int t0 = 64 * tile_of(j);
+    if (t0 < hi) compute_step<1, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
+    if (j + D < SPW) load_step<1>(X, xv, kr, vr, (uint32_t)(64 * tile_of(j + D)), tl);
+  };
+#pragma unroll
+  for (int j = 0; j < SPW; ++j) {
+    if (j & 1)
+      step(T1, vbw[1], j);
+    else
+      step(T0, vbw[0], j);
+  }
+  if (FUSED) {  // the unit's k / v / q, after its last step (as k_decode_rows)
+    bst16(skr, sko, pt.lo);
+    bst16(skr, sko + 64u, pt.hi);
+    bst16(svr, svo, pt.lo);
+    bst16(svr, svo + 64u, pt.hi);
+    bst16(sqr, sqo, pt.lo);
+    bst16(sqr, sqo + 64u, pt.hi);
+  }
+
+  // ---- park (m, l, O) in this wave's first V buffer (free by now); the four waves merge a slice each ----
+  park_partial(reinterpret_cast<float *>(vbw[0]), S, tl);
+  lds_barrier();
+  merge_units<NW>(reinterpret_cast<const float *>(vb0), nullptr, kVTile / 2, 1, row, kh, 0, 0, out, s_ob, s_oh, group,
+                  sl2, w, lane);
 }
 
 template <bool FUSED, int SPW>
@@ -388,8 +571,12 @@ static void launch_rows(int grid, hipStream_t st, const uint16_t *q, int64_t s_q
                         uint16_t *vc, int64_t s_kb, int64_t s_kh, int cache_rows, int cache_len, const int32_t *lens,
                         const int32_t *rowmap, uint16_t *out, int64_t s_ob, int64_t s_oh, int b, int nq, int nkv,
                         int group, float sl2, const StoreIn &si) {
-  hipLaunchKernelGGL((k_decode_rows<FUSED, SPW>), dim3(grid), dim3(64 * kRowsNW), 0, st, q, s_qb, s_qh, kc, vc, s_kb,
-                     s_kh, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, b, nq, nkv, group, sl2, si);
+  if (grid >= b * nkv)  // one unit per workgroup
+    hipLaunchKernelGGL((k_decode_unit<FUSED, SPW>), dim3(b * nkv), dim3(64 * kRowsNW), 0, st, q, s_qb, s_qh, kc, vc,
+                       s_kb, s_kh, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, b, nq, nkv, group, sl2, si);
+  else
+    hipLaunchKernelGGL((k_decode_rows<FUSED, SPW>), dim3(grid), dim3(64 * kRowsNW), 0, st, q, s_qb, s_qh, kc, vc,
+                       s_kb, s_kh, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, b, nq, nkv, group, sl2, si);
 }
 
 // Launches k_decode_rows when it serves the shape (whole rows per chunk at 4 waves x 1 tile per step, at
