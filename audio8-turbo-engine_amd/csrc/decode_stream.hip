@@ -567,12 +567,16 @@ extern "C" int a8_store_decode_stream(const void *qkv, int64_t s_qkv, const void
                       grid, scale, phases, si, stream);
 }
 
-// Launch shape of a8_decode_attn_stream. Measured on MI355X (C3, 384 units of 2048 keys): whole-unit
-// chunks swept by 192 workgroups of 4 waves (2 units each, 37.6 us/layer) beat 256 workgroups (40.7,
-// uneven: some take 1 unit, some 2), 384 (one unit each: twice the concurrent streams) and short
-// chunks in address order (more merges). So: a workgroup target of 3/4 of the compute units, chunks
-// per unit only as many as needed to reach it (long rows of few units), and a grid that divides the
-// chunk count evenly. The workspace caps the chunk count per unit.
+// Launch shape of a8_decode_attn_stream. Whole rows of at most 32 tiles (the slow stack's 2048-position cache)
+// whose units (row, kv head) reach half the compute units take one workgroup of 4 waves per unit while the units
+// fit the compute units (k_decode_unit: every unit streams at once), else two units per workgroup up to twice the
+// compute units (k_decode_rows). Measured on MI355X at KV 2048, fused store + decode, us per layer: 128 units
+// (64 rows) 16.6 one per workgroup against 17.9 for the split kernel; 256 units 24.9 against 30.9 for two per
+// workgroup on 128; 288 units 31.5 two per workgroup against 35.9 one per workgroup (32 compute units then
+// hold two); 384 units (C3) 36.2-36.6 two per workgroup against 39.0 one per workgroup. Beyond that, and for
+// other row lengths: a workgroup target of 3/4 of the compute units, chunks per unit only as many as needed to
+// reach it (long rows of few units), and a grid that divides the chunk count evenly. The workspace caps the
+// chunk count per unit.
 extern "C" int a8_decode_choose_stream(int b, int nkv, int cache_len, int64_t cap_row_splits, int n_cu,
                                        int *waves_out, int *tpw_out, int *grid_out) {
   using namespace a8;
@@ -581,6 +585,12 @@ extern "C" int a8_decode_choose_stream(int b, int nkv, int cache_len, int64_t ca
   const int64_t tiles = cache_len > 0 ? (cache_len + 63) / 64 : 1;
   const int nw = tiles >= 8 ? 4 : tiles >= 4 ? 2 : 1;
   const int64_t units = (int64_t)b * nkv;
+  if (nw == 4 && tiles <= 32 && 2 * units >= n_cu && units <= 2 * (int64_t)n_cu) {
+    *waves_out = 4;
+    *tpw_out = (int)((tiles + 3) / 4);
+    *grid_out = (int)(units <= n_cu ? units : (units + 1) / 2);
+    return 0;
+  }
   const int64_t g0 = n_cu * 3 / 4 > 0 ? n_cu * 3 / 4 : 1;
   const int64_t p_want = (g0 + units - 1) / units;
   int64_t tpw = (tiles + nw * p_want - 1) / (nw * p_want);

@@ -136,9 +136,10 @@ class DecodeAttention:
         them itself (counters in self.counters); launch shape from a8_decode_choose_flat. Opt-in:
         measured on MI355X it does not beat the others at the engine's shapes (a row merged inside the
         launch pays its memory round trips while the KV stream fills the queues).
-      mode "auto" (default): "stream" when every workgroup of its grid gets at least two whole units
-        (row, kv head) of 1024+ keys -- the peak-load shape, where it is measured fastest; for the
-        fused store + decode (store_and_attend) also when rows are short (cache_len <= 512: one
+      mode "auto" (default): "stream" when the rows are whole units (row, kv head) of 1024+ keys that
+        either give every workgroup of the grid two of them -- the peak-load shape -- or, one per
+        workgroup, number at least half the compute units (tick buckets of 64-128 slots at KV 2048); for
+        the fused store + decode (store_and_attend) also when rows are short (cache_len <= 512: one
         workgroup per (row, kv head) holds the whole row, so the store, the decode and the merge take
         one launch); else "split"."""
 
@@ -244,7 +245,9 @@ class DecodeAttention:
             return False
         nw, tpw, grid = self.stream_shape(b, cache_len)
         whole = nw * tpw * 64 >= cache_len
-        return whole and b * self.nkv >= 2 * grid
+        units = b * self.nkv
+        # two whole units per workgroup, or one per workgroup once the units reach half the compute units
+        return whole and (units >= 2 * grid or (grid >= units and 2 * units >= self.n_cu))
 
     def store_and_attend(self, qkv, bias, cos_tab, sin_tab, pos, slot, q, kc, vc, lens, out, nsplit=1,
                          rowmap=None, ring=1 << 30, phases=3, write_q=True):

@@ -161,6 +161,32 @@ def cpu_baseline(w, budget_s):
             "sample": f"1 of {LAYERS} layers (store + decode, {b} slots, same inputs), {len(times)} reps, median"}
 
 
+BUCKETS = (1, 8, 16, 32, 64, 96, 128, 144, 160, 176, 192)
+
+
+def bucket_sweep(a8, torch, w, steps):
+    """The peak-load tick at every tick bucket of the reference (fast_engine.py:669-670: one graph per bucket
+    up to 192 slots, each with its own split count, 776): the first b slots of the C3 workload at KV 2048, 24
+    layers of the fused store + decode as one graph, the reference's split count passed as the lower bound.
+    µs per layer, GB/s and the fraction of HBM peak per bucket, with the schedule the call takes."""
+    from oracle import attn_ref as ref_counts  # byte counts only
+    st = w["st"]
+    res = {}
+    for b in BUCKETS:
+        qkv = [x[:b] for x in w["qkv"]]
+        outs = [o[:b] for o in w["outs"]]
+        nsplit = a8.ref_nsplit(b, NKV)
+        g = capture(torch, lambda: st.forward(qkv, w["bias"], w["pos"][:b], w["slot"][:b], w["lens"][:b],
+                                              nsplit=nsplit, rowmap=False, q=w["q"][:b], outs=outs, fuse=True))
+        us = time_median(torch, g, steps, 10) * 1e3 / LAYERS
+        del g
+        nbytes = ref_counts.decode_bytes(w["lens_h"][:b].tolist(), NQ, NKV, HD)
+        kind, shape = st.attn.schedule(b, w["S"], nsplit, fused=True)
+        res[str(b)] = {"us_per_layer": round(us, 3), "GB/s": round(nbytes / us / 1e3, 1),
+                       "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "schedule": [kind, list(shape)]}
+    return res
+
+
 def per_config(a8, torch, dev, steps):
     """µs per layer (per pass at C5), achieved GB/s or TFLOP/s and the roofline fraction of the other benchmark
     configs, each timed as a captured graph (median of 5 runs). Decode configs: store + decode per layer, the
@@ -651,9 +677,11 @@ def main():
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     if not args.no_configs:
+        buckets = bucket_sweep(a8, torch, w, args.steps)
         del st, w
         torch.cuda.empty_cache()
         line["per_config"] = per_config(a8, torch, dev, args.steps)
+        line["per_config"]["buckets_kv2048"] = buckets
     print(json.dumps(line), flush=True)
 
 
