@@ -471,13 +471,22 @@ constexpr int kMaxDevices = 64;
 static float *g_scratch_dev[kMaxDevices];
 static std::mutex g_scratch_mu;
 
-// The current device's copy of `scratch` (looked up once per device), or nullptr with the error recorded.
-static float *scratch_on_current_device(const char *fn) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+// The copy of `scratch` on the device that `stream` belongs to (the current device for the null stream),
+// looked up once per device with that device current, or nullptr with the error recorded.
+static float *scratch_for_stream(const char *fn, hipStream_t stream) {
+  int cur = -1, dev = -1;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) {
     set_error(A8_EINVAL, "%s: hipGetDevice failed (%d)", fn, (int)e);
     return nullptr;
+  }
+  dev = cur;
+  if (stream) {
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) {
+      set_error(A8_EINVAL, "%s: hipStreamGetDevice failed (%d)", fn, (int)e);
+      return nullptr;
+    }
   }
   if (dev < 0 || dev >= kMaxDevices) {
     set_error(A8_EUNSUP, "%s: device %d beyond the %d supported", fn, dev, kMaxDevices);
@@ -485,8 +494,14 @@ static float *scratch_on_current_device(const char *fn) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_dev[dev]) {
+    // hipGetSymbolAddress answers for the current device: make the stream's device current for the lookup
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+      set_error(A8_EINVAL, "%s: hipSetDevice(%d) failed (%d)", fn, dev, (int)e);
+      return nullptr;
+    }
     void *p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) hipSetDevice(cur);
     if (e != hipSuccess || !p) {
       set_error(A8_EINVAL, "%s: hipGetSymbolAddress(scratch) failed on device %d (%d)", fn, dev, (int)e);
       return nullptr;
@@ -512,7 +527,7 @@ extern "C" int a8_decode_attn_noalloc(const void *q, int64_t s_qb, int64_t s_qh,
   if (b == 0) return 0;
   float *acc = nullptr, *ml = nullptr;
   int64_t row_splits = 0;
-  if (nsplit > 1) {
+  if (nsplit > 1 && hd == 64) {  // head_dim 128 takes the generic-head kernel, which uses no partials
     // every (row, head, split) partial the combine reads is written by the split kernel first: nothing in
     // the array has to start at zero
     const int64_t parts = (int64_t)b * nq * nsplit;
@@ -521,7 +536,7 @@ extern "C" int a8_decode_attn_noalloc(const void *q, int64_t s_qb, int64_t s_qh,
       return set_error(A8_EWSPACE, "%s: b*nq*nsplit*(hd+2) = %lld floats exceed the fixed %lld-float scratch "
                        "(8 MiB); use a8_decode_attn with a caller workspace", fn, (long long)need,
                        (long long)kScratchFloats);
-    float *base = scratch_on_current_device(fn);
+    float *base = scratch_for_stream(fn, (hipStream_t)stream);
     if (!base) return A8_EINVAL;
     acc = base;
     ml = base + parts * hd;  // parts * hd floats in: a multiple of 64 floats, 256-byte aligned
@@ -530,5 +545,5 @@ extern "C" int a8_decode_attn_noalloc(const void *q, int64_t s_qb, int64_t s_qh,
   const StoreIn none{};
   return split_entry(fn, q, s_qb, s_qh, const_cast<void *>(kc), const_cast<void *>(vc), s_kb, s_kh, s_ks,
                      cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, acc, ml, row_splits, nullptr, 0, b, nq,
-                     nkv, hd, nsplit, waves, scale, 3, none, stream);
+                     nkv, hd, hd == 64 ? nsplit : 1, waves, scale, 3, none, stream);
 }

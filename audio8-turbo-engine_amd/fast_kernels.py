@@ -723,8 +723,15 @@ class GemmDispatch:
             dev = next(iter(shapes.values()))[0].device
             self.ws = torch.zeros(need, dtype=torch.uint8, device=dev)  # the tile counters start at zero
 
+    @staticmethod
+    def _operands_ok(x, w):
+        """gemm_small's operand layout: 2-D, unit column strides, 16-byte aligned rows (pointers and row
+        strides); anything else takes torch.matmul, as the reference's mm would."""
+        return (x.dim() == 2 and w.dim() == 2 and x.stride(1) == 1 and w.stride(1) == 1
+                and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0 and w.stride(0) % 8 == 0)
+
     def __call__(self, x, w):
-        if not self.enabled or x.dim() != 2 or x.stride(1) != 1:
+        if not self.enabled or not self._operands_ok(x, w):
             return torch.matmul(x, w.t())
         best = self.small.get((x.shape[0], w.shape[0], w.shape[1]))
         if best is None:
@@ -737,8 +744,8 @@ class GemmDispatch:
         activation runs in its epilogue (gemm_silu_small, same bits, one launch and no [M, 2I] round trip);
         otherwise the product, then silu_mul."""
         key = (x.shape[0], w13.shape[0], w13.shape[1])
-        best = self.small.get(key) if self.enabled and x.dim() == 2 else None
-        if best is not None and best[0] == 1 and x.stride(1) == 1:
+        best = self.small.get(key) if self.enabled and self._operands_ok(x, w13) else None
+        if best is not None and best[0] == 1:
             return gemm_silu_small(x, w13, mblocks=self.gated_best.get(key, best)[1])
         return silu_mul(self(x, w13))
 
@@ -866,8 +873,9 @@ def conv_out_tanh(x, state, a, ib, w, bias, out):
           state.shape[2] == Cin and state.stride(-1) == 1, "state must be float16 [>=B, taps - 1, Cin]")
     _need(out.dtype == torch.float32 and out.dim() == 2 and out.shape[0] == B and out.shape[1] == T and
           out.stride(-1) == 1, "out must be float32 [B, T]")
-    _need(a.dtype == torch.float32 and ib.dtype == torch.float32 and a.is_contiguous() and ib.is_contiguous(),
-          "a / ib must be contiguous float32 vectors")
+    _need(a.dtype == torch.float32 and ib.dtype == torch.float32 and a.is_contiguous() and ib.is_contiguous()
+          and a.numel() >= Cin and ib.numel() >= Cin, f"a / ib must be contiguous float32 vectors of >= {Cin}")
+    _need(bias is None or (bias.dtype == _F16 and bias.numel() >= 1), "bias must be None or float16 [1]")
     _check_device(x=x, state=state, w=w, out=out, a=a, ib=ib, bias=bias)
     st = _lib.load().a8_conv_out_tanh(
         x.data_ptr(), x.stride(0), x.stride(1), state.data_ptr(), state.stride(0), state.stride(1), a.data_ptr(),

@@ -67,7 +67,8 @@ class SlowStack:
         # products, its weight folded into theirs -- two launches fewer per layer, within bf16 rounding noise of
         # the reference's rmsnorm -> product sequence
         self.fuse_norm = False
-        self._folded = None
+        self._folded = None  # built on the first norm-fused step and kept (refold() rebuilds it)
+        self._shapes_ok = None
         self._ss = None
         # prefetch_w13 (norm-fused steps): the o projection's launch carries extra workgroups that read the layer's
         # w13 weights once (gemm_small_norm prefetch), so the w13 product finds them in the memory-side cache
@@ -81,8 +82,33 @@ class SlowStack:
         self.kv_slices = 8
         self._sink = None
 
+    def _fused_shapes_ok(self):
+        """The shapes gemm_small_norm serves: the residual stream's sums of squares in hidden / 32 groups, at
+        most 32 and a multiple of 4, every product's K a multiple of 64, the gated w13 a multiple of 16 rows.
+        Other models take the unfused path."""
+        hidden = self.norm.shape[0]
+        if hidden % 32 or not (4 <= hidden // 32 <= 32) or (hidden // 32) % 4:
+            return False
+        for L in self.layers:
+            for name in ("wqkv", "wo", "w13", "w2"):
+                if L[name].shape[1] % 64:
+                    return False
+            if L["w13"].shape[0] % 16:
+                return False
+        return True
+
+    def refold(self):
+        """Rebuilds the norm-folded weights (fold_norm of wqkv / w13 with their norm weights) the norm-fused steps
+        use. They are built on the first such step and kept: call this after changing any layer's wqkv, w13, ln1
+        or ln2 in place."""
+        self._folded = None
+
     def _fused_ready(self, R, plan):
         if not (self.fuse_norm and isinstance(self.mm, GemmDispatch) and plan is None and R <= self.FUSE_NORM_ROWS):
+            return False
+        if self._shapes_ok is None:
+            self._shapes_ok = self._fused_shapes_ok()
+        if not self._shapes_ok:
             return False
         hidden = self.norm.shape[0]
         if self._folded is None:

@@ -13,9 +13,11 @@ builds [state, snake(x)] and conv_cl reads it, and the state keeps the last ctx 
 CLDecoder (fast_engine.py:276-310): conv_in, then per block [snake + transposed conv, 3 residual units
 (snake, dilated conv k, snake, 1x1 conv, + input)], snake + conv_out (one channel), tanh. The reference's
 fused residual unit (_FusedRU, on for the widths TTS_VOC_FUSED_RU names) is FusedRU here, on ru_cl, and
-`fused_ru` names its widths (ru_cl takes 96, 192 and 384; default 96 and 192, where it measured faster; () keeps every unit as the two convs,
-the reference's default). The fused unit keeps the first conv's output in fp32 where the two convs round it
-to fp16, as the reference's does.
+`fused_ru` names its widths (ru_cl takes 96, 192 and 384). The default, (), keeps every unit as the two convs:
+the reference's default (TTS_VOC_FUSED_RU unset), bit for bit its rounding sequence. FusedRU.DEFAULT_WIDTHS (96
+and 192, where the fused unit measured faster; the benchmark's frame uses it) opts in. The fused unit keeps the
+first conv's output in fp32 where the two convs round it to fp16, as the reference's fused unit does, so it
+matches the two-conv decoder within fp16 rounding, not bit for bit.
 
 The checkpoint's decoder (its modeling file and weights) is absent offline: `decoder_weights` draws a synthetic
 decoder of a stated shape (default: a DAC-style 44.1 kHz decoder, 1024 -> 1536 channels, strides 8, 8, 4, 2,
@@ -165,7 +167,7 @@ class CLDecoder:
     weights; every conv's state is registered in `states` (per row, for snapshots / row resets). frame: the
     input rows a call takes (sizes each conv's split-K workspace once; the streaming decoder's frame is 4)."""
 
-    def __init__(self, wts, Bmax, dev, states=None, frame=4, fused_ru=FusedRU.DEFAULT_WIDTHS):
+    def __init__(self, wts, Bmax, dev, states=None, frame=4, fused_ru=()):
         self.states = states if states is not None else []
         fuse = set(int(c) for c in (fused_ru or ()))
         S = self.states

@@ -319,8 +319,11 @@ def per_config(a8, torch, dev, steps):
                 "projections, the residual RMSNorms, SiLU-mul); synthetic weights; projections on gemm_small "
                 "(its fastest shape per weight, timed at startup on the layers' weights) with the norms inside "
                 "them (SlowStack.fuse_norm: the o / w2 products add the residual and leave the norm's sums of "
-                "squares, the qkv / w13 products apply it, w13 with SiLU-mul in its epilogue); tune_us = "
-                "[library, chosen] per call"}
+                "squares, the qkv / w13 products apply it, w13 with SiLU-mul in its epilogue). Numerics: the "
+                "reference rounds rmsnorm's output to bf16 (twice) before each product; the fused products "
+                "scale their fp32 sums by 1 / rms and round the weight folded with the norm weight instead "
+                "(within bf16 noise of the reference order, not bit for bit; norms_separate keeps its order). "
+                "tune_us = [library, chosen] per call"}
     del g, st, wts, xbuf, mm
     torch.cuda.empty_cache()
 
@@ -364,7 +367,7 @@ def per_config(a8, torch, dev, steps):
     voc = import_module(a8.__name__ + ".vocoder")
     b, T = 192, 4
     wts = voc.decoder_weights(dev=dev, seed=21)
-    dec = voc.CLDecoder(wts, b, dev)
+    dec = voc.CLDecoder(wts, b, dev, fused_ru=voc.FusedRU.DEFAULT_WIDTHS)
     xf = torch.randn(b, T, 1024, generator=gen, device=dev).to(torch.float16)
     g = capture(torch, lambda: dec(xf, b))
     us = time_median(torch, g, max(steps // 5, 5), 3) * 1e3
@@ -405,7 +408,9 @@ def per_config(a8, torch, dev, steps):
                                           "note": "one residual unit, 192 rows x 1024 positions x 192 channels: "
                                                   "snake_cat + ru_cl + state copy vs the k=7 and 1x1 convs"},
                             "note": "one frame of the streaming decoder; synthetic DAC-style weights; residual "
-                                    "units of 96 / 192 channels fused (ru_cl), the 384 / 768-channel ones two convs"}
+                                    "units of 96 / 192 channels fused (ru_cl, opted in: the reference's default "
+                                    "and CLDecoder's are two convs, us_per_frame_two_conv_units; the fused unit "
+                                    "keeps the first conv's output in fp32), the 384 / 768-channel ones two convs"}
     del g, dec, dec2, wts, xf, xr
     torch.cuda.empty_cache()
 
@@ -511,7 +516,7 @@ def vocoder_probe(a8, torch, dev):
     from importlib import import_module
     voc = import_module(a8.__name__ + ".vocoder")
     b = 192
-    dec = voc.CLDecoder(voc.decoder_weights(dev=dev, seed=21), b, dev)
+    dec = voc.CLDecoder(voc.decoder_weights(dev=dev, seed=21), b, dev, fused_ru=voc.FusedRU.DEFAULT_WIDTHS)
     gen = torch.Generator(device=dev).manual_seed(5)
     xf = torch.randn(b, 4, 1024, generator=gen, device=dev).to(torch.float16)
     for _ in range(5):

@@ -122,10 +122,12 @@ int a8_decode_attn(const void *q, int64_t s_qb, int64_t s_qh,
  * in the reference: its DecodeAttention always owns a workspace (fast_kernels.py:256-269).
  * Same arguments, kernels and results (bit for bit) as a8_decode_attn with counters == NULL and
  * phases == 3; the split partials go to a fixed device array of A8_NOALLOC_SCRATCH_BYTES that the library
- * holds on each GPU until the process ends. Allocates nothing. nsplit > 1 needs
- * b * nq * nsplit * (hd + 2) * 4 <= A8_NOALLOC_SCRATCH_BYTES, else A8_EWSPACE. Every call on one GPU
- * shares that GPU's array: calls that overlap in time on one GPU (two streams, two host threads) race;
- * serialise them.
+ * holds on each GPU until the process ends; the array used is the one on the device `stream` belongs to
+ * (the current device for the null stream), looked up on that device's first call, which is best made
+ * outside graph capture. Allocates nothing. nsplit > 1 with hd 64 needs
+ * b * nq * nsplit * (hd + 2) * 4 <= A8_NOALLOC_SCRATCH_BYTES, else A8_EWSPACE (hd 128 uses no partials).
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on one GPU (two streams, two
+ * host threads) race; serialise them.
  */
 #define A8_NOALLOC_SCRATCH_BYTES (8ll << 20)
 int a8_decode_attn_noalloc(const void *q, int64_t s_qb, int64_t s_qh,

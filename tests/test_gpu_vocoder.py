@@ -49,7 +49,7 @@ def test_streaming_decoder_matches_whole_utterance(dev):
 def test_streaming_decoder_with_fused_units(dev):
     """A decoder whose blocks are 192 and 96 channels wide, so every residual unit runs fused (ru_cl): streaming
     chunks (shorter and longer than the units' contexts) reproduce the oracle's whole-utterance decode, and the
-    two-conv decoder (fused_ru=()) agrees with it as closely."""
+    two-conv decoder (the default, fused_ru=()) agrees with it as closely."""
     from oracle import conv_ref
     say("case: CLDecoder 64->384 ch, rates 2,2 (blocks of 192 / 96 channels: fused units), chunks 1,5,2 x 2 rows")
     voc = importlib.import_module("audio8-turbo-engine_amd.vocoder")
@@ -58,7 +58,7 @@ def test_streaming_decoder_with_fused_units(dev):
           "blocks": [(a.to(dev), w.to(dev), b.to(dev), s, [tuple(t.to(dev) if torch.is_tensor(t) else t for t in u)
                                                           for u in us]) for a, w, b, s, us in wts["blocks"]],
           "final": tuple(t.to(dev) for t in wts["final"])}
-    dec, dec2 = voc.CLDecoder(wd, 2, dev), voc.CLDecoder(wd, 2, dev, fused_ru=())
+    dec, dec2 = voc.CLDecoder(wd, 2, dev, fused_ru=voc.FusedRU.DEFAULT_WIDTHS), voc.CLDecoder(wd, 2, dev)
     assert all(fu is not None for _, us in dec.blocks for _, _, fu in us)
     assert all(fu is None for _, us in dec2.blocks for _, _, fu in us)
     g = torch.Generator().manual_seed(10)
