@@ -161,6 +161,24 @@ def cpu_baseline(w, budget_s):
             "sample": f"1 of {LAYERS} layers (store + decode, {b} slots, same inputs), {len(times)} reps, median"}
 
 
+def cpu_leg(fn, work, unit, budget_s, sample):
+    """The CPU oracle timed on the host cores (torch's intra-op threads): fn() repeated until budget_s is spent
+    (at least one rep, at least three when they are short), median. work: bytes (GB/s) or FLOPs (GFLOP/s) per
+    call."""
+    import torch
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while not times or (len(times) < 3 and times[0] < budget_s / 3) or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    model, ncpu = host_cpu()
+    return {"value": round(work / med / 1e9, 3), "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "us_per_call": round(med * 1e6, 1), "cpu_model": model, "os_cpu_count": ncpu, "reps": len(times),
+            "sample": sample}
+
+
 BUCKETS = (1, 8, 16, 32, 64, 96, 128, 144, 160, 176, 192)
 
 
@@ -187,12 +205,13 @@ def bucket_sweep(a8, torch, w, steps):
     return res
 
 
-def per_config(a8, torch, dev, steps):
+def per_config(a8, torch, dev, steps, cpu_budget=4.0):
     """µs per layer (per pass at C5), achieved GB/s or TFLOP/s and the roofline fraction of the other benchmark
     configs, each timed as a captured graph (median of 5 runs). Decode configs: store + decode per layer, the
     engine's calls (fused where the schedule allows). C4: store + packed prefill per layer, and the prefill
-    launch alone against the bf16 MFMA peak."""
-    from oracle import attn_ref as ref_counts  # byte / FLOP counts only
+    launch alone against the bf16 MFMA peak. With cpu_budget > 0, C1, C2, C4 and C5 also carry the CPU
+    oracle (the reference's semantics in torch on the host cores) timed on one layer / pass of the same inputs."""
+    from oracle import attn_ref as ref_counts  # byte / FLOP counts and the CPU-baseline legs
     import numpy as np
 
     res = {}
@@ -229,6 +248,18 @@ def per_config(a8, torch, dev, steps):
                     "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes_per_layer": nbytes,
                     "schedule": [kind, list(shape)], "rows": b, "kv_len": int(max(lens)),
                     "note": "latency bound" if cfg == "C1" else "store + decode per layer"}
+        if cpu_budget > 0:  # the CPU oracle on layer 0's inputs: store, then decode (C1: its whole layer)
+            kc_h, vc_h = st.kc[0].cpu(), st.vc[0].cpu()
+            qkv_h, bias_h, pos_h, slot_h = qkv[0].cpu(), bias[0].cpu(), pos.cpu(), slot.cpu()
+            cos_h, sin_h = ref_counts.rope_tables(10000.0, HD, S)
+
+            def cpu_layer():
+                qh = torch.empty(b, NQ, HD, dtype=torch.bfloat16)
+                ref_counts.bias_rope_store(qkv_h, bias_h, cos_h, sin_h, pos_h, slot_h, qh, kc_h, vc_h, NQ, NKV, HD)
+                ref_counts.decode_attention(qh, kc_h, vc_h, lens, nsplit=1)
+
+            res[cfg]["cpu_baseline"] = cpu_leg(cpu_layer, nbytes, "GB/s", cpu_budget,
+                                               f"1 of {layers} layers (store + decode, {b} rows, same inputs)")
         del g, st, qkv, outs
         torch.cuda.empty_cache()
 
@@ -261,6 +292,20 @@ def per_config(a8, torch, dev, steps):
     res["C5"] = {"us_per_pass_layer": round(us, 3), "passes": len(passes), "layers": layers, "rows": b,
                  "schedule": [list(st.attn.schedule(2 * b, S)), list(st.attn.schedule(b, S, fused=True))],
                  "note": "latency bound (<= 1 MB of KV per pass)"}
+    if cpu_budget > 0:  # the CPU oracle on one pass-layer: the 192-row pass at position 5 (lens 6), layer 0
+        pos5, slot5, lens5, _, nr5 = passes[4]
+        kc_h, vc_h = st.kc[0].cpu(), st.vc[0].cpu()
+        qkv_h, bias_h = qkvs[4][0].cpu(), bias[0].cpu()
+        cos_h, sin_h = ref_counts.rope_tables(10000.0, HD, 16)
+        pos_h, slot_h, lens_h = pos5.cpu(), slot5.cpu(), lens5.cpu()
+
+        def cpu_pass():
+            qh = torch.empty(nr5, NQ, HD, dtype=torch.bfloat16)
+            ref_counts.bias_rope_store(qkv_h, bias_h, cos_h, sin_h, pos_h, slot_h, qh, kc_h, vc_h, NQ, NKV, HD)
+            ref_counts.decode_attention(qh, kc_h, vc_h, lens_h, nsplit=1)
+
+        res["C5"]["cpu_baseline"] = cpu_leg(cpu_pass, ref_counts.decode_bytes(lens_h.tolist(), NQ, NKV, HD), "GB/s",
+                                            cpu_budget, "one pass-layer (192 rows at position 5, store + decode)")
     del g, st, qkvs, outs
     torch.cuda.empty_cache()
 
@@ -473,6 +518,20 @@ def per_config(a8, torch, dev, steps):
                  "frac_mfma_bf16": round(flops / us_pf / 1e6 / MFMA_BF16_TFLOPS, 4), "flops_per_layer": flops,
                  "rows": R, "blocks": plan.nblk,
                  "note": "store + prefill per layer; the prefill's fp32 softmax VALU work bounds it before MFMA does"}
+    if cpu_budget > 0:  # the CPU oracle on layer 0: store, then the packed prefill (prefix already in the caches)
+        kc_h, vc_h = st.kc[0].cpu(), st.vc[0].cpu()
+        qkv_h, bias_h, pos_h, slot_h = qkv[0].cpu(), bias[0].cpu(), pos.cpu(), slot.cpu()
+        cos_h, sin_h = ref_counts.rope_tables(10000.0, HD, S)
+        pl = ref_counts.prefill_plan(r0s, ns, list(range(nreq)), [p0] * nreq)
+
+        def cpu_prefill():
+            qh = torch.empty(R, NQ, HD, dtype=torch.bfloat16)
+            ref_counts.bias_rope_store(qkv_h, bias_h, cos_h, sin_h, pos_h, slot_h, qh, kc_h, vc_h, NQ, NKV, HD)
+            oh = torch.empty(R, NQ, HD, dtype=torch.bfloat16)
+            ref_counts.prefill_attention(qh, kc_h, vc_h, *pl, oh, NQ // NKV)
+
+        res["C4"]["cpu_baseline"] = cpu_leg(cpu_prefill, flops, "GFLOP/s", cpu_budget,
+                                            f"1 of {layers} layers (store + packed prefill, {R} rows, same inputs)")
     del g, st, qkv, outs
     torch.cuda.empty_cache()
     return res
@@ -685,7 +744,7 @@ def main():
         buckets = bucket_sweep(a8, torch, w, args.steps)
         del st, w
         torch.cuda.empty_cache()
-        line["per_config"] = per_config(a8, torch, dev, args.steps)
+        line["per_config"] = per_config(a8, torch, dev, args.steps, 0.0 if args.no_cpu_baseline else 4.0)
         line["per_config"]["buckets_kv2048"] = buckets
     print(json.dumps(line), flush=True)
 
