@@ -97,10 +97,11 @@ __device__ __forceinline__ u32x4 bld16(rsrc_t r, uint32_t off) {
 // 16 bytes from buffer offset voff + soff + IMM land at LDS address lds + IMM + 16 l (the immediate
 // moves both sides, soff only the buffer side). The range check covers voff + soff + IMM; lanes past
 // the range write zeros. lds must be wave-uniform (it goes to M0). Completion is counted in vmcnt.
+// CPOL: the instruction's cache-policy bits (2 = nt: non-temporal, for data read once).
 typedef __attribute__((address_space(3))) void lds_void_t;
-template <int IMM>
+template <int IMM, int CPOL = 0>
 __device__ __forceinline__ void bld16_lds(rsrc_t r, void *lds, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, voff, soff, IMM, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, voff, soff, IMM, CPOL);
 }
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane i supplies the address of 4 consecutive bf16 and
