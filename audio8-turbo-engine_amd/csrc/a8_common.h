@@ -56,6 +56,10 @@ __device__ __forceinline__ uint32_t silu_mul_bf16x2(uint32_t g2, uint32_t u2) {
 }
 
 __device__ __forceinline__ u32x4 ld16(const void *p) { return *reinterpret_cast<const u32x4 *>(p); }
+// 16-byte LDS read (ds_read_b128) from a generic pointer known to point into LDS.
+__device__ __forceinline__ u32x4 lds_ld16(const void *p) {
+  return *(const __attribute__((address_space(3))) u32x4 *)const_cast<void *>(p);
+}
 __device__ __forceinline__ void st16(void *p, u32x4 v) { *reinterpret_cast<u32x4 *>(p) = v; }
 __device__ __forceinline__ void st8(void *p, u32x2 v) { *reinterpret_cast<u32x2 *>(p) = v; }
 

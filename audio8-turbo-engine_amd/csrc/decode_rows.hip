@@ -63,17 +63,20 @@ struct RowUnit {
 
 }  // namespace
 
-// Per-wave partial of a finished unit as parked in LDS: m[16], l[16] (row sum over the lane groups), then O in
-// rows of kOb floats (q head r16 of the group, 64 dims).
-constexpr int kParkFloats = 32 + 16 * kOb;
+// Per-wave partial of a finished unit as parked in LDS: m[PR], l[PR] (row sum over the lane groups), then O in
+// rows of kOb floats (q head r16 < PR of the group, 64 dims). PR = 8 serves groups of up to 8 q heads (the
+// engine's 7) in half the space.
+template <int PR>
+constexpr int park_floats() { return 2 * PR + PR * kOb; }
 
+template <int PR>
 __device__ __forceinline__ void park_partial(float *r, const SoftmaxState &S, const TileLane &tl) {
   const float lsum = sum_over_groups(S.lsum);
-  if (tl.g == 0) {
+  if (tl.g == 0 && tl.r16 < PR) {
     r[tl.r16] = S.m;
-    r[16 + tl.r16] = lsum;
+    r[PR + tl.r16] = lsum;
   }
-  lds_store_4x16(r + 32 + tl.r16 * kOb + 4 * tl.g, S.o[0], S.o[1], S.o[2], S.o[3]);
+  if (PR == 16 || tl.r16 < PR) lds_store_4x16(r + 2 * PR + tl.r16 * kOb + 4 * tl.g, S.o[0], S.o[1], S.o[2], S.o[3]);
 }
 
 // Merges the NW parked partials of each of cnt (<= 2) units and writes the units' outputs. Wave partial v of
@@ -81,7 +84,7 @@ __device__ __forceinline__ void park_partial(float *r, const SoftmaxState &S, co
 // waves (item w * 64 + lane, then + NW * 64), so every wave of the workgroup merges a slice. Arithmetic of
 // k_decode_combine's merge with a running maximum taken over the NW partials at once, the division as a
 // multiplication by the hardware reciprocal.
-template <int NW>
+template <int NW, int PR>
 __device__ __forceinline__ void merge_units(const float *r0, const float *r1, int rstride, int cnt, int row0, int kh0,
                                             int row1, int kh1, uint16_t *out, int64_t s_ob, int64_t s_oh, int group,
                                             float sl2, int w, int lane) {
@@ -97,8 +100,8 @@ __device__ __forceinline__ void merge_units(const float *r0, const float *r1, in
     for (int v = 0; v < NW; ++v) {
       const float *rv = rb + v * rstride;
       mv[v] = rv[head];
-      lv[v] = rv[16 + head];
-      ov[v] = *reinterpret_cast<const f32x4 *>(rv + 32 + head * kOb + d4);
+      lv[v] = rv[PR + head];
+      ov[v] = *reinterpret_cast<const f32x4 *>(rv + 2 * PR + head * kOb + d4);
     }
     float M = kNegInf;
 #pragma unroll
@@ -131,13 +134,16 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
   constexpr int D = 2;
   warm_kernargs<232>();  // the explicit arguments above span 0x00-0xe7
   static_assert(SPW % D == 0 && SPW >= 4, "steps per unit");
-  // V tiles of the two pipeline buffers: separate arrays, so the compiler tells their DMA completions apart and
-  // waits only for the buffer it reads
+  // K and V tiles of the two pipeline buffers: separate arrays, so the compiler tells their DMA completions apart
+  // and waits only for the buffer it reads
+  __shared__ __attribute__((aligned(16))) uint16_t kb0[NW * kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t kb1[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vb0[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vb1[NW * kVTile];
-  // per-wave m, l, O of finished units, parked until MB of them are merged together
-  constexpr int MB = 2;
-  __shared__ __attribute__((aligned(16))) float mrg[MB][NW * kParkFloats];
+  // per-wave m, l, O of finished units (8 q heads), parked until MB of them are merged together
+  constexpr int MB = 2, PR = 8;
+  constexpr int PF = park_floats<PR>();
+  __shared__ __attribute__((aligned(16))) float mrg[MB][NW * PF];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -148,7 +154,10 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
 
   TileLane tl;
   tl.init(lane);
+  KLdsLane kl;
+  kl.init(lane);
   uint16_t *const vbw[2] = {vb0 + w * kVTile, vb1 + w * kVTile};
+  uint16_t *const kbw[2] = {kb0 + w * kVTile, kb1 + w * kVTile};
 
   // ---- metadata, inputs and the tile sources of unit i (i >= nmine: empty ranges, nothing is read) ----
   const rsrc_t lens_r = make_rsrc(lens, (uint32_t)b * 4u);
@@ -267,7 +276,6 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
 
   SoftmaxState S;
   S.reset();
-  KTile T0[1], T1[1];
   RowUnit cur, nxt;
   u32x4 qc0, qc1, qn0, qn1;
   KVPatch ptc, ptn;
@@ -283,7 +291,7 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
   auto finish = [&](const RowUnit &un) {
     const int n = nfin++;
     const int slot = n % MB;
-    park_partial(mrg[slot] + w * kParkFloats, S, tl);
+    park_partial<PR>(mrg[slot] + w * PF, S, tl);
     S.reset();
     if (slot == 0) {
       prow0 = un.row;
@@ -291,36 +299,31 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
     }
     if (slot == MB - 1 || n == nmine - 1) {
       lds_barrier();  // every wave has parked (loads of the next unit stay in flight)
-      merge_units<NW>(mrg[0], mrg[1], kParkFloats, slot + 1, prow0, pkh0, un.row, un.kh, out, s_ob, s_oh, group,
-                      sl2, w, lane);
+      merge_units<NW, PR>(mrg[0], mrg[1], PF, slot + 1, prow0, pkh0, un.row, un.kh, out, s_ob, s_oh, group, sl2,
+                          w, lane);
       if (n < nmine - 1) lds_barrier();  // the area is read before the next unit parks into it
     }
   };
 
   // ---- steps: compute tile j of the current unit from buffer j % D, then request into it tile j + D of the
   // unit, or tile j + D - SPW of the next (one load sequence, sources selected) ----
-  auto step = [&](KTile(&X)[1], uint16_t *xv, int j, bool reload) __attribute__((always_inline)) {
+  auto step = [&](uint16_t *xk, uint16_t *xv, int j, bool reload) __attribute__((always_inline)) {
     const int t0 = 64 * tile_of(cur.rot, j);
-    if (t0 < cur.hi) compute_step<1, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
+    if (t0 < cur.hi) {
+      KTile X[1];
+      read_k_tile(X[0], xk, kl);
+      compute_step<1, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
+    }
     if (reload) {
       const bool in_cur = j + D < SPW;
       const rsrc_t kr = in_cur ? cur.kr : nxt.kr, vr = in_cur ? cur.vr : nxt.vr;
       const int tt = in_cur ? tile_of(cur.rot, j + D) : tile_of(nxt.rot, j + D - SPW);
-      load_step<1>(X, xv, kr, vr, (uint32_t)(64 * tt), tl);
+      load_tile_kv(xk, xv, kr, vr, (uint32_t)(64 * tt), tl, kl);
     }
   };
-  auto step_k = [&](int j, bool reload) __attribute__((always_inline)) {
-    if (j & 1)
-      step(T1, vbw[1], j, reload);
-    else
-      step(T0, vbw[0], j, reload);
-  };
+  auto step_k = [&](int j, bool reload) __attribute__((always_inline)) { step(kbw[j & 1], vbw[j & 1], j, reload); };
   auto first_load = [&](int j) __attribute__((always_inline)) {
-    const uint32_t t0 = (uint32_t)(64 * tile_of(cur.rot, j));
-    if (j & 1)
-      load_step<1>(T1, vbw[1], cur.kr, cur.vr, t0, tl);
-    else
-      load_step<1>(T0, vbw[0], cur.kr, cur.vr, t0, tl);
+    load_tile_kv(kbw[j & 1], vbw[j & 1], cur.kr, cur.vr, (uint32_t)(64 * tile_of(cur.rot, j)), tl, kl);
   };
   constexpr int kRopeStep = D < SPW - 1 ? D : SPW - 1;  // the next unit's inputs have arrived by then
 
@@ -412,6 +415,8 @@ __global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
   constexpr int D = 2;  // tiles in flight per wave
   warm_kernargs<232>();
   static_assert(SPW % D == 0 && SPW >= 4, "steps per unit");
+  __shared__ __attribute__((aligned(16))) uint16_t kb0[NW * kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t kb1[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vb0[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vb1[NW * kVTile];
 
@@ -423,7 +428,10 @@ __global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
 
   TileLane tl;
   tl.init(lane);
+  KLdsLane kl;
+  kl.init(lane);
   uint16_t *const vbw[2] = {vb0 + w * kVTile, vb1 + w * kVTile};
+  uint16_t *const kbw[2] = {kb0 + w * kVTile, kb1 + w * kVTile};
 
   // ---- metadata: row map, length, position, slot (vector loads, in order with the tiles) ----
   const rsrc_t lens_r = make_rsrc(lens, (uint32_t)b * 4u);
@@ -453,13 +461,8 @@ __global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
   // wave w: tiles w, w + NW, ... of the unit, starting at step u % SPW (as k_decode_rows)
   const int rot = u & (SPW - 1);
   auto tile_of = [&](int j) { return w + NW * ((j + rot) & (SPW - 1)); };
-  KTile T0[1], T1[1];
   auto first_load = [&](int j) __attribute__((always_inline)) {
-    const uint32_t t0 = (uint32_t)(64 * tile_of(j));
-    if (j & 1)
-      load_step<1>(T1, vbw[1], kr, vr, t0, tl);
-    else
-      load_step<1>(T0, vbw[0], kr, vr, t0, tl);
+    load_tile_kv(kbw[j & 1], vbw[j & 1], kr, vr, (uint32_t)(64 * tile_of(j)), tl, kl);
   };
 
   u32x4 q0, q1;
@@ -538,18 +541,17 @@ __global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
 
   SoftmaxState S;
   S.reset();
-  auto step = [&](KTile(&X)[1], uint16_t *xv, int j) __attribute__((always_inline)) {
+  auto step = [&](uint16_t *xk, uint16_t *xv, int j) __attribute__((always_inline)) {
     const int t0 = 64 * tile_of(j);
-    if (t0 < hi) compute_step<1, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
-    if (j + D < SPW) load_step<1>(X, xv, kr, vr, (uint32_t)(64 * tile_of(j + D)), tl);
+    if (t0 < hi) {
+      KTile X[1];
+      read_k_tile(X[0], xk, kl);
+      compute_step<1, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
+    }
+    if (j + D < SPW) load_tile_kv(xk, xv, kr, vr, (uint32_t)(64 * tile_of(j + D)), tl, kl);
   };
 #pragma unroll
-  for (int j = 0; j < SPW; ++j) {
-    if (j & 1)
-      step(T1, vbw[1], j);
-    else
-      step(T0, vbw[0], j);
-  }
+  for (int j = 0; j < SPW; ++j) step(kbw[j & 1], vbw[j & 1], j);
   if (FUSED) {  // the unit's k / v / q, after its last step (as k_decode_rows)
     bst16(skr, sko, pt.lo);
     bst16(skr, sko + 64u, pt.hi);
@@ -560,10 +562,10 @@ __global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
   }
 
   // ---- park (m, l, O) in this wave's first V buffer (free by now); the four waves merge a slice each ----
-  park_partial(reinterpret_cast<float *>(vbw[0]), S, tl);
+  park_partial<16>(reinterpret_cast<float *>(vbw[0]), S, tl);
   lds_barrier();
-  merge_units<NW>(reinterpret_cast<const float *>(vb0), nullptr, kVTile / 2, 1, row, kh, 0, 0, out, s_ob, s_oh, group,
-                  sl2, w, lane);
+  merge_units<NW, 16>(reinterpret_cast<const float *>(vb0), nullptr, kVTile / 2, 1, row, kh, 0, 0, out, s_ob, s_oh,
+                      group, sl2, w, lane);
 }
 
 template <bool FUSED, int SPW>
@@ -586,6 +588,7 @@ bool rows_launch(int grid, hipStream_t st, const uint16_t *q, int64_t s_qb, int6
                  uint16_t *out, int64_t s_ob, int64_t s_oh, int b, int nq, int nkv, int group, float sl2,
                  const StoreIn &si) {
   const bool fused = si.qkv != nullptr;
+  if (grid < b * nkv && group > 8) return false;  // k_decode_rows parks 8 q heads per wave
   const int spw = (cache_len + 64 * kRowsNW - 1) / (64 * kRowsNW);
   const int SPW = spw <= 4 ? 4 : spw <= 8 ? 8 : spw <= 16 ? 16 : 0;
   if (SPW == 0 || spw < 2) return false;

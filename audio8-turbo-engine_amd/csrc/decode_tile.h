@@ -96,6 +96,68 @@ __device__ __forceinline__ void load_tile(KTile &T, uint16_t *vtile, rsrc_t kr, 
   bld16_lds<3072, A8_TILE_CPOL_V>(vr, hi, v1, 4096u);
 }
 
+// ---- K tiles in LDS (the whole-row decode kernels) ----
+// K, like V, goes into a wave-private LDS tile by DMA, whole 128-byte rows (8 rows per instruction) with the
+// non-temporal policy, and the A operands are read from there: the register loads of the S^T layout take each
+// row as two 64-byte halves, and streamed that way K cost ~0.5 us per layer more at the peak load (the halves
+// cannot be non-temporal). The 16-byte chunks of row r are permuted by chunk ^ kswz(r), so the 16 rows one
+// A-operand read touches per lane group fall in 8 distinct 16-byte bank groups per 8 lanes.
+__device__ __forceinline__ int kswz(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
+
+struct KLdsLane {
+  uint32_t kd[2];     // DMA source offset inside a tile for rows 8j + lane / 8: j even / odd (row bit 3)
+  uint32_t ko0, ko1;  // A-operand reads: row 8(r16/4) + r16%4, chunk g (dims 8g..) and 4 + g (32 + 8g..)
+  __device__ __forceinline__ void init(int lane) {
+    const int row8 = lane >> 3, ch8 = lane & 7;
+    kd[0] = (uint32_t)row8 * kRow + 16u * (uint32_t)(ch8 ^ (row8 & 3));
+    kd[1] = (uint32_t)row8 * kRow + 16u * (uint32_t)(ch8 ^ ((row8 & 3) | 4));
+    const int r16 = lane & 15, g = lane >> 4;
+    const int krow = 8 * (r16 >> 2) + (r16 & 3), kz = kswz(krow);
+    ko0 = (uint32_t)krow * kRow + 16u * (uint32_t)(g ^ kz);
+    ko1 = (uint32_t)krow * kRow + 16u * (uint32_t)((4 + g) ^ kz);
+  }
+};
+
+// Loads keys [t0, t0+64) of one (cache row, kv head): K into the LDS tile ktile, V into vtile (8 KB each, this
+// wave's), both non-temporal. Same range semantics as load_tile.
+__device__ __forceinline__ void load_tile_kv(uint16_t *ktile, uint16_t *vtile, rsrc_t kr, rsrc_t vr, uint32_t t0,
+                                             const TileLane &L, const KLdsLane &K) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS reads of the buffers done (see load_tile)
+  const uint32_t base = t0 * kRow;
+  const uint32_t a0 = base + K.kd[0], a1 = base + K.kd[1];
+  char *kl = reinterpret_cast<char *>(ktile), *kh = kl + 4096;
+  bld16_lds<0, 2>(kr, kl, a0, 0u);
+  bld16_lds<1024, 2>(kr, kl, a1, 0u);
+  bld16_lds<2048, 2>(kr, kl, a0, 0u);
+  bld16_lds<3072, 2>(kr, kl, a1, 0u);
+  bld16_lds<0, 2>(kr, kh, a0, 4096u);
+  bld16_lds<1024, 2>(kr, kh, a1, 4096u);
+  bld16_lds<2048, 2>(kr, kh, a0, 4096u);
+  bld16_lds<3072, 2>(kr, kh, a1, 4096u);
+  const uint32_t v0 = base + L.vd[0], v1 = base + L.vd[1];
+  char *lo = reinterpret_cast<char *>(vtile), *hi = lo + 4096;
+  bld16_lds<0, 2>(vr, lo, v0, 0u);
+  bld16_lds<1024, 2>(vr, lo, v1, 0u);
+  bld16_lds<2048, 2>(vr, lo, v0, 0u);
+  bld16_lds<3072, 2>(vr, lo, v1, 0u);
+  bld16_lds<0, 2>(vr, hi, v0, 4096u);
+  bld16_lds<1024, 2>(vr, hi, v1, 4096u);
+  bld16_lds<2048, 2>(vr, hi, v0, 4096u);
+  bld16_lds<3072, 2>(vr, hi, v1, 4096u);
+}
+
+// The S^T A operands of a K tile in LDS (load_tile_kv's layout) into registers, as load_tile leaves them.
+__device__ __forceinline__ void read_k_tile(KTile &T, const uint16_t *ktile, const KLdsLane &K) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const char *kp = reinterpret_cast<const char *>(ktile) + (32 * c + 4 * t) * kRow;
+      T.ka[c][t][0] = lds_ld16(kp + K.ko0);
+      T.ka[c][t][1] = lds_ld16(kp + K.ko1);
+    }
+}
+
 // Loads keys [t0, t0 + 64 NT) as NT tiles (V tiles consecutive in vbuf).
 template <int NT>
 __device__ __forceinline__ void load_step(KTile (&T)[NT], uint16_t *vbuf, rsrc_t kr, rsrc_t vr, uint32_t t0,
