@@ -45,8 +45,12 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     float *__restrict__ ml_ws, int32_t *__restrict__ counters, int nq, int nkv, int group, int ns, float scale_log2,
     StoreIn si) {
   warm_kernargs<256>();  // the explicit arguments above span 0x000-0x0ff and more
-  // V tiles of the two pipeline buffers (one per wave each); separate arrays, so the compiler tells
-  // their DMA completions apart and waits only for the buffer it reads.
+  // K and V tiles of the two pipeline buffers (one per wave each, load_tile_kv); separate arrays, so the
+  // compiler tells their DMA completions apart and waits only for the buffer it reads.
+  // (8 waves: K stays in registers, load_tile -- their K and V tiles would exceed the LDS)
+  constexpr bool KL = NW <= 4;
+  __shared__ __attribute__((aligned(16))) uint16_t kbA[KL ? NW * kVTile : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t kbB[KL ? NW * kVTile : 8];
   __shared__ __attribute__((aligned(16))) uint16_t vbA[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vbB[NW * kVTile];
   const int sp = blockIdx.x, kh = blockIdx.y, row = blockIdx.z;
@@ -70,6 +74,9 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   const rsrc_t kr = make_rsrc(kc + cbase, (uint32_t)hi * row_bytes);
   const rsrc_t vr = make_rsrc(vc + cbase, (uint32_t)hi * row_bytes);
   uint16_t *va = vbA + w * kVTile, *vb = vbB + w * kVTile;
+  uint16_t *ka = kbA + (KL ? w * kVTile : 0), *kb = kbB + (KL ? w * kVTile : 0);
+  KLdsLane kl;
+  kl.init(lane);
 
   // Software pipeline over the wave's tiles first + k * 64*NW, k = 0..n-1, two register buffers, the
   // loads one tile ahead. The first tile is requested before the q / qkv prologue, so its latency and
@@ -81,8 +88,17 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   constexpr int kStep = 64 * NW;
   const int first = lo + 64 * __builtin_amdgcn_readfirstlane(w);
   const int n = first < hi ? (hi - first + kStep - 1) / kStep : 0;
-  KTile A[1], B[1];
-  load_step<1>(A, va, kr, vr, (uint32_t)first, tl);
+  KTile A[1], B[1];  // K operands: the tile in flight (registers) or read from LDS before its step
+  auto load = [&](KTile &T, uint16_t *kt, uint16_t *vt, int t0) __attribute__((always_inline)) {
+    if constexpr (KL)
+      load_tile_kv(kt, vt, kr, vr, (uint32_t)t0, tl, kl);
+    else
+      load_tile(T, vt, kr, vr, (uint32_t)t0, tl);
+  };
+  auto kread = [&](KTile &T, const uint16_t *kt) __attribute__((always_inline)) {
+    if constexpr (KL) read_k_tile(T, kt, kl);
+  };
+  load(A[0], ka, va, first);
 
   // Q^T operand: column r16 = q head kh*group + r16 (zeros past the group).
   u32x4 qB0, qB1;
@@ -103,13 +119,16 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   S.reset();
 
   if (n > 0) {
-    load_step<1>(B, vb, kr, vr, (uint32_t)(first + kStep), tl);
+    load(B[0], kb, vb, first + kStep);
+    kread(A[0], ka);
     compute_step<1, FUSED>(A, va, first, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
     for (int k = 1; k < n; k += 2) {
-      load_step<1>(A, va, kr, vr, (uint32_t)(first + (k + 1) * kStep), tl);
+      load(A[0], ka, va, first + (k + 1) * kStep);
+      kread(B[0], kb);
       compute_step<1, FUSED>(B, vb, first + k * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
       if (k + 1 >= n) break;
-      load_step<1>(B, vb, kr, vr, (uint32_t)(first + (k + 2) * kStep), tl);
+      load(B[0], kb, vb, first + (k + 2) * kStep);
+      kread(A[0], ka);
       compute_step<1, FUSED>(A, va, first + (k + 1) * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
     }
   }
