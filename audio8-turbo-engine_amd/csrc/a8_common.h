@@ -108,6 +108,17 @@ __device__ __forceinline__ void bld16_lds(rsrc_t r, void *lds, uint32_t voff, ui
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)lds, 16, voff, soff, IMM, CPOL);
 }
 
+// s_waitcnt vmcnt(N), expcnt and lgkmcnt left at their maxima: at most N of this wave's vector-memory
+// operations (loads, stores, LDS DMA) still outstanding. They complete in issue order, so an operation is
+// done once N others are known to have been issued after it. Every read of LDS written by DMA waits this
+// way, with N counted at the call site: the compiler's own wait for LDS DMA has been seen missing (no
+// wait at all before the reads at a loop's head, for DMA issued in the previous iteration).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane i supplies the address of 4 consecutive bf16 and
 // lane j receives, in slot k, element j%4 of lane 4k + j/4's data. With lane i pointing at row
 // (r0 + i/4), columns c0 + 4(i%4).. of a row-major bf16 matrix, lane j receives column c0 + j of rows

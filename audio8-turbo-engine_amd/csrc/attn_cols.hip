@@ -186,6 +186,7 @@ __global__ __launch_bounds__(64 * kColWaves) void k_attn_cols(
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
     }
+    wait_vmcnt<4 * KS>();  // the V tile has landed (the tile's 4 KS K loads went out after its DMA)
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll

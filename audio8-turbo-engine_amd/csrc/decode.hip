@@ -45,8 +45,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
     float *__restrict__ ml_ws, int32_t *__restrict__ counters, int nq, int nkv, int group, int ns, float scale_log2,
     StoreIn si) {
   warm_kernargs<256>();  // the explicit arguments above span 0x000-0x0ff and more
-  // K and V tiles of the two pipeline buffers (one per wave each, load_tile_kv); separate arrays, so the
-  // compiler tells their DMA completions apart and waits only for the buffer it reads.
+  // K and V tiles of the two pipeline buffers (one per wave each, load_tile_kv). Each read waits for its
+  // tile's DMA with a counted vmcnt: the next tile's 16 requests are issued before the step.
   // (8 waves: K stays in registers, load_tile -- their K and V tiles would exceed the LDS)
   constexpr bool KL = NW <= 4;
   __shared__ __attribute__((aligned(16))) uint16_t kbA[KL ? NW * kVTile : 8];
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
       load_tile(T, vt, kr, vr, (uint32_t)t0, tl);
   };
   auto kread = [&](KTile &T, const uint16_t *kt) __attribute__((always_inline)) {
-    if constexpr (KL) read_k_tile(T, kt, kl);
+    if constexpr (KL) read_k_tile<16>(T, kt, kl);  // the next tile's 16 requests went out after it
   };
   load(A[0], ka, va, first);
 
@@ -121,15 +121,15 @@ __global__ __launch_bounds__(64 * NW, 2) void k_decode_split(
   if (n > 0) {
     load(B[0], kb, vb, first + kStep);
     kread(A[0], ka);
-    compute_step<1, FUSED>(A, va, first, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
+    compute_step<1, 16, FUSED>(A, va, first, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
     for (int k = 1; k < n; k += 2) {
       load(A[0], ka, va, first + (k + 1) * kStep);
       kread(B[0], kb);
-      compute_step<1, FUSED>(B, vb, first + k * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
+      compute_step<1, 16, FUSED>(B, vb, first + k * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
       if (k + 1 >= n) break;
       load(B[0], kb, vb, first + (k + 2) * kStep);
       kread(A[0], ka);
-      compute_step<1, FUSED>(A, va, first + (k + 1) * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
+      compute_step<1, 16, FUSED>(A, va, first + (k + 1) * kStep, hi, qB0, qB1, scale_log2, S, tl, lane, &pt);
     }
   }
   // The last request past the range still writes (zeros) into LDS when it returns: let it land

@@ -306,7 +306,7 @@ __global__ __launch_bounds__(64 * kFlatNW, 1) void k_decode_flat(
       fresh = false;
     }
     const int key0 = 64 * (t - cu.us);
-    if (key0 < cu.L) compute_step<1, FUSED>(X, xv, key0, cu.L, qc0, qc1, sl2, S, tl, lane, &pt);
+    if (key0 < cu.L) compute_step<1, 16, FUSED>(X, xv, key0, cu.L, qc0, qc1, sl2, S, tl, lane, &pt);
     if (!more || cross) {
       finish(cu, tn);
       S.reset();

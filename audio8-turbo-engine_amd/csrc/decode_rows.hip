@@ -134,8 +134,7 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
   constexpr int D = 2;
   warm_kernargs<232>();  // the explicit arguments above span 0x00-0xe7
   static_assert(SPW % D == 0 && SPW >= 4, "steps per unit");
-  // K and V tiles of the two pipeline buffers: separate arrays, so the compiler tells their DMA completions apart
-  // and waits only for the buffer it reads
+  // K and V tiles of the two pipeline buffers (each read waits for its tile's DMA with a counted vmcnt)
   __shared__ __attribute__((aligned(16))) uint16_t kb0[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t kb1[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vb0[NW * kVTile];
@@ -307,12 +306,20 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
 
   // ---- steps: compute tile j of the current unit from buffer j % D, then request into it tile j + D of the
   // unit, or tile j + D - SPW of the next (one load sequence, sources selected) ----
-  auto step = [&](uint16_t *xk, uint16_t *xv, int j, bool reload) __attribute__((always_inline)) {
+  // The tile read at step j had the next tile's 16 requests issued after it, except at the launch's very last
+  // step (`tail`: nothing requested after it); the reads wait for it with those counts (D = 2).
+  static_assert(D == 2, "wait counts assume one tile requested after the one read");
+  auto step = [&](uint16_t *xk, uint16_t *xv, int j, bool reload, bool tail) __attribute__((always_inline)) {
     const int t0 = 64 * tile_of(cur.rot, j);
     if (t0 < cur.hi) {
       KTile X[1];
-      read_k_tile(X[0], xk, kl);
-      compute_step<1, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
+      if (tail) {
+        read_k_tile<0>(X[0], xk, kl);
+        compute_step<1, 0, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
+      } else {
+        read_k_tile<16>(X[0], xk, kl);
+        compute_step<1, 16, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
+      }
     }
     if (reload) {
       const bool in_cur = j + D < SPW;
@@ -321,7 +328,9 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
       load_tile_kv(xk, xv, kr, vr, (uint32_t)(64 * tt), tl, kl);
     }
   };
-  auto step_k = [&](int j, bool reload) __attribute__((always_inline)) { step(kbw[j & 1], vbw[j & 1], j, reload); };
+  auto step_k = [&](int j, bool reload, bool tail) __attribute__((always_inline)) {
+    step(kbw[j & 1], vbw[j & 1], j, reload, tail);
+  };
   auto first_load = [&](int j) __attribute__((always_inline)) {
     load_tile_kv(kbw[j & 1], vbw[j & 1], cur.kr, cur.vr, (uint32_t)(64 * tile_of(cur.rot, j)), tl, kl);
   };
@@ -376,7 +385,7 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
         }
         mn = meta_load(i + 2);
       }
-      step_k(j, true);
+      step_k(j, true, false);
       if (FUSED && j == kRopeStep) rope_unit(nxt, true, mcur_p, mcur_s, rn, qn0, qn1, ptn, sdn);
     }
     // the unit's k / v / q go out after its last step (stored at its first step they cost ~0.45 us per layer at
@@ -393,9 +402,11 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
   }
   // ---- the last unit: no request past its last tile ----
 #pragma unroll
-  for (int j = 0; j < SPW; ++j) step_k(j, j + D < SPW);
+  for (int j = 0; j < SPW; ++j) step_k(j, j + D < SPW, j + 1 == SPW);
   if (FUSED) rope_store(ptc, sdc);
   finish(cur);
+  // tiles past a unit's length are requested but not read: let every DMA land before the wave ends
+  wait_vmcnt<0>();
 }
 
 // One unit (row, kv head) per workgroup, two workgroups per compute unit: the launch for grids of at least one
@@ -541,12 +552,19 @@ __global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
 
   SoftmaxState S;
   S.reset();
+  // tile j + 1 was requested after tile j, except for the last (wait counts as in k_decode_rows)
+  static_assert(D == 2, "wait counts assume one tile requested after the one read");
   auto step = [&](uint16_t *xk, uint16_t *xv, int j) __attribute__((always_inline)) {
     const int t0 = 64 * tile_of(j);
     if (t0 < hi) {
       KTile X[1];
-      read_k_tile(X[0], xk, kl);
-      compute_step<1, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
+      if (j + 1 == SPW) {
+        read_k_tile<0>(X[0], xk, kl);
+        compute_step<1, 0, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
+      } else {
+        read_k_tile<16>(X[0], xk, kl);
+        compute_step<1, 16, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
+      }
     }
     if (j + D < SPW) load_tile_kv(xk, xv, kr, vr, (uint32_t)(64 * tile_of(j + D)), tl, kl);
   };
@@ -561,7 +579,9 @@ __global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
     bst16(sqr, sqo + 64u, pt.hi);
   }
 
-  // ---- park (m, l, O) in this wave's first V buffer (free by now); the four waves merge a slice each ----
+  // ---- park (m, l, O) in this wave's first V buffer (free once every DMA has landed: tiles past the length
+  // are requested but not read); the four waves merge a slice each ----
+  wait_vmcnt<0>();
   park_partial<16>(reinterpret_cast<float *>(vbw[0]), S, tl);
   lds_barrier();
   merge_units<NW, 16>(reinterpret_cast<const float *>(vb0), nullptr, kVTile / 2, 1, row, kh, 0, 0, out, s_ob, s_oh,

@@ -43,8 +43,8 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
     float *__restrict__ ml_ws, int b, int nq, int nkv, int group, int tpw, int P,
     float sl2, StoreIn si) {
   warm_kernargs<264>();  // the explicit arguments above span 0x000-0x10f
-  // V tiles of the two pipeline buffers (NT per wave each); separate arrays, so the compiler tells
-  // their DMA completions apart and waits only for the buffer it reads.
+  // V tiles of the two pipeline buffers (NT per wave each). A step reads its tiles after a counted
+  // vmcnt wait: the next step's 16 NT requests are issued before it.
   __shared__ __attribute__((aligned(16))) uint16_t vbA[NW * NT * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vbB[NW * NT * kVTile];
   __shared__ __attribute__((aligned(16))) float mrg[2][NW * (32 + 16 * kOb)];  // per-wave m, l, O (x2)
@@ -309,8 +309,7 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
   int i = 0, j = 0;
   int hi = 0;
   bool fresh = true;  // cur's hi not refined yet
-  // always inlined: each call site then sees which V buffer (vbA or vbB) it reads and writes, so the
-  // compiler waits only for that buffer's DMA
+  // always inlined: each call site then sees which V buffer (vbA or vbB) it reads and writes
   auto step = [&](KTile (&X)[NT], uint16_t *xv, KTile (&Y)[NT], uint16_t *yv) __attribute__((always_inline)) -> bool {
     // request the tile after (i, j) into Y, then consume X
     const bool last_tile = (j + 1 == spw);
@@ -334,7 +333,7 @@ __global__ __launch_bounds__(64 * NW, (NT == 1 && !FUSED) ? 2 : 1) void k_decode
       fresh = false;
     }
     const int t0 = cur.lo + KS * (w + NW * j);
-    if (t0 < hi) compute_step<NT, FUSED>(X, xv, t0, hi, qc0, qc1, sl2, S, tl, lane, &pt);
+    if (t0 < hi) compute_step<NT, 16 * NT, FUSED>(X, xv, t0, hi, qc0, qc1, sl2, S, tl, lane, &pt);
     if (FUSED && j == 0) {
       // the next chunk's qkv rows go out now, a whole chunk ahead of their use, into the registers this
       // chunk's rows were just consumed from (no copy at the transition): requested at the chunk's last

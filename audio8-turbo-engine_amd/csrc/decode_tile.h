@@ -147,7 +147,12 @@ __device__ __forceinline__ void load_tile_kv(uint16_t *ktile, uint16_t *vtile, r
 }
 
 // The S^T A operands of a K tile in LDS (load_tile_kv's layout) into registers, as load_tile leaves them.
+// VW: vector-memory operations this wave has certainly issued after the tile's load_tile_kv (the later
+// tiles' requests; 16 per tile). Its K DMAs are the sequence's first 8, so they have landed at
+// vmcnt(VW + 8).
+template <int VW>
 __device__ __forceinline__ void read_k_tile(KTile &T, const uint16_t *ktile, const KLdsLane &K) {
+  wait_vmcnt<VW + 8>();
 #pragma unroll
   for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -236,13 +241,12 @@ struct StoreIn {
   int ring;
 };
 
-// Replaces key column pt.col (when it lies in [t0, t0 + 64 NT)) in the tiles: its K row in the four
-// lanes that hold it (ka[c][t][*] of lanes r16 = 4 (r / 8) + r % 4, r = column % 32; the k comes from
-// lane kLaneK of the same group by a shuffle), its V row in the LDS tile (chunks permuted as the DMA
-// placed them, written by the kLaneV lanes). The LDS write follows the tile's DMA.
+// Replaces key column pt.col (when it lies in [t0, t0 + 64 NT)) in the tiles. patch_k: its K row in the
+// four lanes that hold it (ka[c][t][*] of lanes r16 = 4 (r / 8) + r % 4, r = column % 32; the k comes
+// from lane kLaneK of the same group by a shuffle). patch_v: its V row in the LDS tile (chunks permuted
+// as the DMA placed them, written by the kLaneV lanes), after the tile's DMA has landed.
 template <int NT>
-__device__ __forceinline__ void patch_column(KTile (&T)[NT], uint16_t *vbuf, int t0, const KVPatch &pt,
-                                             const TileLane &L) {
+__device__ __forceinline__ void patch_k(KTile (&T)[NT], int t0, const KVPatch &pt, const TileLane &L) {
   const int kk = pt.col - t0;
   if (kk < 0 || kk >= 64 * NT) return;
   const int h = kk >> 6, r64 = kk & 63, cc = r64 >> 5, rr = r64 & 31;
@@ -265,23 +269,30 @@ __device__ __forceinline__ void patch_column(KTile (&T)[NT], uint16_t *vbuf, int
         T[hh].ka[c][t][0] = sel ? klo : T[hh].ka[c][t][0];
         T[hh].ka[c][t][1] = sel ? khi : T[hh].ka[c][t][1];
       }
-  if (L.r16 == kLaneV) {
-    const int s = (r64 & 3) ^ ((r64 >> 3) & 1);
-    uint16_t *row = vbuf + h * kVTile + r64 * 64;
-    st16(row + 8 * (L.g ^ (2 * s)), pt.lo);
-    st16(row + 8 * ((4 + L.g) ^ (2 * s)), pt.hi);
-  }
+}
+template <int NT>
+__device__ __forceinline__ void patch_v(uint16_t *vbuf, int t0, const KVPatch &pt, const TileLane &L) {
+  const int kk = pt.col - t0;
+  if (kk < 0 || kk >= 64 * NT || L.r16 != kLaneV) return;
+  const int h = kk >> 6, r64 = kk & 63;
+  const int s = (r64 & 3) ^ ((r64 >> 3) & 1);
+  uint16_t *row = vbuf + h * kVTile + r64 * 64;
+  st16(row + 8 * (L.g ^ (2 * s)), pt.lo);
+  st16(row + 8 * ((4 + L.g) ^ (2 * s)), pt.hi);
 }
 
 // Consumes keys [t0, min(t0 + 64 NT, hi)) of the NT tiles (K in T, V in vbuf; t0 < hi). Rows past hi
 // may hold anything: their scores are masked and their LDS value rows zeroed (0 * NaN would not be
 // 0). One softmax update covers all NT tiles. qB0 / qB1: Q^T operands (dims 8g.. and 32+8g..).
 // sl2 = scale * log2(e). With PATCH, key column pt.col takes the new K / V row first.
-template <int NT, bool PATCH = false>
+// VW: vector-memory operations this wave has certainly issued after the last DMA of the V tiles (the next
+// step's requests); every LDS access of the V tiles (patch, zeroed rows, operand reads) follows
+// s_waitcnt vmcnt(VW).
+template <int NT, int VW, bool PATCH = false>
 __device__ __forceinline__ void compute_step(KTile (&T)[NT], uint16_t *vbuf, int t0, int hi, u32x4 qB0,
                                              u32x4 qB1, float sl2, SoftmaxState &S, const TileLane &L,
                                              int lane, const KVPatch *pt = nullptr) {
-  if (PATCH) patch_column<NT>(T, vbuf, t0, *pt, L);
+  if (PATCH) patch_k<NT>(T, t0, *pt, L);
   f32x4 s[NT][2][2];
   const bool full = t0 + 64 * NT <= hi;
   float mt = kNegInf;
@@ -290,10 +301,7 @@ __device__ __forceinline__ void compute_step(KTile (&T)[NT], uint16_t *vbuf, int
     for (int h = 0; h < NT; ++h) mt = fmaxf(mt, tile_scores<false>(T[h], t0 + 64 * h, hi, qB0, qB1, s[h], L));
   } else {
 #pragma unroll
-    for (int h = 0; h < NT; ++h) {
-      mt = fmaxf(mt, tile_scores<true>(T[h], t0 + 64 * h, hi, qB0, qB1, s[h], L));
-      zero_rows(vbuf + h * kVTile, hi - (t0 + 64 * h), lane);
-    }
+    for (int h = 0; h < NT; ++h) mt = fmaxf(mt, tile_scores<true>(T[h], t0 + 64 * h, hi, qB0, qB1, s[h], L));
   }
   mt = max_over_groups(mt);
   const float mn = fmaxf(S.m, mt);
@@ -322,6 +330,12 @@ __device__ __forceinline__ void compute_step(KTile (&T)[NT], uint16_t *vbuf, int
   if (__ballot(alpha != 1.f)) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) S.o[dt] *= alpha;
+  }
+  wait_vmcnt<VW>();  // the V tiles have landed
+  if (PATCH) patch_v<NT>(vbuf, t0, *pt, L);
+  if (!full) {
+#pragma unroll
+    for (int h = 0; h < NT; ++h) zero_rows(vbuf + h * kVTile, hi - (t0 + 64 * h), lane);
   }
 #pragma unroll
   for (int h = 0; h < NT; ++h) {
