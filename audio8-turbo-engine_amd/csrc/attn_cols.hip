@@ -16,14 +16,16 @@
 //     wave-private LDS tile, row r's 16-byte chunks permuted by chunk ^= 2 (r & 3) (the permutation goes into
 //     the DMA's source offsets), so the transposing reads of four consecutive rows hit distinct banks; it is
 //     read as V^T by ds_read_b64_tr_b16, HD/16 row blocks of 16 dims.
-// Work is one wave per column group (four independent waves per workgroup); the kernel is not tuned like the
-// head_dim-64 paths: it is the generic-head fallback those entry points route to.
+// One wave per column group, NWV independent waves per workgroup. Decode: one wave per workgroup and two tile
+// buffers (PIPE), the next tile's K / V requests in flight while a tile is computed (four waves with one buffer
+// measured 105.8 us per layer at 192 rows x 2048 keys, 0.48 of HBM; this 73.4 us, 0.69). Prefill: four waves
+// per workgroup -- the four 16-row column groups of one (block, q head), whose K / V reads then meet in one
+// compute unit's cache -- and one buffer each (one-wave workgroups measured 237-240 us at C4 against 219 us).
 #include "decode_tile.h"
 
 namespace a8 {
 namespace {
 
-constexpr int kColWaves = 4;  // independent waves per workgroup
 
 // The column group of one wave: its columns' query / output rows, q heads and key counts (per lane), the
 // cache row and kv head (uniform), and the wave's largest and smallest key counts over its valid columns.
@@ -38,8 +40,8 @@ struct ColGroup {
   int L;            // this lane's key count
 };
 
-template <int HD>
-__global__ __launch_bounds__(64 * kColWaves) void k_attn_cols(
+template <int HD, bool PIPE, int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_attn_cols(
     const uint16_t *__restrict__ q, int64_t s_qr, int64_t s_qh, int R,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh,
     int cache_rows, int cache_len, uint16_t *__restrict__ out, int64_t s_or, int64_t s_oh,
@@ -52,12 +54,14 @@ __global__ __launch_bounds__(64 * kColWaves) void k_attn_cols(
   constexpr int DT = HD / 16;   // 16-dim row blocks of O^T
   constexpr int PITCH = HD * 2;  // bytes per key row of the LDS V tile
   constexpr int NCH = HD / 8;    // 16-byte chunks per key row
-  __shared__ __attribute__((aligned(16))) char vbuf[kColWaves][64 * PITCH];
+  // each wave's V tile buffers (two when PIPE; separate arrays)
+  __shared__ __attribute__((aligned(16))) char vbufA[NWV][64 * PITCH];
+  __shared__ __attribute__((aligned(16))) char vbufB[NWV][PIPE ? 64 * PITCH : 16];
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int r16 = lane & 15, g = lane >> 4;
-  const int gw = blockIdx.x * kColWaves + w;
-  if (gw >= ngroups) return;  // whole wave (waves of a workgroup never meet at a barrier)
-  char *vt = vbuf[w];
+  const int gw = blockIdx.x * NWV + w;
+  if (gw >= ngroups) return;  // whole wave (the waves of a workgroup never meet at a barrier)
+  char *vbA = vbufA[w], *vbB = vbufB[w];
 
   ColGroup cg{};
   if (!prefill) {
@@ -129,12 +133,15 @@ __global__ __launch_bounds__(64 * kColWaves) void k_attn_cols(
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int t0 = 0; t0 < cg.lmax; t0 += 64) {
-    // the V tile into LDS by DMA, K operands into registers
+  // PIPE: two tile buffers (V in LDS, K in registers), the next tile's loads in flight while one is computed;
+  // a request past lmax reads zeros without memory traffic. Otherwise one buffer, loads then compute.
+  u32x4 kA[2][2][KS], kB[2][2][KS];
+  auto load = [&](u32x4 (&ka)[2][2][KS], char *vtile, int t0) __attribute__((always_inline)) {
+    // every earlier read of this buffer done before its DMA can land
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
 #pragma unroll
     for (int i = 0; i < VDMA; ++i)
-      bld16_lds<0>(vr, vt + i * 1024, (uint32_t)t0 * kRowB + (uint32_t)i * 1024u + vsrc, 0u);
-    u32x4 ka[2][2][KS];
+      bld16_lds<0>(vr, vtile + i * 1024, (uint32_t)t0 * kRowB + (uint32_t)i * 1024u + vsrc, 0u);
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -142,6 +149,10 @@ __global__ __launch_bounds__(64 * kColWaves) void k_attn_cols(
 #pragma unroll
         for (int s = 0; s < KS; ++s)
           ka[c][t][s] = bld16(kr, ((uint32_t)t0 + 32u * c + krow + 4u * t) * kRowB + (uint32_t)(32 * s + 8 * g) * 2u);
+  };
+  // consumes the tile at t0 (K in ka, V in vtile); the V reads wait for its DMA: after it went out, its own
+  // 4 KS K loads, and with PIPE the next tile's VDMA + 4 KS requests
+  auto tile = [&](const u32x4 (&ka)[2][2][KS], const char *vtile, int t0) __attribute__((always_inline)) {
     // scores, masked per column where the tile reaches past some column's key count
     f32x4 sc[2][2];
     float mt = kNegInf;
@@ -186,18 +197,33 @@ __global__ __launch_bounds__(64 * kColWaves) void k_attn_cols(
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
     }
-    wait_vmcnt<4 * KS>();  // the V tile has landed (the tile's 4 KS K loads went out after its DMA)
+    wait_vmcnt<PIPE ? 8 * KS + VDMA : 4 * KS>();  // the V tile has landed
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const char *p = vt + (32 * c + 8 * g + vrr) * PITCH + ((((uint32_t)(2 * dt) + vc0) ^ vperm) << 4) + vhalf;
+        const char *p = vtile + (32 * c + 8 * g + vrr) * PITCH + ((((uint32_t)(2 * dt) + vc0) ^ vperm) << 4) + vhalf;
         const u32x2 lo = lds_tr16(p), hi2 = lds_tr16(p + 4 * PITCH);
         o[dt] = mfma16x16x32(u32x4{lo[0], lo[1], hi2[0], hi2[1]}, pB[c], o[dt]);
       }
-    // every lane's reads of the tile are done before the next tile's DMA overwrites it
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  };
+  if (PIPE) {
+    load(kA, vbA, 0);
+    for (int t0 = 0; t0 < cg.lmax; t0 += 128) {
+      load(kB, vbB, t0 + 64);
+      tile(kA, vbA, t0);
+      if (t0 + 64 >= cg.lmax) break;
+      load(kA, vbA, t0 + 128);
+      tile(kB, vbB, t0 + 64);
+    }
+  } else {
+    for (int t0 = 0; t0 < cg.lmax; t0 += 64) {
+      load(kA, vbA, t0);
+      tile(kA, vbA, t0);
+    }
   }
+  // the request past the last tile still writes (zeros) into LDS: let it land before the wave ends
+  wait_vmcnt<0>();
 
   // l = 0 (no key, decode lens = 0) gives 0 * inf = NaN, like the reference's 0 / 0
   const float rl = __builtin_amdgcn_rcpf(sum_over_groups(lsum));
@@ -224,8 +250,7 @@ int attn_cols_decode(const char *fn, const void *q, int64_t s_qb, int64_t s_qh, 
   if (ngroups > INT32_MAX / 2) return set_error(A8_EUNSUP, "%s: %d rows x %d kv heads too many", fn, b, nkv);
   if ((int64_t)cache_len * hd * 2 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "%s: cache of %d positions too long for 32-bit offsets", fn, cache_len);
-  const unsigned grid = (unsigned)((ngroups + kColWaves - 1) / kColWaves);
-  hipLaunchKernelGGL(k_attn_cols<128>, dim3(grid), dim3(64 * kColWaves), 0, stream, (const uint16_t *)q, s_qb, s_qh,
+  hipLaunchKernelGGL((k_attn_cols<128, true, 1>), dim3((unsigned)ngroups), dim3(64), 0, stream, (const uint16_t *)q, s_qb, s_qh,
                      b, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, cache_rows, cache_len,
                      (uint16_t *)out, s_ob, s_oh, lens, rowmap, nullptr, nullptr, nullptr, nullptr, (int)ngroups, nq,
                      nkv, group, false, scale * kLog2e);
@@ -240,11 +265,12 @@ int attn_cols_prefill(const void *q, int64_t s_qr, int64_t s_qh, int R, const vo
   if (hd != 128) return set_error(A8_EUNSUP, "prefill_attn: head_dim %d not supported (64 or 128)", hd);
   const int64_t ngroups = (int64_t)nblk * nq * 4;
   if (ngroups == 0) return 0;
+  constexpr int kPfWaves = 4;
   if (ngroups > INT32_MAX / 2) return set_error(A8_EUNSUP, "prefill_attn: %d blocks x %d heads too many", nblk, nq);
   if ((int64_t)cache_len * hd * 2 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "prefill_attn: cache of %d positions too long for 32-bit offsets", cache_len);
-  const unsigned grid = (unsigned)((ngroups + kColWaves - 1) / kColWaves);
-  hipLaunchKernelGGL(k_attn_cols<128>, dim3(grid), dim3(64 * kColWaves), 0, stream, (const uint16_t *)q, s_qr, s_qh,
+  hipLaunchKernelGGL((k_attn_cols<128, false, kPfWaves>), dim3((unsigned)((ngroups + kPfWaves - 1) / kPfWaves)),
+                     dim3(64 * kPfWaves), 0, stream, (const uint16_t *)q, s_qr, s_qh,
                      R, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, cache_rows, cache_len,
                      (uint16_t *)out, s_or, s_oh, nullptr, nullptr, bq0, bn, bslot, bpos0, (int)ngroups, nq,
                      nq / group, group, true, scale * kLog2e);

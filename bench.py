@@ -534,7 +534,113 @@ def per_config(a8, torch, dev, steps, cpu_budget=4.0):
                                             f"1 of {layers} layers (store + packed prefill, {R} rows, same inputs)")
     del g, st, qkv, outs
     torch.cuda.empty_cache()
+    res["hd128"] = hd128_configs(a8, torch, dev, steps, gen)
     return res
+
+
+def hd128_configs(a8, torch, dev, steps, gen):
+    """head_dim 128 (the fast AR's head width comes from its checkpoint, fast_engine.py:608, and 128 is the
+    other width the kernels serve): the C3 decode load, the C5 fast-AR passes and the C4 packed prefill at
+    head_dim 128 with the slow stack's 14 / 2 heads, 8 layers per graph. At this width the store is its own
+    launch (the fused store + decode kernels are head_dim 64) and every launch is k_attn_cols<128>. µs per
+    layer (per pass-layer), GB/s or TFLOP/s and the roofline fraction."""
+    from oracle import attn_ref as ref_counts  # byte / FLOP counts only
+    hd, layers = 128, 8
+    w128 = (NQ + 2 * NKV) * hd
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=gen, device=dev) * std).to(torch.bfloat16)
+
+    out = {}
+    # decode: 192 rows x KV 2048 (C3's load), store + decode per layer and the decode launch alone
+    b, S = 192, 2048
+    st = a8.AttnStack(layers, NQ, NKV, hd, 10000.0, max_rows=16 * b, cache_rows=b + 1, cache_len=S, max_pos=S,
+                      dev=dev)
+    for i in range(layers):
+        st.kc[i].normal_(generator=gen)
+        st.vc[i].normal_(generator=gen)
+    lens = torch.full((b,), S, dtype=torch.int32, device=dev)
+    pos, slot = lens - 1, torch.arange(b, dtype=torch.int32, device=dev)
+    qkv = [randn(b, w128) for _ in range(layers)]
+    bias = [randn(w128, std=0.02) for _ in range(layers)]
+    q = torch.empty(b, NQ, hd, dtype=torch.bfloat16, device=dev)
+    outs = [torch.empty(b, NQ, hd, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+    nsplit = a8.ref_nsplit(b, NKV)
+    g = capture(torch, lambda: st.forward(qkv, bias, pos, slot, lens, nsplit=nsplit, rowmap=False, q=q, outs=outs,
+                                          fuse=True))
+    us = time_median(torch, g, steps, 10) * 1e3 / layers
+    del g
+
+    def dec_only():
+        for i in range(layers):
+            st.attn(q, st.kc[i], st.vc[i], lens, outs[i], nsplit)
+
+    g = capture(torch, dec_only)
+    us_d = time_median(torch, g, steps, 10) * 1e3 / layers
+    del g
+    nb = ref_counts.decode_bytes([S] * b, NQ, NKV, hd)
+    nb_d = ref_counts.decode_bytes([S] * b, NQ, NKV, hd, with_store=False)
+    out["decode_192x2048"] = {"us_per_layer": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                              "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4), "bytes_per_layer": nb,
+                              "decode_us_per_layer": round(us_d, 3),
+                              "decode_frac_hbm": round(nb_d / us_d / 1e3 / HBM_PEAK_GBS, 4),
+                              "note": "store (k_bias_rope_store) + decode (k_attn_cols<128>, one workgroup per "
+                                      "16 query columns)"}
+    del st, qkv, outs
+    torch.cuda.empty_cache()
+    # fast-AR passes (C5's shape): 192 slots, cache 10, a 2-token pass then 8 one-token passes
+    b, S, nl = 192, 10, 4
+    st = a8.AttnStack(nl, NQ, NKV, hd, 10000.0, max_rows=4 * b, cache_rows=b, cache_len=S, max_pos=16, dev=dev,
+                      nsplit_max=1)
+    r = torch.arange(2 * b, dtype=torch.int32)
+    passes = [((r % 2).to(dev), (r // 2).to(dev), (r % 2 + 1).to(dev), True, 2 * b)]
+    for p in range(2, 10):
+        passes.append((torch.full((b,), p, dtype=torch.int32, device=dev), torch.arange(b, dtype=torch.int32,
+                       device=dev), torch.full((b,), p + 1, dtype=torch.int32, device=dev), False, b))
+    qkvs = [[randn(nr, w128) for _ in range(nl)] for (_, _, _, _, nr) in passes]
+    bias = [randn(w128, std=0.02) for _ in range(nl)]
+    q = torch.empty(2 * b, NQ, hd, dtype=torch.bfloat16, device=dev)
+    outs = [torch.empty(2 * b, NQ, hd, dtype=torch.bfloat16, device=dev) for _ in range(nl)]
+
+    def c5():
+        for (ps, sl, ln, rmap, nr), qk in zip(passes, qkvs):
+            st.forward(qk, bias, ps, sl, ln, nsplit=1, rowmap=rmap, q=q[:nr], outs=[o[:nr] for o in outs],
+                       fuse=not rmap)
+
+    g = capture(torch, c5)
+    us = time_median(torch, g, steps, 10) * 1e3 / (len(passes) * nl)
+    del g, st, qkvs, outs
+    torch.cuda.empty_cache()
+    out["fast_ar_passes"] = {"us_per_pass_layer": round(us, 3), "passes": len(passes), "layers": nl, "rows": b,
+                             "note": "C5's passes at head_dim 128: store + decode per pass-layer, latency bound"}
+    # packed prefill at C4's shape
+    import numpy as np
+    ns = torch.randint(40, 401, (64,), generator=torch.Generator().manual_seed(0)).tolist()
+    p0, nreq = 300, 64
+    R, S = sum(ns), 704
+    st = a8.AttnStack(layers, NQ, NKV, hd, 10000.0, max_rows=8192, cache_rows=nreq + 1, cache_len=S, max_pos=S,
+                      dev=dev)
+    for i in range(layers):
+        st.kc[i].normal_(generator=gen)
+        st.vc[i].normal_(generator=gen)
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    plan = a8.PrefillPlan(r0s, ns, list(range(nreq)), [p0] * nreq, dev)
+    q = randn(R, NQ, hd)
+    outs = [torch.empty(R, NQ, hd, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+
+    def pf_only():
+        for i in range(layers):
+            a8.prefill_attention(q, st.kc[i], st.vc[i], plan, outs[i], NQ // NKV)
+
+    g = capture(torch, pf_only)
+    us_pf = time_median(torch, g, steps, 10) * 1e3 / layers
+    del g, st, outs
+    torch.cuda.empty_cache()
+    flops = ref_counts.prefill_flops(ns, [p0] * nreq, NQ, hd)
+    out["prefill_c4"] = {"us_per_layer": round(us_pf, 3), "TFLOP/s": round(flops / us_pf / 1e6, 1),
+                         "frac_mfma_bf16": round(flops / us_pf / 1e6 / MFMA_BF16_TFLOPS, 4), "flops_per_layer": flops,
+                         "note": "C4's 64 requests after a 300-position prefix, packed prefill alone"}
+    return out
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c3_traffic.md")
