@@ -554,33 +554,8 @@ __global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
   S.reset();
   // tile j + 1 was requested after tile j, except for the last (wait counts as in k_decode_rows)
   static_assert(D == 2, "wait counts assume one tile requested after the one read");
-#ifndef A8_UNIT_EARLY_K
-#define A8_UNIT_EARLY_K 0
-#endif
   auto step = [&](uint16_t *xk, uint16_t *xv, int j) __attribute__((always_inline)) {
     const int t0 = 64 * tile_of(j);
-    if (A8_UNIT_EARLY_K) {
-      // the K half of tile j + 2 goes out as soon as tile j's K operands are in registers, the V half after
-      // its P.V reads: DMA issued after V(j) at the V reads is K(j+1), V(j+1), K(j+2)
-      KTile X[1];
-      if (t0 < hi) {
-        if (j + 1 < SPW)
-          read_k_tile<16>(X[0], xk, kl);
-        else
-          read_k_tile<0>(X[0], xk, kl);
-      }
-      if (j + D < SPW) load_k_lds(xk, kr, (uint32_t)(64 * tile_of(j + D)), kl);
-      if (t0 < hi) {
-        if (j + 2 < SPW)
-          compute_step<1, 24, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
-        else if (j + 1 < SPW)
-          compute_step<1, 16, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
-        else
-          compute_step<1, 0, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
-      }
-      if (j + D < SPW) load_v_lds(xv, vr, (uint32_t)(64 * tile_of(j + D)), tl);
-      return;
-    }
     if (t0 < hi) {
       KTile X[1];
       if (j + 1 == SPW) {
