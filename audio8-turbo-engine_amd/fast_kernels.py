@@ -619,7 +619,9 @@ class GemmDispatch:
     chooses between cuBLAS and tuned Triton configs the same way). `tune(weights, Ms)` times both (with each
     split count) for every weight shape and token count; `__call__(x, w)` then takes the faster, and the
     library GEMM for shapes not tuned. The split partials share one workspace sized by tune (calls on one
-    instance run in stream order)."""
+    instance run in stream order). Prefill-sized M (over 192 rows) always takes the library GEMM: tune records
+    its time at `large_m` rows per shape. With `cache_path`, results persist in a JSON file keyed by GPU, so
+    a later startup times only what the file lacks."""
 
     SPLITS = (1, 2, 3, 4, 7, 8, 14)
     MBLOCKS = (1, 2, 3, 6)
@@ -628,6 +630,7 @@ class GemmDispatch:
         self.small = {}     # (M, N, K) -> (splits, mblocks) or None (library GEMM)
         self.small_best = {}  # (M, N, K) -> the fastest gemm_small (splits, mblocks), chosen or not
         self.gated_best = {}  # (M, N, K) -> the fastest gemm_silu_small (1, mblocks) for the gated weights
+        self.large = {}     # (N, K) -> the prefill-sized record: {"M", "choice": "library", "us", "TFLOP/s"}
         self.enabled = True
         self.ws = None
         self.log = []
@@ -663,65 +666,149 @@ class GemmDispatch:
     def applies(M, N, K):
         return 0 < M <= 192 and K % 64 == 0 and N % 8 == 0
 
+    @staticmethod
+    def gpu_key(device) -> str:
+        """The tuning cache's key for a GPU: architecture, compute units and name (the name alone can be empty
+        or generic on ROCm)."""
+        p = torch.cuda.get_device_properties(device)
+        return f"{getattr(p, 'gcnArchName', '?')}/{p.multi_processor_count}CU/{p.name}"
+
+    def _cache_load(self, cache_path, gpu):
+        import json
+        import os
+        if not cache_path or not os.path.exists(cache_path):
+            return {}
+        try:
+            with open(cache_path) as f:
+                return json.load(f).get(gpu, {})
+        except (OSError, ValueError):
+            return {}
+
+    def _cache_store(self, cache_path, gpu, entries):
+        import json
+        import os
+        try:
+            with open(cache_path) as f:
+                allc = json.load(f)
+        except (OSError, ValueError):
+            allc = {}
+        allc.setdefault(gpu, {}).update(entries)
+        tmp = f"{cache_path}.{os.getpid()}.tmp"
+        with open(tmp, "w") as f:
+            json.dump(allc, f, indent=1, sort_keys=True)
+        os.replace(tmp, cache_path)
+
     @torch.inference_mode()
-    def tune(self, weights, Ms, log=None, gated=()):
+    def tune(self, weights, Ms, log=None, gated=(), large_m=4096, cache_path=None):
         """weights: iterable of [N, K] bf16 tensors (a model's projections: the calls are timed cycling through
         every weight of a shape, as the model's layers would); Ms: token counts. gated: those of the weights that
         are [gate; up] products (w13): their shape is also timed through the launch that runs it with the
         activation in its epilogue (gemm_silu_small), whose best row-block count `gated` and the norm-fused
-        products then take."""
+        products then take.
+        large_m: the prefill-sized token count each weight shape is also timed at (M > 192, where only the
+        library GEMM applies: the choice recorded in `large` is the library, with its time).
+        cache_path: a JSON file of results keyed by GPU (gpu_key), as the reference keeps its tuning
+        (fast_kernels.py:442-505): shapes found there are not timed again, new results are merged into it."""
         shapes = {}
         for w in weights:
             shapes.setdefault((w.shape[0], w.shape[1]), []).append(w)
         gshapes = {}
         for w in gated:
             gshapes.setdefault((w.shape[0], w.shape[1]), []).append(w)
+        if not shapes:
+            return
+        dev = next(iter(shapes.values()))[0].device
+        gpu = self.gpu_key(dev)
+        disk = self._cache_load(cache_path, gpu)
+        fresh = {}
         need = 0
+
+        def tup(v):
+            return None if v is None else tuple(int(a) for a in v)
+
         for (N, K), ws_ in shapes.items():
             for M in sorted(set(int(m) for m in Ms)):
+                key = f"{M},{N},{K}"
+                gkey = (N, K) in gshapes and N % 16 == 0
                 if not self.applies(M, N, K):
                     self.small[(M, N, K)] = None
                     continue
-                x = torch.randn(M, K, device=ws_[0].device, dtype=ws_[0].dtype)
-                y = torch.empty(M, N, device=ws_[0].device, dtype=ws_[0].dtype)
-                n = max(20, len(ws_))
-                best, best_t = None, self._time([lambda w=w: torch.matmul(x, w.t(), out=y) for w in ws_], n)
-                lib_t = best_t
-                small_t = None
-                for sp in self.SPLITS:
-                    if sp > K // 64:
-                        continue
-                    wsp = torch.zeros(gemm_ws_bytes(M, N, sp), dtype=torch.uint8, device=x.device) if sp > 1 else None
-                    for mb in self.MBLOCKS:
-                        if mb > 1 and (M + mb - 1) // mb < 32:
+                if f"s{key}" in disk and (not gkey or f"g{key}" in disk):
+                    self.small[(M, N, K)] = tup(disk[f"s{key}"])
+                    if disk.get(f"b{key}") is not None:
+                        self.small_best[(M, N, K)] = tup(disk[f"b{key}"])
+                    if gkey and disk.get(f"g{key}") is not None:
+                        self.gated_best[(M, N, K)] = tup(disk[f"g{key}"])
+                    lib_us, best_us = disk.get(f"t{key}", [None, None])
+                    self.log.append(((M, N, K), None if lib_us is None else lib_us / 1e3, self.small[(M, N, K)],
+                                     None if best_us is None else best_us / 1e3))
+                else:
+                    x = torch.randn(M, K, device=dev, dtype=ws_[0].dtype)
+                    y = torch.empty(M, N, device=dev, dtype=ws_[0].dtype)
+                    n = max(20, len(ws_))
+                    best, best_t = None, self._time([lambda w=w: torch.matmul(x, w.t(), out=y) for w in ws_], n)
+                    lib_t = best_t
+                    small_t = None
+                    for sp in self.SPLITS:
+                        if sp > K // 64:
                             continue
-                        t = self._time([lambda w=w: gemm_small(x, w, y, splits=sp, ws=wsp, mblocks=mb) for w in ws_], n)
-                        if t < best_t:
-                            best, best_t = (sp, mb), t
-                        if small_t is None or t < small_t:
-                            self.small_best[(M, N, K)], small_t = (sp, mb), t
-                self.small[(M, N, K)] = best
+                        wsp = torch.zeros(gemm_ws_bytes(M, N, sp), dtype=torch.uint8, device=dev) if sp > 1 else None
+                        for mb in self.MBLOCKS:
+                            if mb > 1 and (M + mb - 1) // mb < 32:
+                                continue
+                            t = self._time([lambda w=w: gemm_small(x, w, y, splits=sp, ws=wsp, mblocks=mb)
+                                            for w in ws_], n)
+                            if t < best_t:
+                                best, best_t = (sp, mb), t
+                            if small_t is None or t < small_t:
+                                self.small_best[(M, N, K)], small_t = (sp, mb), t
+                    self.small[(M, N, K)] = best
+                    if gkey:
+                        gws = gshapes[(N, K)]
+                        yg = torch.empty(M, N // 2, device=dev, dtype=x.dtype)
+                        gt = None
+                        for mb in self.MBLOCKS:
+                            if mb > 1 and (M + mb - 1) // mb < 32:
+                                continue
+                            t = self._time([lambda w=w: gemm_silu_small(x, w, yg, mblocks=mb) for w in gws],
+                                           max(20, len(gws)))
+                            if gt is None or t < gt:
+                                self.gated_best[(M, N, K)], gt = (1, mb), t
+                    self.log.append(((M, N, K), lib_t, best, best_t))
+                    fresh[f"s{key}"] = None if best is None else list(best)
+                    fresh[f"b{key}"] = None if (M, N, K) not in self.small_best else list(self.small_best[(M, N, K)])
+                    if gkey:
+                        fresh[f"g{key}"] = (None if (M, N, K) not in self.gated_best
+                                            else list(self.gated_best[(M, N, K)]))
+                    fresh[f"t{key}"] = [round(lib_t * 1e3, 3), round(best_t * 1e3, 3)]
+                    if log:
+                        log(f"[gemm] M={M} N={N} K={K}: library {lib_t * 1e3:.1f} us, "
+                            + (f"gemm_small splits={best[0]} mblocks={best[1]} {best_t * 1e3:.1f} us" if best
+                               else "kept"))
                 sb = self.small_best.get((M, N, K))
                 if sb is not None and sb[0] > 1:  # the norm-fused products run gemm_small whatever was chosen
                     need = max(need, gemm_ws_bytes(M, N, sb[0]))
-                if (N, K) in gshapes and N % 16 == 0:
-                    gws = gshapes[(N, K)]
-                    yg = torch.empty(M, N // 2, device=x.device, dtype=x.dtype)
-                    gt = None
-                    for mb in self.MBLOCKS:
-                        if mb > 1 and (M + mb - 1) // mb < 32:
-                            continue
-                        t = self._time([lambda w=w: gemm_silu_small(x, w, yg, mblocks=mb) for w in gws],
-                                       max(20, len(gws)))
-                        if gt is None or t < gt:
-                            self.gated_best[(M, N, K)], gt = (1, mb), t
-                self.log.append(((M, N, K), lib_t, best, best_t))
-                if log:
-                    log(f"[gemm] M={M} N={N} K={K}: library {lib_t * 1e3:.1f} us, "
-                        + (f"gemm_small splits={best[0]} mblocks={best[1]} {best_t * 1e3:.1f} us" if best else "kept"))
+            # prefill-sized M: the library GEMM (gemm_small serves M <= 192); its time is recorded
+            if large_m and int(large_m) > 192:
+                lkey = f"l{N},{K}"
+                if lkey in disk:
+                    self.large[(N, K)] = disk[lkey]
+                else:
+                    M = int(large_m)
+                    x = torch.randn(M, K, device=dev, dtype=ws_[0].dtype)
+                    y = torch.empty(M, N, device=dev, dtype=ws_[0].dtype)
+                    t = self._time([lambda w=w: torch.matmul(x, w.t(), out=y) for w in ws_], 5, reps=3)
+                    ent = {"M": M, "choice": "library", "us": round(t * 1e3, 2),
+                           "TFLOP/s": round(2 * M * N * K / t / 1e9, 1)}
+                    self.large[(N, K)] = ent
+                    fresh[lkey] = ent
+                    del x, y
         if need and (self.ws is None or self.ws.numel() < need):
-            dev = next(iter(shapes.values()))[0].device
             self.ws = torch.zeros(need, dtype=torch.uint8, device=dev)  # the tile counters start at zero
+        if cache_path and fresh:
+            self._cache_store(cache_path, gpu, fresh)
+        if log and cache_path:
+            log(f"[gemm] {len(fresh)} entries timed, the rest from {cache_path}")
 
     @staticmethod
     def _operands_ok(x, w):

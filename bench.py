@@ -336,7 +336,8 @@ def per_config(a8, torch, dev, steps, cpu_budget=4.0):
     # GEMM (gemm_small, with its split count and row blocks), whichever the timing at startup finds faster --
     # timed cycling through the 24 layers' weights, as the step reads them
     mm = a8.GemmDispatch()
-    mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b], gated=[L["w13"] for L in wts])
+    mm.tune([L[k] for L in wts for k in ("wqkv", "wo", "w13", "w2")], [b], gated=[L["w13"] for L in wts],
+            large_m=8192)
     st.mm = mm
     xbuf.copy_(x0)
     g = capture(torch, lambda: st.forward(xbuf, pos, slot, lens_d, rowmap=False, fuse=True))
@@ -355,8 +356,9 @@ def per_config(a8, torch, dev, steps, cpu_budget=4.0):
                     for (M, N, K), c in mm.small.items()},
         "gemm_small_shapes": {f"{N}x{K}": {"splits": c[0], "mblocks": c[1]} for (M, N, K), c in mm.small_best.items()},
         "gated_shapes": {f"{N}x{K}": {"mblocks": c[1]} for (M, N, K), c in mm.gated_best.items()},
-        "tune_us": {f"{N}x{K}": [round(lt * 1e3, 2), None if bt is None else round(bt * 1e3, 2)]
+        "tune_us": {f"{N}x{K}": [None if lt is None else round(lt * 1e3, 2), None if bt is None else round(bt * 1e3, 2)]
                     for (M, N, K), lt, _, bt in mm.log},
+        "prefill_sized_m": {f"{N}x{K}": v for (N, K), v in mm.large.items()},
         "library": lib_step,
         "norms_separate": {"us_per_step": round(us_dispatch, 1), "us_per_layer": round(us_dispatch / layers, 2),
                            "note": "GemmDispatch per shape (hipBLASLt or gemm_small), rmsnorm as its own launch"},

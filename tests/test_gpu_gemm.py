@@ -113,6 +113,41 @@ def test_gemm_dispatch_graph(a8, dev):
     say(f"  choices {mm.small}")
 
 
+def test_gemm_dispatch_tuning_cache(a8, dev, tmp_path):
+    """tune(..., cache_path) writes its choices (small M, the gated launch, the prefill-sized record) into a JSON
+    file keyed by GPU; a second dispatcher tuned from that file times nothing and makes the same choices, and
+    an entry missing from the file is timed and merged in."""
+    say("case: GemmDispatch tuning cache round trip")
+    import json
+    g = torch.Generator().manual_seed(9)
+    wq, w13 = randn_bf16(g, 1152, 896).to(dev), randn_bf16(g, 2 * 512, 896).to(dev)
+    path = str(tmp_path / "gemm_tune.json")
+    a = a8.GemmDispatch()
+    a.tune([wq, w13], [192], gated=[w13], large_m=1024, cache_path=path)
+    disk = json.load(open(path))
+    key = a8.GemmDispatch.gpu_key(dev)
+    assert set(disk) == {key}
+    assert {"s192,1152,896", "s192,1024,896", "g192,1024,896", "l1152,896", "l1024,896"} <= set(disk[key])
+    assert a.large[(1152, 896)]["choice"] == "library"
+
+    b = a8.GemmDispatch()
+    timed = []
+    orig = b._time
+    b._time = lambda *args, **kw: timed.append(1) or orig(*args, **kw)
+    b.tune([wq, w13], [192], gated=[w13], large_m=1024, cache_path=path)
+    assert not timed
+    assert b.small == a.small and b.small_best == a.small_best and b.gated_best == a.gated_best
+    assert b.large == a.large
+    x = randn_bf16(g, 192, 896).to(dev)
+    assert torch.equal(b(x, wq), a(x, wq))
+
+    # a new token count is timed and merged; the earlier entries stay
+    b.tune([wq], [64], large_m=1024, cache_path=path)
+    assert timed
+    disk = json.load(open(path))[key]
+    assert "s64,1152,896" in disk and "s192,1152,896" in disk
+
+
 @pytest.mark.parametrize("M,I,K,mblocks", [(192, 4864, 896, 1), (192, 4864, 896, 3), (37, 1000, 640, 1),
                                            (100, 24, 128, 2), (1, 8, 64, 1)])
 def test_gemm_silu_small(a8, dev, M, I, K, mblocks):
