@@ -105,26 +105,30 @@ class AttnStack:
 
 class PrefillMeta:
     """The graph-mode packed-prefill plan: one int32 device buffer
-    [pos NT | slot NT | q0, n, bslot, pos0 NB | last, st, cpos NR] with NB = NT/64 + NR, rewritten by one
-    host-to-device copy per admission and read by a captured prefill (fast_engine.py:681-691, 820-853).
-    Padding rows, blocks and requests point at the scratch cache row `scr` with n = 0 and pos = 0."""
+    [pos NT | slot NT | q0, n, bslot, pos0 NB | last, st, cpos NR | dq0, dn, dbslot, dpos0 NB] with
+    NB = NT/64 + NR, rewritten by one host-to-device copy per admission and read by a captured prefill
+    (fast_engine.py:681-691, 820-853). The first nine fields are the reference's layout and contents; the
+    last four hold the same blocks heaviest first, the order the kernel dispatches them in (see
+    PrefillPlan). Padding rows, blocks and requests point at the scratch cache row `scr` with n = 0 and
+    pos = 0."""
 
-    FIELDS = ("pos", "slot", "q0", "n", "bslot", "pos0", "last", "st", "cpos")
+    FIELDS = ("pos", "slot", "q0", "n", "bslot", "pos0", "last", "st", "cpos", "dq0", "dn", "dbslot", "dpos0")
 
     def __init__(self, NT, NR, scr, dev):
         BM = PrefillPlan.BM
         self.NT, self.NR, self.NB, self.scr = NT, NR, NT // BM + NR, scr
-        self.off = np.cumsum([0, NT, NT, self.NB, self.NB, self.NB, self.NB, NR, NR, NR])
+        NB = self.NB
+        self.off = np.cumsum([0, NT, NT, NB, NB, NB, NB, NR, NR, NR, NB, NB, NB, NB])
         self.buf = torch.zeros(int(self.off[-1]), dtype=torch.int32, device=dev)
         self.v = SimpleNamespace(**{k: self.buf[self.off[i]:self.off[i + 1]] for i, k in enumerate(self.FIELDS)})
 
     def host(self, nt, slots, ns, starts):
         """Host int32 contents for requests of ns tokens at positions starts.. in slots, packed in order
-        (fast_engine.py:837-853); the query blocks are listed heaviest first (see PrefillPlan)."""
+        (fast_engine.py:837-853); the dispatch copy of the query blocks is heaviest first."""
         BM, o = PrefillPlan.BM, self.off
         m = np.zeros(int(o[-1]), np.int32)
-        pos, slot, q0, n, bslot, p0, last, st, cpos = (m[o[i]:o[i + 1]] for i in range(9))
-        slot[:], bslot[:], st[:] = self.scr, self.scr, self.scr
+        pos, slot, q0, n, bslot, p0, last, st, cpos, dq0, dn, dbslot, dp0 = (m[o[i]:o[i + 1]] for i in range(13))
+        slot[:], bslot[:], st[:], dbslot[:] = self.scr, self.scr, self.scr, self.scr
         r0, blocks = 0, []
         for k, (s, cnt, a) in enumerate(zip(slots, ns, starts)):
             pos[r0:r0 + cnt] = np.arange(a, a + cnt)
@@ -134,8 +138,9 @@ class PrefillMeta:
             r0 += cnt
         bi = len(blocks)
         assert r0 <= nt and bi <= nt // BM + self.NR and len(slots) <= self.NR
-        if bi:  # heaviest first, as in PrefillPlan
-            q0[:bi], n[:bi], bslot[:bi], p0[:bi] = zip(*heaviest_first(blocks))
+        if bi:
+            q0[:bi], n[:bi], bslot[:bi], p0[:bi] = zip(*blocks)
+            dq0[:bi], dn[:bi], dbslot[:bi], dp0[:bi] = zip(*heaviest_first(blocks))
         return m
 
     def load(self, nt, slots, ns, starts):
@@ -150,4 +155,6 @@ class PrefillMeta:
         (fast_engine.py:824-826): nt/64 + NR blocks, padding blocks are no-ops."""
         v, nb = self.v, nt // PrefillPlan.BM + self.NR
         return SimpleNamespace(q0=v.q0[:nb], n=v.n[:nb], slot=v.bslot[:nb], pos0=v.pos0[:nb], nblk=nb,
-                               BM=PrefillPlan.BM)
+                               BM=PrefillPlan.BM,
+                               dispatch=SimpleNamespace(q0=v.dq0[:nb], n=v.dn[:nb], slot=v.dbslot[:nb],
+                                                        pos0=v.dpos0[:nb]))

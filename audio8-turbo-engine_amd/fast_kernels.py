@@ -17,6 +17,7 @@ or a launch fails, the call raises.
 from __future__ import annotations
 
 import ctypes
+from types import SimpleNamespace
 
 import torch
 
@@ -389,27 +390,30 @@ def heaviest_first(blocks):
 class PrefillPlan:
     """Query-block schedule for a packed prefill: request i's rows [r0_i, r0_i+n_i) sit at
     positions [p0_i, p0_i+n_i) of cache row slot_i (keys [0, p0_i) are an already-stored prefix)
-    (fast_kernels.py:335-347). The blocks are the reference's; they are listed heaviest first (most keys,
-    ties in request order) instead of in request order, so the kernel, which dispatches its workgroups
-    in list order, starts the long blocks first and the short ones fill the end. Every block writes its
-    own rows, so the order changes no result."""
+    (fast_kernels.py:335-347). q0, n, slot, pos0 are the reference's blocks in its order (request order).
+    `dispatch` holds the same blocks heaviest first (most keys, ties in request order): the kernel
+    dispatches its workgroups in that list's order, so the long blocks start first and the short ones fill
+    the end. Every block writes its own rows, so the order changes no result."""
     BM = 64
 
     def __init__(self, r0s, ns, slots, p0s, device):
-        blocks = heaviest_first([(r0 + off, min(self.BM, n - off), s, p0 + off)
-                                 for r0, n, s, p0 in zip(r0s, ns, slots, p0s) for off in range(0, n, self.BM)])
-        q0, cnt, sl, ps = (list(c) for c in zip(*blocks)) if blocks else ([], [], [], [])
-        t = torch.tensor([q0, cnt, sl, ps], dtype=torch.int32)
+        blocks = [(r0 + off, min(self.BM, n - off), s, p0 + off)
+                  for r0, n, s, p0 in zip(r0s, ns, slots, p0s) for off in range(0, n, self.BM)]
+        cols = [list(c) for c in zip(*blocks)] if blocks else [[], [], [], []]
+        dcols = [list(c) for c in zip(*heaviest_first(blocks))] if blocks else [[], [], [], []]
+        t = torch.tensor(cols + dcols, dtype=torch.int32)
         if torch.device(device).type == "cuda":
             t = t.pin_memory().to(device, non_blocking=True)
         self.q0, self.n, self.slot, self.pos0 = t[0], t[1], t[2], t[3]
-        self.nblk = len(q0)
+        self.dispatch = SimpleNamespace(q0=t[4], n=t[5], slot=t[6], pos0=t[7])
+        self.nblk = len(blocks)
 
 
 def prefill_attention(q, kc, vc, plan, out, group, scale=None):
     """q/out: [R, nq, hd] packed rows; kc/vc: [rows, nkv, S, hd] (fast_kernels.py:350-358).
     `plan` is a PrefillPlan or any object with int32 device tensors q0, n, slot, pos0, an int nblk and
-    BM = 64 (the graph-mode plan of fast_engine.py:825-826)."""
+    BM = 64 (the graph-mode plan of fast_engine.py:825-826). When the plan carries `dispatch` (the same
+    blocks in the order to launch them: PrefillPlan, PrefillMeta.plan), the kernel reads that list."""
     _check_bf16("q", q, 3)
     nq, hd = q.shape[1], q.shape[2]
     scale = scale if scale is not None else hd ** -0.5
@@ -420,16 +424,17 @@ def prefill_attention(q, kc, vc, plan, out, group, scale=None):
           f"out shape {tuple(out.shape)} does not match q {tuple(q.shape)}")
     bm = int(getattr(plan, "BM", PrefillPlan.BM))
     nblk = int(plan.nblk)
+    blocks = getattr(plan, "dispatch", None) or plan
     for name in ("q0", "n", "slot", "pos0"):
-        _check_i32(f"plan.{name}", getattr(plan, name), nblk)
-    _check_device(q=q, kc=kc, vc=vc, out=out, **{f"plan.{k}": getattr(plan, k) for k in ("q0", "n", "slot", "pos0")})
+        _check_i32(f"plan.{name}", getattr(blocks, name), nblk)
+    _check_device(q=q, kc=kc, vc=vc, out=out, **{f"plan.{k}": getattr(blocks, k) for k in ("q0", "n", "slot", "pos0")})
     if nblk == 0 or q.shape[0] == 0:
         return out
     st = _lib.load().a8_prefill_attn(
         q.data_ptr(), q.stride(0), q.stride(1), q.shape[0],
         kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
         out.data_ptr(), out.stride(0), out.stride(1),
-        plan.q0.data_ptr(), plan.n.data_ptr(), plan.slot.data_ptr(), plan.pos0.data_ptr(), nblk, bm,
+        blocks.q0.data_ptr(), blocks.n.data_ptr(), blocks.slot.data_ptr(), blocks.pos0.data_ptr(), nblk, bm,
         nq, group, hd, float(scale), _lib.stream_of(q))
     _lib.check(st, "prefill_attention")
     return out

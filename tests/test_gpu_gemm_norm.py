@@ -85,6 +85,45 @@ def test_norm_consumer_against_float64(a8, lref, dev, M, N, K, splits, mblocks, 
     assert (err <= tol).all()
 
 
+@pytest.mark.parametrize("M,N,K,splits,mblocks", [(192, 1152, 896, 1, 6), (192, 9728, 896, 1, 1),
+                                                  (64, 1152, 896, 3, 1), (33, 256, 512, 1, 1)])
+def test_folded_norm_against_reference_sequence(a8, lref, dev, M, N, K, splits, mblocks):
+    """The folded-norm product (norm weight folded into the weight, 1 / rms on the fp32 products) against the
+    reference's own sequence as the oracle restates it: rmsnorm (two bf16 roundings) then the bf16 product
+    (fast_kernels.py:30-46, fast_engine.py:90). Two bars:
+      * absolute, every element: with u = 2^-8 (bf16) and t_k = h_k r g_k w_nk, the reference rounds each
+        term's factors twice and the fused path once, so |got - ref| <= 3u sum|t_k| + 2 gamma_K sum|t_k|
+        + u (|got| + |ref|) (gamma_K = K 2^-24 for the fp32 sums; the last term: each output's own rounding);
+      * statistical: the roundings are independent, so the RMS difference stays within 2u of the RMS output;
+        a dropped or misplaced factor (norm weight, 1 / rms, eps) moves it by percents."""
+    say(f"case: folded norm vs rmsnorm -> product M={M} N={N} K={K} splits={splits} mblocks={mblocks}")
+    g = torch.Generator().manual_seed(3 * M + N + K)
+    h = (randn_bf16(g, M, K) * 3).to(BF)
+    w = (randn_bf16(g, N, K) * (K ** -0.5)).to(BF)
+    ln = (1 + 0.05 * torch.randn(K, generator=g)).to(BF)
+    eps = 1e-6
+    y, _ = lref.rmsnorm(h, ln, eps)
+    ref_out = lref.linear(y, w).double()
+    ss = (h.float() ** 2).view(M, K // 32, 32).sum(-1).contiguous()
+    ws = torch.zeros(a8.gemm_ws_bytes(M, N, splits), dtype=torch.uint8, device=dev) if splits > 1 else None
+    out = torch.empty(M, N, dtype=BF, device=dev)
+    a8.gemm_small_norm(h.to(dev), a8.fold_norm(w, ln).to(dev), out, splits=splits, mblocks=mblocks, ws=ws,
+                       ss_in=ss.to(dev), eps=eps)
+    torch.cuda.synchronize()
+    got = out.cpu().double()
+    hd = h.double()
+    r = torch.rsqrt((hd ** 2).mean(-1, keepdim=True) + eps)
+    tabs = (hd.abs() * r) @ (w.double().abs() * ln.double().abs()).t()   # sum_k |t_k|
+    u, gam = 2.0 ** -8, K * 2.0 ** -24
+    bound = (3 * u + 2 * gam) * tabs + u * (got.abs() + ref_out.abs())
+    diff = (got - ref_out).abs()
+    rms_d, rms_y = diff.pow(2).mean().sqrt().item(), ref_out.pow(2).mean().sqrt().item()
+    say(f"  max |diff| {diff.max().item():.3e}, worst diff / bound {(diff / bound).max().item():.3f}, "
+        f"RMS diff / RMS out {rms_d / rms_y:.2e} (bar {2 * u:.2e})")
+    assert (diff <= bound).all()
+    assert rms_d <= 2 * u * rms_y
+
+
 def test_slow_stack_fused_norm(a8, ref, lref, dev):
     """The decode tick with fuse_norm (every projection on gemm_small, the norms inside them) at the slow AR's
     widths and 192 rows against the oracle, with the same bar as the unfused stack, and its graph replays

@@ -35,37 +35,45 @@ def _heaviest_first_of(got, want):
 
 
 def test_prefill_plan_matches_oracle(a8, ref):
+    """The plan's q0, n, slot, pos0 are the reference's blocks in its order (exact int equality); the
+    dispatch copy holds the same blocks heaviest first."""
     r0s, ns, slots, p0s = [0, 70, 75], [70, 5, 200], [3, 1, 0], [300, 0, 64]
     p = a8.PrefillPlan(r0s, ns, slots, p0s, "cpu")
     want = ref.prefill_plan(r0s, ns, slots, p0s)
     assert p.nblk == len(want[0]) == 2 + 1 + 4
     assert all(t.dtype == torch.int32 for t in (p.q0, p.n, p.slot, p.pos0))
-    _heaviest_first_of((p.q0.tolist(), p.n.tolist(), p.slot.tolist(), p.pos0.tolist()), want)
-    assert p.pos0.tolist()[:2] == [300 + 64, 300]  # request 0's blocks (keys 370 and 364) lead
+    assert [p.q0.tolist(), p.n.tolist(), p.slot.tolist(), p.pos0.tolist()] == [list(map(int, c)) for c in want]
+    d = p.dispatch
+    _heaviest_first_of((d.q0.tolist(), d.n.tolist(), d.slot.tolist(), d.pos0.tolist()), want)
+    assert d.pos0.tolist()[:2] == [300 + 64, 300]  # request 0's blocks (keys 370 and 364) lead
     assert a8.PrefillPlan.BM == 64
     assert a8.PrefillPlan([], [], [], [], "cpu").nblk == 0
 
 
 def test_prefill_meta_matches_oracle(a8, ref):
+    """The buffer's first nine fields equal the reference's graph-mode plan (fast_engine.py:837-853) int for
+    int; the four dispatch fields hold its blocks heaviest first, then the same padding blocks."""
     meta = a8.PrefillMeta(2048, 64, 192, "cpu")
     for slots, ns, starts, nt in (([], [], [], 2048), ([5, 9], [300, 64], [300, 300], 512),
                                   (list(range(64)), [1] * 64, list(range(64)), 64)):
         h = meta.host(nt, slots, ns, starts)
         w = ref.pf_meta_host(nt, slots, ns, starts, 2048, 64, 192)
         o = meta.off
-        blk = slice(o[2], o[6])  # q0, n, bslot, pos0: the same blocks, heaviest first
-        np.testing.assert_array_equal(np.delete(h, np.r_[blk]), np.delete(w, np.r_[blk]))
+        np.testing.assert_array_equal(h[:o[9]], w)
         nb = int((w[o[3]:o[4]] > 0).sum())
         cols = [lambda m, i=i: m[o[i]:o[i] + nb] for i in (2, 3, 4, 5)]
-        _heaviest_first_of([c(h) for c in cols], [c(w) for c in cols])
-        for i in (2, 3, 4, 5):
-            np.testing.assert_array_equal(h[o[i] + nb:o[i + 1]], w[o[i] + nb:o[i + 1]])  # padding blocks
+        dcols = [lambda m, i=i: m[o[i]:o[i] + nb] for i in (9, 10, 11, 12)]
+        _heaviest_first_of([c(h) for c in dcols], [c(w) for c in cols])
+        for i, j in zip((9, 10, 11, 12), (2, 3, 4, 5)):  # padding blocks as the reference's
+            np.testing.assert_array_equal(h[o[i] + nb:o[i + 1]], w[o[j] + nb:o[j + 1]])
     meta.load(512, [5, 9], [300, 64], [300, 300])
     plan = meta.plan(512)
     assert plan.nblk == 512 // 64 + 64 and plan.BM == 64
-    assert plan.n[:6].tolist() == [44, 64, 64, 64, 64, 64] and (plan.n[6:] == 0).all()
-    assert plan.pos0[:6].tolist() == [556, 492, 428, 364, 300, 300]
-    assert (plan.slot[6:] == 192).all()
+    assert plan.n[:6].tolist() == [64, 64, 64, 64, 44, 64] and (plan.n[6:] == 0).all()
+    assert plan.pos0[:6].tolist() == [300, 364, 428, 492, 556, 300]
+    assert plan.dispatch.n[:6].tolist() == [44, 64, 64, 64, 64, 64] and (plan.dispatch.n[6:] == 0).all()
+    assert plan.dispatch.pos0[:6].tolist() == [556, 492, 428, 364, 300, 300]
+    assert (plan.slot[6:] == 192).all() and (plan.dispatch.slot[6:] == 192).all()
 
 
 def _store_inputs(dev="cpu"):
