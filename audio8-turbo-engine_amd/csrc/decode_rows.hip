@@ -27,12 +27,13 @@
 //     last wave to arrive, cost ~0.7 us per layer more (the merging wave falls behind, the last merge runs
 //     on one wave).
 //   * Nothing is requested past the last tile (the pipeline's last two steps issue no load).
-// Measured at 192 rows x 2048 keys, 24 layers in a graph: 35.0-35.4 us per layer unfused and 36.2-36.5
-// fused (store included). Tried and slower: four tiles in flight per wave (+1 us), the first tiles requested
-// before the position (+0.9 to +2.3 us: the table rows then return behind them), the table rows read through
-// the scalar cache after the first tiles (+1.8 us), each step's refill requested in two halves inside the
-// step (K after the score products, V after the P.V operand reads: +0.8 us), one unit per workgroup over all
-// compute units (k_decode_unit at grid 384: +2 us).
+//   * K and V tiles go into LDS by non-temporal DMA; a step refills its K buffer as soon as the K operands are
+//     in registers and its V buffer after the P.V operand reads.
+// Measured at 192 rows x 2048 keys, 24 layers in a graph: 31.4 us per layer unfused and 32.4 fused (store
+// included). Tried and slower: four tiles in flight per wave (+1 us), the first tiles requested before the
+// position (+0.9 to +2.3 us: the table rows then return behind them), the table rows read through the scalar
+// cache after the first tiles (+1.8 us), K kept in registers with its refill after the score products (+0.8
+// us), one unit per workgroup over all compute units (k_decode_unit at grid 384: +2 us).
 #include "fused_qkv.h"
 
 namespace a8 {
@@ -306,27 +307,33 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
 
   // ---- steps: compute tile j of the current unit from buffer j % D, then request into it tile j + D of the
   // unit, or tile j + D - SPW of the next (one load sequence, sources selected) ----
-  // The tile read at step j had the next tile's 16 requests issued after it, except at the launch's very last
-  // step (`tail`: nothing requested after it); the reads wait for it with those counts (D = 2).
-  static_assert(D == 2, "wait counts assume one tile requested after the one read");
+  static_assert(D == 2, "wait counts assume one tile requested between a tile and its reads");
+  // K(j+2) goes out as soon as tile j's K operands are in registers and V(j+2) after its P.V operand reads
+  // (refilling each buffer at once, as one load sequence after the step, measured 0.2 us per layer slower at
+  // the peak load, fused). Issued after V(j) when its reads wait: K(j+1), V(j+1) (unless `tail`) and K(j+2)
+  // (when reloading); after K(j): V(j), then K(j+1), V(j+1) (unless `tail`).
   auto step = [&](uint16_t *xk, uint16_t *xv, int j, bool reload, bool tail) __attribute__((always_inline)) {
     const int t0 = 64 * tile_of(cur.rot, j);
+    const bool in_cur = j + D < SPW;
+    const rsrc_t kr = in_cur ? cur.kr : nxt.kr, vr = in_cur ? cur.vr : nxt.vr;
+    const int tt = in_cur ? tile_of(cur.rot, j + D) : tile_of(nxt.rot, j + D - SPW);
+    KTile X[1];
     if (t0 < cur.hi) {
-      KTile X[1];
-      if (tail) {
+      if (tail)
         read_k_tile<0>(X[0], xk, kl);
-        compute_step<1, 0, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
-      } else {
+      else
         read_k_tile<16>(X[0], xk, kl);
+    }
+    if (reload) load_k_lds(xk, kr, (uint32_t)(64 * tt), kl);
+    if (t0 < cur.hi) {
+      if (reload)
+        compute_step<1, 24, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
+      else if (!tail)
         compute_step<1, 16, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
-      }
+      else
+        compute_step<1, 0, FUSED>(X, xv, t0, cur.hi, qc0, qc1, sl2, S, tl, lane, &ptc);
     }
-    if (reload) {
-      const bool in_cur = j + D < SPW;
-      const rsrc_t kr = in_cur ? cur.kr : nxt.kr, vr = in_cur ? cur.vr : nxt.vr;
-      const int tt = in_cur ? tile_of(cur.rot, j + D) : tile_of(nxt.rot, j + D - SPW);
-      load_tile_kv(xk, xv, kr, vr, (uint32_t)(64 * tt), tl, kl);
-    }
+    if (reload) load_v_lds(xv, vr, (uint32_t)(64 * tt), tl);
   };
   auto step_k = [&](int j, bool reload, bool tail) __attribute__((always_inline)) {
     step(kbw[j & 1], vbw[j & 1], j, reload, tail);

@@ -118,6 +118,37 @@ struct KLdsLane {
   }
 };
 
+// The halves of load_tile_kv, for a step that refills its K buffer as soon as the K operands are in registers
+// and its V buffer after the P.V operand reads: keys [t0, t0+64) into ktile / vtile (8 DMA instructions each).
+__device__ __forceinline__ void load_k_lds(uint16_t *ktile, rsrc_t kr, uint32_t t0, const KLdsLane &K) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS reads of the buffer done (see load_tile)
+  const uint32_t base = t0 * kRow;
+  const uint32_t a0 = base + K.kd[0], a1 = base + K.kd[1];
+  char *kl = reinterpret_cast<char *>(ktile), *kh = kl + 4096;
+  bld16_lds<0, 2>(kr, kl, a0, 0u);
+  bld16_lds<1024, 2>(kr, kl, a1, 0u);
+  bld16_lds<2048, 2>(kr, kl, a0, 0u);
+  bld16_lds<3072, 2>(kr, kl, a1, 0u);
+  bld16_lds<0, 2>(kr, kh, a0, 4096u);
+  bld16_lds<1024, 2>(kr, kh, a1, 4096u);
+  bld16_lds<2048, 2>(kr, kh, a0, 4096u);
+  bld16_lds<3072, 2>(kr, kh, a1, 4096u);
+}
+__device__ __forceinline__ void load_v_lds(uint16_t *vtile, rsrc_t vr, uint32_t t0, const TileLane &L) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS reads of the buffer done (see load_tile)
+  const uint32_t base = t0 * kRow;
+  const uint32_t v0 = base + L.vd[0], v1 = base + L.vd[1];
+  char *lo = reinterpret_cast<char *>(vtile), *hi = lo + 4096;
+  bld16_lds<0, 2>(vr, lo, v0, 0u);
+  bld16_lds<1024, 2>(vr, lo, v1, 0u);
+  bld16_lds<2048, 2>(vr, lo, v0, 0u);
+  bld16_lds<3072, 2>(vr, lo, v1, 0u);
+  bld16_lds<0, 2>(vr, hi, v0, 4096u);
+  bld16_lds<1024, 2>(vr, hi, v1, 4096u);
+  bld16_lds<2048, 2>(vr, hi, v0, 4096u);
+  bld16_lds<3072, 2>(vr, hi, v1, 4096u);
+}
+
 // Loads keys [t0, t0+64) of one (cache row, kv head): K into the LDS tile ktile, V into vtile (8 KB each, this
 // wave's), both non-temporal. Same range semantics as load_tile.
 __device__ __forceinline__ void load_tile_kv(uint16_t *ktile, uint16_t *vtile, rsrc_t kr, rsrc_t vr, uint32_t t0,
