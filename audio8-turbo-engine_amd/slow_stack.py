@@ -76,9 +76,10 @@ class SlowStack:
         self.pf_slices = 8  # grid slices of prefetch workgroups (each as many as the o product's weight tiles)
         # prefetch_kv_bytes: the qkv product's launch (layers after the first) also reads about this many bytes of
         # the layer's K cache -- the last rows of the tick, which the whole-row decode reaches in its second pass --
-        # into the memory-side cache, at most a sixth of the rows (measured at 192 rows x 2048: 32 rows, 16.8 MB,
-        # -0.55 us per layer; 64 rows outlast the qkv product and cost +3 us). 0: none.
-        self.prefetch_kv_bytes = 16 << 20
+        # into the memory-side cache, at most a sixth of the rows. Off: since the decode streams K and V by
+        # non-temporal DMA it gains nothing from it (192 rows x 2048, one box: 0 / 8 / 16 / 24 MB -> 69.85 /
+        # 70.17 / 70.53 / 70.49 us per layer; with the register-loaded K it had saved 0.55 us).
+        self.prefetch_kv_bytes = 0
         self.kv_slices = 8
         self._sink = None
 

@@ -221,9 +221,9 @@ def test_prefetch_workgroups_change_nothing(a8, dev):
 
 
 def test_slow_stack_prefetch_is_the_same_step(a8, dev):
-    """The norm-fused slow-AR step with the w13 prefetch (the default) against the same step without: the final
-    hidden state and the caches bit for bit."""
-    say("case: slow stack fused step, w13 prefetch on / off")
+    """The norm-fused slow-AR step with the w13 prefetch (the default) and the K-cache prefetch (opt-in) against
+    the same step without either: the final hidden state and the caches bit for bit."""
+    say("case: slow stack fused step, w13 + K prefetch on / off")
     from importlib import import_module
     ss_mod = import_module(a8.__name__ + ".slow_stack")
     layers, norm = ss_mod.random_weights(2, 896, 14, 2, 64, 1024, dev, seed=13)
@@ -234,6 +234,7 @@ def test_slow_stack_prefetch_is_the_same_step(a8, dev):
         mm = a8.GemmDispatch()
         mm.tune([L[k] for L in layers for k in ("wqkv", "wo", "w13", "w2")], [16], gated=[L["w13"] for L in layers])
         st.mm, st.fuse_norm, st.prefetch_w13 = mm, True, pf
+        st.prefetch_kv_bytes = (1 << 20) if pf else 0
         gen = torch.Generator(device=dev).manual_seed(14)
         st.kc_all.normal_(generator=gen)
         st.vc_all.normal_(generator=gen)
