@@ -118,9 +118,10 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // Q^T operands: column r16 <-> query row 16qt + r16, slot (g, j) <-> dim 8g+j / 32+8g+j
   uint16_t *qw = qs + w * (4 * 2 * 64 * 8) + lane * 8;
   f32x4 o[UPW][4];   // O^T rows d = 16dt + 4g + i, column = query row 16qt + r16
-  // per query group: the running max (raw score units), the level above which a score raises it
-  // (mrun + the lazy margin) and the exp2 offset mrun * sl2 (0 while mrun is -inf)
-  float mrun[UPW], mlim[UPW], mcs[UPW];
+  // per query group: the exp2 offset mcs (the column's running max in exp2 units, 0 before its first key) and
+  // the level of a tile's scores, relative to it, above which the offset is raised (kPfLazy once the column
+  // has a key, -inf before)
+  float mlim[UPW], mcs[UPW];
   f32x4 lacc[UPW];  // column sums of the weights (all four rows alike)
   const u32x4 ones{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
   // The Q^T operands go from HBM straight into LDS by DMA (requested before the first K / V tiles, so the
@@ -141,7 +142,6 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     live[k] = active;
     head[k] = kh * group + gi;
     qt_of[k] = k;
-    mrun[k] = kNegInf;
     mlim[k] = kNegInf;
     mcs[k] = 0.f;
     lacc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -168,19 +168,22 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     }
     lds_barrier();
   };
-  // Lazy running maximum: a column's max (the exp2 offset) is raised only when a tile's score exceeds it
-  // by more than kPfLazy in exp2 units, so most tiles skip the accumulator rescale; until then its
-  // weights stay below 2^kPfLazy (well inside bf16's range; the sums are fp32). Same softmax, the
-  // rounding happens at other points.
-  const float thr = kPfLazy / sl2;  // in raw score units
+  // Scores in exp2 units: the Q^T operands are pre-scaled by sl2 = scale * log2(e) once per block (rounded to
+  // bf16) and the score products start from -mcs (the MFMA's C operand), so S = q.k * sl2 - mcs comes out of the
+  // matrix cores and a weight is one v_exp_f32 (no FMA per score). Lazy running maximum: a column's offset is
+  // raised only when a tile's score exceeds it by more than kPfLazy, so most tiles skip the accumulator
+  // rescale; until then its weights stay below 2^kPfLazy (well inside bf16's range; the sums are fp32). Same
+  // softmax; the roundings happen at other points (q * sl2 once in bf16 instead of the product in fp32). C4, one
+  // box: 43.7 -> 43.2 us per layer against the FMA per score.
+  auto c0 = [&](int k) __attribute__((always_inline)) { return f32x4{-mcs[k], -mcs[k], -mcs[k], -mcs[k]}; };
   // S^T of query group k against the tile's K rows (8 MFMAs)
   auto scores = [&](int k, const u32x4 (&ka)[2][2][2], f32x4 (&s)[2][2]) __attribute__((always_inline)) {
     const u32x4 qb0 = ld16(qw + (2 * k) * 64 * 8), qb1 = ld16(qw + (2 * k + 1) * 64 * 8);
+    const f32x4 ci = c0(k);
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-        s[c][tt] = mfma16x16x32(ka[c][tt][1], qb1, mfma16x16x32(ka[c][tt][0], qb0, f32x4{0.f, 0.f, 0.f, 0.f}));
+      for (int tt = 0; tt < 2; ++tt) s[c][tt] = mfma16x16x32(ka[c][tt][1], qb1, mfma16x16x32(ka[c][tt][0], qb0, ci));
   };
   // O^T += V^T . P^T for query group k, and the weights' column sums by the same products with a ones
   // operand (10 MFMAs, no VALU adds)
@@ -287,17 +290,23 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
       // mt is this lane group's max (16 of the column's 64 scores): a raise is needed iff some lane group
       // of some column exceeds its column's limit, and only then is the column max formed
       if (__ballot(mt > mlim[k])) {  // some column's max moved by more than kPfLazy: raise all
-        const float mn = fmaxf(mrun[k], max_over_groups_ieee(mt));
-        const float alpha = (mrun[k] == kNegInf) ? 0.f : fast_exp2(mcs[k] - mn * sl2);
+        // t: the column's max relative to its offset. A column with no key yet takes it as its offset (one that
+        // still has none, a padding row, stays inert); the others move up by max(t, 0); the tile's scores and
+        // the accumulators follow.
+        const float t = max_over_groups_ieee(mt);
+        const bool fresh = mlim[k] == kNegInf;
+        const float up = t == kNegInf ? 0.f : fresh ? t : fmaxf(t, 0.f);
+        const float alpha = fresh ? 0.f : fast_exp2(-up);
         lacc[k] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[k][dt] *= alpha;
-        mrun[k] = mn;
-        mlim[k] = mn + thr;
-        // mrun stays -inf only for a column with no key yet (a padding row): keep it inert.
-        mcs[k] = mn == kNegInf ? 0.f : mn * sl2;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) s[c][tt] -= up;
+        mcs[k] += up;
+        mlim[k] = (fresh && t == kNegInf) ? kNegInf : kPfLazy;
       }
-      const float mc = mcs[k];
       // group k's weights on the VALU, one score product of group k+1 beside each quarter tile
       f32x4 sn[2][2];
       u32x4 pB[2];
@@ -305,15 +314,15 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-          if (k + 1 < UPW) sn[c][tt] = mfma16x16x32(ka[c][tt][0], qn0, f32x4{0.f, 0.f, 0.f, 0.f});
+          if (k + 1 < UPW) sn[c][tt] = mfma16x16x32(ka[c][tt][0], qn0, c0(k + 1));
           float pv[4];
-          pv[0] = fast_exp2(__builtin_fmaf(s[c][tt][0], sl2, -mc));
-          pv[1] = fast_exp2(__builtin_fmaf(s[c][tt][1], sl2, -mc));
+          pv[0] = fast_exp2(s[c][tt][0]);
+          pv[1] = fast_exp2(s[c][tt][1]);
           pB[c][2 * tt] = pack_bf16x2(pv[0], pv[1]);
           __builtin_amdgcn_sched_barrier(0);
           if (k + 1 < UPW) sn[c][tt] = mfma16x16x32(ka[c][tt][1], qn1, sn[c][tt]);
-          pv[2] = fast_exp2(__builtin_fmaf(s[c][tt][2], sl2, -mc));
-          pv[3] = fast_exp2(__builtin_fmaf(s[c][tt][3], sl2, -mc));
+          pv[2] = fast_exp2(s[c][tt][2]);
+          pv[3] = fast_exp2(s[c][tt][3]);
           pB[c][2 * tt + 1] = pack_bf16x2(pv[2], pv[3]);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -334,6 +343,19 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   const int nfull = min(max((p0 + 1) / 64, 0), hi / 64);
   issue(0, kA, vA);
   if (ntile > 1) issue(1, kB, vB);
+  // the Q^T operands times sl2, rounded to bf16, in place, once their DMA has landed (it went out before this
+  // wave's share of tile 0: at least 16 / NW requests after it)
+  if (active) {
+    wait_vmcnt<16 / NW>();
+#pragma unroll
+    for (int j = 0; j < 2 * UPW; ++j) {
+      uint16_t *p = qw + j * 64 * 8;
+      u32x4 v = ld16(p);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = pack_bf16x2(bf_lo(v[e]) * sl2, bf_hi(v[e]) * sl2);
+      st16(p, v);
+    }
+  }
   int t = 0;
   if (nfull > 0) {
     for (;; t += 3) {
