@@ -205,11 +205,13 @@ def test_decode_after_store_c1(a8, ref, dev):
 
 
 @pytest.mark.parametrize("nw,tpw,grid", [(4, 2, 512), (4, 2, 1), (4, 2, 3), (1, 1, 7), (2, 1, 64), (2, 2, 256),
-                                         (4, 4, 100), (1, 3, 1000), (1, 2, 2), (2, 8, 40)])
+                                         (4, 4, 100), (1, 3, 1000), (1, 2, 2), (2, 8, 40), (4, 6, 40), (4, 8, 20)])
 def test_decode_stream_shapes(a8, ref, dev, nw, tpw, grid):
     """The streaming kernel at forced launch shapes: chunks of nw * tpw * 64 keys swept by `grid`
     workgroups (grid 1: one workgroup takes every chunk; 64-key chunks: many partials per row, merged by
-    the merge kernel; waves <= 2 with an even tile count: 128-key steps). Ragged lengths, a row map, empty rows; two calls in a row give the same bits."""
+    the merge kernel; waves <= 2 with an even tile count: 128-key steps; whole rows at one unit per
+    workgroup and at two: the unit and rows kernels, tiles past the cache length requested and dropped). Ragged
+    lengths, a row map, empty rows; two calls in a row give the same bits."""
     say(f"case: decode stream waves={nw} tpw={tpw} grid={grid}")
     g = torch.Generator().manual_seed(27)
     b, rows, S = 20, 9, 1500

@@ -62,12 +62,14 @@ def _bits_equal(a, b):
     return torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+@pytest.mark.parametrize("shape", [(4, 8, 48), (4, 8, 192)])
 @pytest.mark.parametrize("mode", ["rowmap=slot", "tick", "rowmap off, mixed slots"])
-def test_store_and_attend_peak_shape(a8, dev, mode):
-    """The C3 launch shape (whole 2048-key rows, 4 waves, 2 units per workgroup), rows at pos = lens - 1:
-    shuffled slots attended through the row map; the tick (slot = row, no row map); no row map with some
-    rows storing into their own cache row and others into rows past the query rows (no new key seen)."""
-    say(f"case: fused store+decode, 96 rows x 2048, shape (4, 8, 48), {mode}")
+def test_store_and_attend_peak_shape(a8, dev, mode, shape):
+    """The C3 launch shape (whole 2048-key rows, 4 waves, 2 units per workgroup) and the one-unit-per-workgroup
+    launch, rows at pos = lens - 1: shuffled slots attended through the row map; the tick (slot = row, no row
+    map); no row map with some rows storing into their own cache row and others into rows past the query rows
+    (no new key seen)."""
+    say(f"case: fused store+decode, 96 rows x 2048, shape {shape}, {mode}")
     b, S = 96, 2048
     g = torch.Generator().manual_seed(41)
     if mode == "rowmap=slot":
@@ -80,7 +82,7 @@ def test_store_and_attend_peak_shape(a8, dev, mode):
     pos = [L - 1 for L in lens]
     x = _inputs(41, b, max(slot) + 1, S, lens, pos, slot)
     for write_q in (True, False):
-        (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, (4, 8, 48), write_q=write_q,
+        (o0, q0, k0, v0), (o1, q1, k1, v1) = _run_both(a8, dev, x, shape, write_q=write_q,
                                                        use_rowmap=(mode == "rowmap=slot"))
         assert _bits_equal(q0, q1) if write_q else not q1.any()           # q untouched when not asked for
         assert _bits_equal(k0, k1) and _bits_equal(v0, v1)
@@ -89,7 +91,7 @@ def test_store_and_attend_peak_shape(a8, dev, mode):
 
 
 @pytest.mark.parametrize("shape", [(4, 8, 64), (4, 2, 100), (2, 2, 37), (1, 2, 9), (1, 1, 200), (2, 16, 5),
-                                   (4, 4, 1)])
+                                   (4, 4, 1), (4, 4, 16), (4, 4, 32)])
 def test_store_and_attend_edge_rows(a8, dev, shape):
     """Ragged lengths; the new key at the end, in the middle of the attended range (lens > pos + 1) or past
     it (pos >= lens); ring wrap (pos >= ring); a slot outside the cache (NaN row, nothing stored); no
