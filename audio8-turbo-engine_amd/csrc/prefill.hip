@@ -32,6 +32,7 @@ namespace a8 {
 
 constexpr int kPfMaxHW = 4;   // q heads (waves) per workgroup: two workgroups fit a compute unit's LDS
 constexpr float kPfLazy = 8.f;  // exp2 units a column's running max may lag behind its scores
+constexpr float kPfLow = -64.f;  // on a block's first tile: a column max below this sets the offset (underflow)
 
 // K chunk permutation of tile row r (see above).
 __device__ __forceinline__ int pf_kswz(int r) { return (r & 3) | (((r >> 3) & 1) << 2); }
@@ -118,12 +119,17 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // Q^T operands: column r16 <-> query row 16qt + r16, slot (g, j) <-> dim 8g+j / 32+8g+j
   uint16_t *qw = qs + w * (4 * 2 * 64 * 8) + lane * 8;
   f32x4 o[UPW][4];   // O^T rows d = 16dt + 4g + i, column = query row 16qt + r16
-  // per query group: the exp2 offset mcs (the column's running max in exp2 units, 0 before its first key) and
-  // the level of a tile's scores, relative to it, above which the offset is raised (kPfLazy once the column
-  // has a key, -inf before)
-  float mlim[UPW], mcs[UPW];
+  // per query group: the exp2 offset mcs (in exp2 units, 0 to start with; see the raise below)
+  float mcs[UPW];
+  f32x4 cneg[UPW];  // {-mcs} x 4: the score products' C operand, kept in registers
   f32x4 lacc[UPW];  // column sums of the weights (all four rows alike)
-  const u32x4 ones{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
+  // bf16 1.0 pairs, made once by an opaque move so that the compiler keeps them in registers (it would
+  // otherwise rebuild the constant before every group's row-sum products)
+  u32x4 ones;
+  asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(ones[0]));
+  ones[1] = ones[0];
+  ones[2] = ones[0];
+  ones[3] = ones[0];
   // The Q^T operands go from HBM straight into LDS by DMA (requested before the first K / V tiles, so the
   // first wait covers both): lane l of request (k, half) reads dims 8g.. (+32) of query row 16k + r16, and
   // rows past nv read as zeros (the descriptor ends at row nv - 1; the host keeps s_qr >= hd).
@@ -142,8 +148,8 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     live[k] = active;
     head[k] = kh * group + gi;
     qt_of[k] = k;
-    mlim[k] = kNegInf;
     mcs[k] = 0.f;
+    cneg[k] = f32x4{0.f, 0.f, 0.f, 0.f};
     lacc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[k][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -175,7 +181,7 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // rescale; until then its weights stay below 2^kPfLazy (well inside bf16's range; the sums are fp32). Same
   // softmax; the roundings happen at other points (q * sl2 once in bf16 instead of the product in fp32). C4, one
   // box: 43.7 -> 43.2 us per layer against the FMA per score.
-  auto c0 = [&](int k) __attribute__((always_inline)) { return f32x4{-mcs[k], -mcs[k], -mcs[k], -mcs[k]}; };
+  auto c0 = [&](int k) __attribute__((always_inline)) { return cneg[k]; };
   // S^T of query group k against the tile's K rows (8 MFMAs)
   auto scores = [&](int k, const u32x4 (&ka)[2][2][2], f32x4 (&s)[2][2]) __attribute__((always_inline)) {
     const u32x4 qb0 = ld16(qw + (2 * k) * 64 * 8), qb1 = ld16(qw + (2 * k + 1) * 64 * 8);
@@ -248,14 +254,16 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
         qn1 = ld16(qw + (2 * k + 3) * 64 * 8);
       }
       if (MASKED) {
-        const int lim = min(p0 + 16 * qt_of[k] + r16, hi - 1);  // keys <= query position (and < hi)
+        // keys <= query position (and < hi): key kt0 + 8g + off of this lane, off = 32c + 4tt + i, against
+        // one threshold per lane (16 compares with constants)
+        const int d = min(p0 + 16 * qt_of[k] + r16, hi - 1) - kt0 - 8 * g;
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              if (kt0 + 32 * c + 8 * g + 4 * tt + i > lim) s[c][tt][i] = kNegInf;
+              if (32 * c + 4 * tt + i > d) s[c][tt][i] = kNegInf;
       }
       // group k's column max on the VALU, one step beside each of group k-1's products (the
       // scheduling barriers keep the interleave: a wave issues in order, so a run of MFMAs would stall
@@ -287,16 +295,21 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
         o[k - 1][3] = mfma16x16x32(va[3][1], pP[1], o[k - 1][3]);
         lacc[k - 1] = mfma16x16x32(ones, pP[1], mfma16x16x32(ones, pP[0], lacc[k - 1]));
       }
-      // mt is this lane group's max (16 of the column's 64 scores): a raise is needed iff some lane group
-      // of some column exceeds its column's limit, and only then is the column max formed
-      if (__ballot(mt > mlim[k])) {  // some column's max moved by more than kPfLazy: raise all
-        // t: the column's max relative to its offset. A column with no key yet takes it as its offset (one that
-        // still has none, a padding row, stays inert); the others move up by max(t, 0); the tile's scores and
-        // the accumulators follow.
+      // mt is this lane group's max (16 of the column's 64 scores). The offset starts at 0 and is raised only
+      // when some lane group of some column passes it by more than kPfLazy (its weights stay below 2^kPfLazy;
+      // the column max is formed only then). On the block's first tile -- key 0 is visible to every row, so
+      // every column has a key there -- it is also set when a lane group's max is below kPfLow, so that a
+      // column's weights cannot all underflow (fp32 reaches 2^-126): a column's largest weight stays in
+      // [2^kPfLow, 2^kPfLazy]. With ordinary scores no raise happens on the first tile (it used to take the
+      // first tile's max as the offset in every group).
+      const bool first = kt0 == 0;
+      if (__ballot(mt > kPfLazy || mt < (first ? kPfLow : kNegInf))) {
+        // t: the column's max relative to its offset; on the first tile it becomes the offset (nothing has
+        // accumulated yet), later the offset moves up by max(t, 0); the tile's scores and the accumulators
+        // follow.
         const float t = max_over_groups_ieee(mt);
-        const bool fresh = mlim[k] == kNegInf;
-        const float up = t == kNegInf ? 0.f : fresh ? t : fmaxf(t, 0.f);
-        const float alpha = fresh ? 0.f : fast_exp2(-up);
+        const float up = first ? t : fmaxf(t, 0.f);
+        const float alpha = first ? 0.f : fast_exp2(-up);
         lacc[k] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[k][dt] *= alpha;
@@ -305,7 +318,7 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
 #pragma unroll
           for (int tt = 0; tt < 2; ++tt) s[c][tt] -= up;
         mcs[k] += up;
-        mlim[k] = (fresh && t == kNegInf) ? kNegInf : kPfLazy;
+        cneg[k] = f32x4{-mcs[k], -mcs[k], -mcs[k], -mcs[k]};
       }
       // group k's weights on the VALU, one score product of group k+1 beside each quarter tile
       f32x4 sn[2][2];
@@ -396,8 +409,8 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     if (!live[k]) continue;
     const int mrow = 16 * qt_of[k] + r16;
     if (mrow >= nv) continue;
-    // a live row has l >= 1 (its largest weight is 2^0 .. 2^kPfLazy): one hardware reciprocal (1 ulp)
-    // instead of sixteen IEEE divisions
+    // a live row has l >= 2^kPfLow (its largest weight is 2^kPfLow .. 2^kPfLazy): one hardware reciprocal
+    // (1 ulp) instead of sixteen IEEE divisions
     const float rl = __builtin_amdgcn_rcpf(lacc[k][0]);
     uint16_t *op = out + (int64_t)(q0 + mrow) * s_or + (int64_t)head[k] * s_oh + 4 * g;
 #pragma unroll
