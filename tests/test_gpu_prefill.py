@@ -109,6 +109,37 @@ def test_prefill_random_cache(a8, ref, dev, seed):
     assert err <= TOL
 
 
+@pytest.mark.parametrize("first,later", [(-4.5, 1.0), (-4.5, -4.5), (4.5, 4.5), (4.5, -4.5), (-2.0, 3.0)])
+def test_prefill_extreme_scores(a8, ref, dev, first, later):
+    """Scores far from 0 in exp2 units (q . k x scale x log2 e up to about +-207): the keys of each block's first
+    tile (positions 0..63) and the later keys are `first` and `later` times a ones vector (plus noise), the
+    queries 4 x ones. Covers the running offset's underflow guard (every first-tile score far below 0,
+    later ones higher or as low), the raise on the first tile (far above 0) and a first tile far above the
+    rest; every row finite and within the bar of the oracle."""
+    say(f"case: prefill extreme scores, first tile {first}, later keys {later}")
+    g = torch.Generator().manual_seed(int(first * 10 + later * 100) & 0xffff)
+    ns, p0s, slots = [64, 150, 40, 1], [100, 0, 400, 511], [0, 1, 2, 3]
+    S, rows = 512, 4
+    R = sum(ns)
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    noise = lambda *shape: (torch.randn(*shape, generator=g) * 0.05)
+    kc = (torch.full((rows, NKV, S, HD), later) + noise(rows, NKV, S, HD))
+    kc[:, :, :64] = first + noise(rows, NKV, 64, HD)
+    kc = kc.to(BF)
+    vc = randn_bf16(g, rows, NKV, S, HD)
+    q = (4.0 + noise(R, NQ, HD)).to(BF)
+    want = torch.zeros(R, NQ, HD, dtype=BF)
+    ref.prefill_attention(q, kc, vc, *ref.prefill_plan(r0s, ns, slots, p0s), want, 7)
+    out = torch.full((R, NQ, HD), float("nan"), dtype=BF, device=dev)
+    a8.prefill_attention(q.to(dev), kc.to(dev), vc.to(dev), a8.PrefillPlan(r0s, ns, slots, p0s, dev), out, 7)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert torch.isfinite(got.float()).all()
+    err = maxabs(got, want)
+    say(f"  max-abs {err:.3e}")
+    assert err <= TOL
+
+
 def test_prefill_graph_mode_plan(a8, ref, dev):
     """The graph-mode plan buffer (padding blocks point at the scratch row with n = 0) gives the same rows as
     an exact PrefillPlan, and leaves rows past the packed tokens untouched."""
