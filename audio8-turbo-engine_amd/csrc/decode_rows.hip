@@ -418,29 +418,26 @@ __global__ __launch_bounds__(64 * kRowsNW, 1) void k_decode_rows(
 
 // One unit (row, kv head) per workgroup: the launch for grids of at least one workgroup per unit (short rows,
 // and row counts whose units do not fill the compute units twice over). Every unit streams at once. The work per
-// wave, the order of its tiles (rotated as in k_decode_rows) and the merge are those of k_decode_rows; each wave
-// parks its partial in its first V buffer (free by then) and the waves merge a slice of the outputs each. D =
-// tiles in flight per wave. NW = 4, D = 2: K and V tiles in LDS (128 KB, one workgroup per compute unit), the
-// same bits as k_decode_rows. Otherwise K in registers and only the V tiles in LDS (D * NW * 8 KB). Every tile
-// buffer is an array of its own, so the compiler tells their DMA apart (a shared array makes it wait for every
-// request before each LDS read).
-template <bool FUSED, int SPW, int NW, int D>
-__global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_decode_unit(
+// wave, the order of its tiles (rotated as in k_decode_rows) and the merge are those of k_decode_rows, so the
+// results are the same bits; each wave parks its partial in its first V buffer (free by then) and the four waves
+// merge a slice of the outputs each. LDS: two K and two V tiles per wave, 128 KB, one workgroup per compute unit.
+// Measured on MI355X at 64-256 units and no faster: 8 waves with K in registers (+2.5 us at 128 units), three
+// or four tiles in flight per wave with K in registers (+2.5 / +2.9 us).
+template <bool FUSED, int SPW>
+__global__ __launch_bounds__(64 * kRowsNW, 2) void k_decode_unit(
     const uint16_t *__restrict__ q, int64_t s_qb, int64_t s_qh,
     uint16_t *kc, uint16_t *vc, int64_t s_kb, int64_t s_kh,
     int cache_rows, int cache_len, const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap,
     uint16_t *__restrict__ out, int64_t s_ob, int64_t s_oh, int b, int nq, int nkv, int group,
     float sl2, StoreIn si) {
-  static_assert(NW == 4 || NW == 8, "waves");
-  static_assert(D >= 2 && D <= 4 && D * NW <= 16 && SPW >= 4, "tiles in flight / steps per unit");
-  constexpr bool KL = NW == 4 && D == 2;  // K tiles in LDS
+  constexpr int NW = kRowsNW;
+  constexpr int D = 2;  // tiles in flight per wave
   warm_kernargs<232>();
-  __shared__ __attribute__((aligned(16))) uint16_t kb0[KL ? NW * kVTile : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t kb1[KL ? NW * kVTile : 8];
+  static_assert(SPW % D == 0 && SPW >= 4, "steps per unit");
+  __shared__ __attribute__((aligned(16))) uint16_t kb0[NW * kVTile];
+  __shared__ __attribute__((aligned(16))) uint16_t kb1[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vb0[NW * kVTile];
   __shared__ __attribute__((aligned(16))) uint16_t vb1[NW * kVTile];
-  __shared__ __attribute__((aligned(16))) uint16_t vb2[D > 2 ? NW * kVTile : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t vb3[D > 3 ? NW * kVTile : 8];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -452,11 +449,8 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_decode_unit(
   tl.init(lane);
   KLdsLane kl;
   kl.init(lane);
-  // this wave's buffers for the tile of step j: index j % D
-  uint16_t *const vbw[4] = {vb0 + w * kVTile, vb1 + w * kVTile, vb2 + (D > 2 ? w * kVTile : 0),
-                            vb3 + (D > 3 ? w * kVTile : 0)};
-  uint16_t *const kbw[2] = {kb0 + (KL ? w * kVTile : 0), kb1 + (KL ? w * kVTile : 0)};
-  KTile KR[KL ? 1 : D];  // K in registers: the K operands of the tiles in flight
+  uint16_t *const vbw[2] = {vb0 + w * kVTile, vb1 + w * kVTile};
+  uint16_t *const kbw[2] = {kb0 + w * kVTile, kb1 + w * kVTile};
 
   // ---- metadata: row map, length, position, slot (vector loads, in order with the tiles) ----
   const rsrc_t lens_r = make_rsrc(lens, (uint32_t)b * 4u);
@@ -486,13 +480,9 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_decode_unit(
   // wave w: tiles w, w + NW, ... of the unit, starting at step u % SPW (as k_decode_rows)
   const int rot = u & (SPW - 1);
   auto tile_of = [&](int j) { return w + NW * ((j + rot) & (SPW - 1)); };
-  auto load_j = [&](int j, int tile) __attribute__((always_inline)) {  // tile `tile` into buffer j % D
-    if constexpr (KL)
-      load_tile_kv(kbw[j & 1], vbw[j & 1], kr, vr, (uint32_t)(64 * tile), tl, kl);
-    else
-      load_tile(KR[KL ? 0 : j % D], vbw[j % D], kr, vr, (uint32_t)(64 * tile), tl);
+  auto first_load = [&](int j) __attribute__((always_inline)) {
+    load_tile_kv(kbw[j & 1], vbw[j & 1], kr, vr, (uint32_t)(64 * tile_of(j)), tl, kl);
   };
-  auto first_load = [&](int j) __attribute__((always_inline)) { load_j(j, tile_of(j)); };
 
   u32x4 q0, q1;
   KVPatch pt;
@@ -570,30 +560,24 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void k_decode_unit(
 
   SoftmaxState S;
   S.reset();
-  // step j: tiles j + 1 .. min(j + D - 1, SPW - 1) were requested after tile j (16 loads each, K then V)
-  auto step = [&](int j) __attribute__((always_inline)) {
+  // tile j + 1 was requested after tile j, except for the last (wait counts as in k_decode_rows)
+  static_assert(D == 2, "wait counts assume one tile requested after the one read");
+  auto step = [&](uint16_t *xk, uint16_t *xv, int j) __attribute__((always_inline)) {
     const int t0 = 64 * tile_of(j);
-    const int after = min(D - 1, SPW - 1 - j);
-    uint16_t *const xv = vbw[j % D];
     if (t0 < hi) {
       KTile X[1];
-      if constexpr (!KL) X[0] = KR[KL ? 0 : j % D];
-      if (after == 0) {
-        if constexpr (KL) read_k_tile<0>(X[0], kbw[j & 1], kl);
+      if (j + 1 == SPW) {
+        read_k_tile<0>(X[0], xk, kl);
         compute_step<1, 0, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
-      } else if (after == 1) {
-        if constexpr (KL) read_k_tile<16>(X[0], kbw[j & 1], kl);
-        compute_step<1, 16, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
-      } else if (after == 2) {
-        compute_step<1, 32, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
       } else {
-        compute_step<1, 48, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
+        read_k_tile<16>(X[0], xk, kl);
+        compute_step<1, 16, FUSED>(X, xv, t0, hi, q0, q1, sl2, S, tl, lane, &pt);
       }
     }
-    if (j + D < SPW) load_j(j, tile_of(j + D));
+    if (j + D < SPW) load_tile_kv(xk, xv, kr, vr, (uint32_t)(64 * tile_of(j + D)), tl, kl);
   };
 #pragma unroll
-  for (int j = 0; j < SPW; ++j) step(j);
+  for (int j = 0; j < SPW; ++j) step(kbw[j & 1], vbw[j & 1], j);
   if (FUSED) {  // the unit's k / v / q, after its last step (as k_decode_rows)
     bst16(skr, sko, pt.lo);
     bst16(skr, sko + 64u, pt.hi);
@@ -618,7 +602,7 @@ static void launch_rows(int grid, hipStream_t st, const uint16_t *q, int64_t s_q
                         const int32_t *rowmap, uint16_t *out, int64_t s_ob, int64_t s_oh, int b, int nq, int nkv,
                         int group, float sl2, const StoreIn &si) {
   if (grid >= b * nkv)  // one unit per workgroup
-    hipLaunchKernelGGL((k_decode_unit<FUSED, SPW, kRowsNW, 2>), dim3(b * nkv), dim3(64 * kRowsNW), 0, st, q, s_qb, s_qh, kc, vc,
+    hipLaunchKernelGGL((k_decode_unit<FUSED, SPW>), dim3(b * nkv), dim3(64 * kRowsNW), 0, st, q, s_qb, s_qh, kc, vc,
                        s_kb, s_kh, cache_rows, cache_len, lens, rowmap, out, s_ob, s_oh, b, nq, nkv, group, sl2, si);
   else
     hipLaunchKernelGGL((k_decode_rows<FUSED, SPW>), dim3(grid), dim3(64 * kRowsNW), 0, st, q, s_qb, s_qh, kc, vc,
