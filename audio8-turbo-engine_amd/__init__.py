@@ -10,12 +10,13 @@ The directory name contains dashes, so it is loaded under the module name `audio
 (see load_package in __graft_entry__.py at the repository root).
 """
 from .fast_kernels import (DecodeAttention, PrefillPlan, bias_rope_store, prefill_attention,  # noqa: F401
-                           prefix_copy, rmsnorm, silu_mul, conv_cl, conv_cl_ws_bytes, conv_out_tanh, snake_cat, ru_cl, gemm_small,
+                           prefill_attention_qkv, prefix_copy, rmsnorm, silu_mul, conv_cl, conv_cl_ws_bytes, conv_out_tanh, snake_cat, ru_cl, gemm_small,
                            gemm_silu_small, gemm_small_norm, fold_norm, gemm_ws_bytes, GemmDispatch)
 from .attn_stack import AttnStack, PrefillMeta, permute_qk, ref_nsplit, rope_tables  # noqa: F401
 from .slow_stack import SlowStack  # noqa: F401
 from ._lib import LIB_PATH, load as load_library, runtime_path, version  # noqa: F401
 
-__all__ = ["bias_rope_store", "DecodeAttention", "PrefillPlan", "prefill_attention", "prefix_copy",
+__all__ = ["bias_rope_store", "DecodeAttention", "PrefillPlan", "prefill_attention", "prefill_attention_qkv",
+           "prefix_copy",
            "rmsnorm", "silu_mul", "conv_cl", "conv_out_tanh", "snake_cat", "ru_cl", "gemm_small", "gemm_silu_small", "gemm_small_norm", "fold_norm", "gemm_ws_bytes", "GemmDispatch", "SlowStack", "AttnStack", "PrefillMeta",
            "permute_qk", "ref_nsplit", "rope_tables", "load_library", "LIB_PATH", "version", "runtime_path"]

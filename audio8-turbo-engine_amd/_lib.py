@@ -67,6 +67,8 @@ SIGNATURES = {
                                   _P, _P, _L, _P, _L, _I, _I, _I, _I, _I, _I, _F, _P]),
     "a8_prefill_attn": (_I, [_P, _L, _L, _I, _P, _P, _L, _L, _L, _I, _I, _P, _L, _L,
                              _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
+    "a8_prefill_attn_qkv": (_I, [_P, _L, _P, _P, _P, _L, _I, _I, _P, _P, _L, _L, _L, _I, _I, _P, _L, _L,
+                                 _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
 }
 
 _lock = threading.Lock()

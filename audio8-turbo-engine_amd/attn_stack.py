@@ -19,7 +19,8 @@ from types import SimpleNamespace
 import numpy as np
 import torch
 
-from .fast_kernels import DecodeAttention, PrefillPlan, bias_rope_store, heaviest_first, prefill_attention
+from .fast_kernels import (DecodeAttention, PrefillPlan, bias_rope_store, heaviest_first, prefill_attention,
+                           prefill_attention_qkv)
 
 
 def rope_tables(base, hd, n, dev):
@@ -75,11 +76,19 @@ class AttnStack:
         slow stack's decode tick: slot[r] = r with rowmap off, fast_engine.py:752-753; or distinct slots
         with rowmap on); the decode then stores and attends in one launch where the schedule allows
         (DecodeAttention.store_and_attend), with the same results. Rows sharing a slot (the fast stack's
-        2-token pass) must keep fuse=False."""
+        2-token pass) must keep fuse=False. With a plan (the admission's packed prefill), fuse=True stores
+        k / v only and the prefill forms q from qkv itself (prefill_attention_qkv; each row's position is its
+        block's pos0 + its index in the block, as the plan of an admission has it): the same out bits, and q
+        is neither written nor read."""
         if plan is None and fuse:
             return self.attn.store_and_attend(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
                                               lens, o, nsplit=nsplit, rowmap=slot if rowmap else None,
                                               ring=self.ring, write_q=False)
+        if plan is not None and fuse:
+            bias_rope_store(qkv, bias, self.cos, self.sin, pos, slot, None, self.kc[i], self.vc[i],
+                            self.nq, self.nkv, self.hd, ring=self.ring)
+            return prefill_attention_qkv(qkv, bias, self.cos, self.sin, self.kc[i], self.vc[i], plan, o,
+                                         self.nq // self.nkv)
         bias_rope_store(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
                         self.nq, self.nkv, self.hd, ring=self.ring)
         if plan is not None:

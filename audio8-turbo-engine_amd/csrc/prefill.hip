@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "decode_tile.h"
+#include "rope.h"
 
 namespace a8 {
 
@@ -51,17 +52,25 @@ __device__ __forceinline__ void pf_dma(int i, uint32_t t0, rsrc_t kr, rsrc_t vr,
     bld16_lds<0>(vr, reinterpret_cast<char *>(vt) + j * 1024, off + (odd ? v1 : v0), 0u);
 }
 
+// The query operands formed from the qkv rows (a8_prefill_attn_qkv): bias and RoPE tables; unused otherwise.
+struct PfQkv {
+  const uint16_t *bias, *cos_tab, *sin_tab;
+  int64_t s_cs;
+  int n_tab;
+};
+
 // UPW = 16-row query groups per wave (the block's 64 rows).
 constexpr int UPW = 4;
-// NW = waves (q heads) per workgroup, 1..kPfMaxHW.
-template <int NW>
+// NW = waves (q heads) per workgroup, 1..kPfMaxHW. QKV: q / s_qr / s_qh address the q columns of the qkv rows
+// (s_qh = the head dimension) and the query operands are formed from them with qk's bias and tables.
+template <int NW, bool QKV>
 __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
     const uint16_t *__restrict__ q, int64_t s_qr, int64_t s_qh, int R,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
     int cache_rows, int cache_len, uint16_t *__restrict__ out, int64_t s_or, int64_t s_oh,
     const int32_t *__restrict__ bq0, const int32_t *__restrict__ bn, const int32_t *__restrict__ bslot,
-    const int32_t *__restrict__ bpos0, int group, int hsplit, int hpw, float sl2, int nh, int nblk_) {
-  warm_kernargs<160>();  // the explicit arguments above span 0x00-0x9f
+    const int32_t *__restrict__ bpos0, int group, int hsplit, int hpw, float sl2, int nh, int nblk_, PfQkv qk) {
+  warm_kernargs<200>();  // the explicit arguments above span 0x00-0xc7
   // a ring of three K and three V tile buffers (tiles are requested two ahead), separate arrays so the
   // compiler tells their DMA apart
   __shared__ __attribute__((aligned(16))) uint16_t kA[kVTile];
@@ -139,15 +148,40 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   // The Q^T operands go from HBM straight into LDS by DMA (requested before the first K / V tiles, so the
   // first wait covers both): lane l of request (k, half) reads dims 8g.. (+32) of query row 16k + r16, and
   // rows past nv read as zeros (the descriptor ends at row nv - 1; the host keeps s_qr >= hd).
+  // QKV: the same chunks of the qkv rows, the bias chunks and the tables' chunks at each row's position go to
+  // registers instead (before the first K / V requests; formed into the operands after them).
+  u32x4 qx[UPW][2], qcs[UPW][4], qb[2];
   if (active) {
     const rsrc_t qrs = make_rsrc(q + (int64_t)q0 * s_qr + (int64_t)(kh * group + gi) * s_qh,
                                  (uint32_t)((int64_t)(nv - 1) * s_qr * 2 + 128));
+    if constexpr (QKV) {
+      const int hq = kh * group + gi;
+      // every operand through a buffer of its own extent (the host keeps n_tab x s_cs x 2 below 2^32):
+      // a position past the tables, or no bias, reads zeros
+      const rsrc_t br = make_rsrc(qk.bias, qk.bias ? (uint32_t)((hq + 1) * 128) : 0u);
+      const uint32_t tab = (uint32_t)((int64_t)qk.n_tab * qk.s_cs * 2);
+      const rsrc_t cr = make_rsrc(qk.cos_tab, tab), sr = make_rsrc(qk.sin_tab, tab);
+      qb[0] = bld16(br, (uint32_t)(hq * 128 + 16 * g));
+      qb[1] = bld16(br, (uint32_t)(hq * 128 + 64 + 16 * g));
 #pragma unroll
-    for (int k = 0; k < UPW; ++k)
+      for (int k = 0; k < UPW; ++k) {
+        qx[k][0] = bld16(qrs, (uint32_t)(((int64_t)(16 * k + r16) * s_qr + 8 * g) * 2));
+        qx[k][1] = bld16(qrs, (uint32_t)(((int64_t)(16 * k + r16) * s_qr + 8 * g + 32) * 2));
+        const int p = p0 + 16 * k + r16;  // >= 0 (p0 is)
+        const uint32_t co = p < qk.n_tab ? (uint32_t)((int64_t)p * qk.s_cs * 2) : tab;
+        qcs[k][0] = bld16(cr, co + 16u * g);
+        qcs[k][1] = bld16(cr, co + 64u + 16u * g);
+        qcs[k][2] = bld16(sr, co + 16u * g);
+        qcs[k][3] = bld16(sr, co + 64u + 16u * g);
+      }
+    } else {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        bld16_lds<0>(qrs, reinterpret_cast<char *>(qs) + (w * 8 + 2 * k + h) * 1024,
-                     (uint32_t)(((int64_t)(16 * k + r16) * s_qr + 8 * g + 32 * h) * 2), 0u);
+      for (int k = 0; k < UPW; ++k)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          bld16_lds<0>(qrs, reinterpret_cast<char *>(qs) + (w * 8 + 2 * k + h) * 1024,
+                       (uint32_t)(((int64_t)(16 * k + r16) * s_qr + 8 * g + 32 * h) * 2), 0u);
+    }
   }
 #pragma unroll
   for (int k = 0; k < UPW; ++k) {
@@ -363,16 +397,43 @@ __global__ __launch_bounds__(64 * kPfMaxHW, 2) void k_prefill(
   issue(0, kA, vA);
   if (ntile > 1) issue(1, kB, vB);
   // the Q^T operands times sl2, rounded to bf16, in place, once their DMA has landed (it went out before this
-  // wave's share of tile 0: at least 16 / NW requests after it)
+  // wave's share of tile 0: at least 16 / NW requests after it). QKV: the operands are the q bias_rope_store
+  // writes (rope.h, the store kernel's arithmetic, with the same bits for every non-NaN input; zeros for rows
+  // past nv and positions outside the tables), then scaled alike and written to the same LDS slots.
   if (active) {
-    wait_vmcnt<16 / NW>();
-#pragma unroll
-    for (int j = 0; j < 2 * UPW; ++j) {
-      uint16_t *p = qw + j * 64 * 8;
-      u32x4 v = ld16(p);
+    auto scale = [&](u32x4 v) __attribute__((always_inline)) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = pack_bf16x2(bf_lo(v[e]) * sl2, bf_hi(v[e]) * sl2);
-      st16(p, v);
+      return v;
+    };
+    if constexpr (QKV) {
+#pragma unroll
+      for (int k = 0; k < UPW; ++k) {
+        float xl[8], xh[8];
+        u32x4 olo, ohi;
+        float ol[8], oh[8];
+        rope_x(qx[k][0], qx[k][1], qb[0], qb[1], qk.bias != nullptr, xl, xh);
+        rope_rotate_f(xl, xh, qcs[k][0], qcs[k][1], qcs[k][2], qcs[k][3], ol, oh);
+        // narrowed by the hardware conversion (round to nearest even: the store's bits for every non-NaN
+        // value, at one instruction per pair)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          olo[e] = pack_bf16x2(ol[2 * e], ol[2 * e + 1]);
+          ohi[e] = pack_bf16x2(oh[2 * e], oh[2 * e + 1]);
+        }
+        const int mrow = 16 * k + r16, p = p0 + mrow;
+        const bool ok = mrow < nv && p < qk.n_tab;
+        const u32x4 z{0u, 0u, 0u, 0u};
+        st16(qw + (2 * k) * 64 * 8, ok ? scale(olo) : z);
+        st16(qw + (2 * k + 1) * 64 * 8, ok ? scale(ohi) : z);
+      }
+    } else {
+      wait_vmcnt<16 / NW>();
+#pragma unroll
+      for (int j = 0; j < 2 * UPW; ++j) {
+        uint16_t *p = qw + j * 64 * 8;
+        st16(p, scale(ld16(p)));
+      }
     }
   }
   // Wave priority (s_setprio, inside this workgroup's waves; no stream priority): 1 while more than half of
@@ -444,26 +505,30 @@ static inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) 
 
 }  // namespace a8
 
-extern "C" int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
-                               const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
-                               int cache_rows, int cache_len,
-                               void *out, int64_t s_or, int64_t s_oh,
-                               const int32_t *bq0, const int32_t *bn, const int32_t *bslot,
-                               const int32_t *bpos0, int nblk, int bm,
-                               int nq, int group, int hd, float scale, void *stream) {
-  using namespace a8;
-  if (hd != 64 && hd != 128)
-    return set_error(A8_EUNSUP, "prefill_attn: head_dim %d not supported (64 or 128)", hd);
-  if (bm != 64) return set_error(A8_EUNSUP, "prefill_attn: block size %d not supported (64 only)", bm);
+namespace a8 {
+// Body of a8_prefill_attn and a8_prefill_attn_qkv (qk non-null: q / s_qr address the qkv rows' q columns).
+static int prefill_entry(const char *fn, const void *q, int64_t s_qr, int64_t s_qh, int R, const void *kc,
+                         const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks, int cache_rows, int cache_len,
+                         void *out, int64_t s_or, int64_t s_oh, const int32_t *bq0, const int32_t *bn,
+                         const int32_t *bslot, const int32_t *bpos0, int nblk, int bm, int nq, int group, int hd,
+                         float scale, const PfQkv *qk, void *stream) {
+  if (hd != 64 && (qk || hd != 128))
+    return set_error(A8_EUNSUP, "%s: head_dim %d not supported (64%s)", fn, hd, qk ? "" : " or 128");
+  if (bm != 64) return set_error(A8_EUNSUP, "%s: block size %d not supported (64 only)", fn, bm);
   if (nblk < 0 || R < 0 || nq <= 0 || group <= 0 || nq % group || cache_rows < 0 || cache_len < 0)
-    return set_error(A8_EINVAL, "prefill_attn: bad sizes nblk=%d R=%d nq=%d group=%d", nblk, R, nq, group);
+    return set_error(A8_EINVAL, "%s: bad sizes nblk=%d R=%d nq=%d group=%d", fn, nblk, R, nq, group);
+  if (qk && (qk->n_tab < 0 || qk->s_cs < hd))
+    return set_error(A8_EINVAL, "%s: bad tables n_tab=%d s_cs=%lld", fn, qk->n_tab, (long long)qk->s_cs);
+  if (qk && (int64_t)qk->n_tab * qk->s_cs * 2 >= (int64_t)UINT32_MAX - 256)  // the tables' 32-bit byte offsets
+    return set_error(A8_EUNSUP, "%s: RoPE tables of %d x %lld too large", fn, qk->n_tab, (long long)qk->s_cs);
   if (nblk == 0 || R == 0) return 0;
-  if (!q || !kc || !vc || !out || !bq0 || !bn || !bslot || !bpos0)
-    return set_error(A8_EINVAL, "prefill_attn: null pointer");
-  if (!al16(q) || !al16(kc) || !al16(vc) || !al16(out) || (s_qr | s_qh | s_kb | s_kh | s_ks | s_or | s_oh) & 7)
-    return set_error(A8_EALIGN, "prefill_attn: pointers must be 16-byte aligned and strides multiples of 8");
+  if (!q || !kc || !vc || !out || !bq0 || !bn || !bslot || !bpos0 || (qk && (!qk->cos_tab || !qk->sin_tab)))
+    return set_error(A8_EINVAL, "%s: null pointer", fn);
+  if (!al16(q) || !al16(kc) || !al16(vc) || !al16(out) || (s_qr | s_qh | s_kb | s_kh | s_ks | s_or | s_oh) & 7 ||
+      (qk && (!al16(qk->cos_tab) || !al16(qk->sin_tab) || (qk->bias && !al16(qk->bias)) || (qk->s_cs & 7))))
+    return set_error(A8_EALIGN, "%s: pointers must be 16-byte aligned and strides multiples of 8", fn);
   if (s_ks != hd)
-    return set_error(A8_EUNSUP, "prefill_attn: cache positions must be contiguous rows (s_ks %lld)", (long long)s_ks);
+    return set_error(A8_EUNSUP, "%s: cache positions must be contiguous rows (s_ks %lld)", fn, (long long)s_ks);
   const int nkv = nq / group;
   if (hd != 64)  // the generic-head kernel
     return attn_cols_prefill(q, s_qr, s_qh, R, kc, vc, s_kb, s_kh, cache_rows, cache_len, out, s_or, s_oh, bq0, bn,
@@ -472,15 +537,44 @@ extern "C" int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
   const int hsplit = (group + hpw - 1) / hpw;
   const int nh = nkv * hsplit;
   if (s_qr < hd || s_qr >= (1 << 25))  // the Q requests' 32-bit byte offsets (63 rows) and their row range
-    return set_error(A8_EUNSUP, "prefill_attn: q row stride %lld outside [%d, 2^25)", (long long)s_qr, hd);
+    return set_error(A8_EUNSUP, "%s: q row stride %lld outside [%d, 2^25)", fn, (long long)s_qr, hd);
   const int64_t grid = ((int64_t)nblk * nkv + 7) / 8 * 8 * hsplit;  // whole runs of 8 units (see k_prefill)
   if (grid * 64 * hpw > (int64_t)UINT32_MAX)  // the launch counts its threads in 32 bits
-    return set_error(A8_EUNSUP, "prefill_attn: too many blocks x heads (%d x %d)", nblk, nh);
+    return set_error(A8_EUNSUP, "%s: too many blocks x heads (%d x %d)", fn, nblk, nh);
   static_assert(kPfMaxHW == 4, "one instantiation per workgroup size");
-  auto kern = hpw == 1 ? k_prefill<1> : hpw == 2 ? k_prefill<2> : hpw == 3 ? k_prefill<3> : k_prefill<4>;
+  const PfQkv none{nullptr, nullptr, nullptr, 0, 0};
+  auto kern = qk ? (hpw == 1 ? k_prefill<1, true> : hpw == 2 ? k_prefill<2, true> : hpw == 3 ? k_prefill<3, true>
+                                                                                            : k_prefill<4, true>)
+                 : (hpw == 1 ? k_prefill<1, false> : hpw == 2 ? k_prefill<2, false> : hpw == 3 ? k_prefill<3, false>
+                                                                                             : k_prefill<4, false>);
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * hpw), 0, (hipStream_t)stream,
                      (const uint16_t *)q, s_qr, s_qh, R, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, s_ks,
                      cache_rows, cache_len, (uint16_t *)out, s_or, s_oh, bq0, bn, bslot, bpos0, group, hsplit, hpw,
-                     scale * kLog2e, nh, nblk);
+                     scale * kLog2e, nh, nblk, qk ? *qk : none);
   return (int)hipGetLastError();
+}
+}  // namespace a8
+
+extern "C" int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
+                               const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                               int cache_rows, int cache_len,
+                               void *out, int64_t s_or, int64_t s_oh,
+                               const int32_t *bq0, const int32_t *bn, const int32_t *bslot,
+                               const int32_t *bpos0, int nblk, int bm,
+                               int nq, int group, int hd, float scale, void *stream) {
+  return a8::prefill_entry("prefill_attn", q, s_qr, s_qh, R, kc, vc, s_kb, s_kh, s_ks, cache_rows, cache_len, out,
+                           s_or, s_oh, bq0, bn, bslot, bpos0, nblk, bm, nq, group, hd, scale, nullptr, stream);
+}
+
+extern "C" int a8_prefill_attn_qkv(const void *qkv, int64_t s_qkv, const void *bias,
+                                   const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab, int R,
+                                   const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                                   int cache_rows, int cache_len,
+                                   void *out, int64_t s_or, int64_t s_oh,
+                                   const int32_t *bq0, const int32_t *bn, const int32_t *bslot,
+                                   const int32_t *bpos0, int nblk, int bm,
+                                   int nq, int group, int hd, float scale, void *stream) {
+  const a8::PfQkv qk{(const uint16_t *)bias, (const uint16_t *)cos_tab, (const uint16_t *)sin_tab, s_cs, n_tab};
+  return a8::prefill_entry("prefill_attn_qkv", qkv, s_qkv, hd, R, kc, vc, s_kb, s_kh, s_ks, cache_rows, cache_len,
+                           out, s_or, s_oh, bq0, bn, bslot, bpos0, nblk, bm, nq, group, hd, scale, &qk, stream);
 }

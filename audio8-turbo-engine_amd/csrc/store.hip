@@ -6,7 +6,8 @@
 //   x  = f32(qkv[r, h*HD + d]) + f32(bias[h*HD + d])
 //   q/k: o[d] = bf16(x[d]*cos[pos, d] + sign(d) * x[(d+HD/2) % HD] * sin[pos, d]),  sign = -1 for d < HD/2
 //   v:   o[d] = bf16(x[d])
-// q goes to qo[r, h]; k / v go to kc / vc[slot[r], h', pos[r] % ring].
+// q goes to qo[r, h]; k / v go to kc / vc[slot[r], h', pos[r] % ring]. qo may be null: then only the k / v heads
+// are launched (the fused prefill, a8_prefill_attn_qkv, forms q itself from the same qkv rows).
 //
 // MI355X layout: one thread owns the partner pair of 16-byte chunks (d = 8c..8c+7 and HD/2+8c..)
 // of one head, so rotate_half needs no cross-lane traffic and every global access is a 128-bit
@@ -24,7 +25,8 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
     uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
     int cache_rows, int cache_len, int nq, int nkv, int ring, int hd) {
   warm_kernargs<168>();  // the explicit arguments above span 0x00-0xa7
-  const int H = nq + 2 * nkv;
+  const int h0 = qo ? 0 : nq;              // first head launched: the k heads when q is not wanted
+  const int H = nq + 2 * nkv - h0;
   const int np = hd >> 4;                  // chunk pairs (threads) per head
   const int half = hd >> 1;                // the partner chunk's offset
   const uint32_t per = (uint32_t)np * (uint32_t)H;  // threads per row (the host keeps R * per below 2^31)
@@ -32,7 +34,7 @@ __global__ __launch_bounds__(256) void k_bias_rope_store(
   if (t >= (uint32_t)R * per) return;
   const int r = (int)(t / per);
   const int rem = (int)(t - (uint32_t)r * per);
-  const int h = rem / np, c = rem - h * np;
+  const int h = h0 + rem / np, c = rem - (h - h0) * np;
 
   // Every load that does not depend on the position goes out before anything waits for it; the position
   // check only decides the stores (so the loads are not held behind it).
@@ -95,12 +97,12 @@ extern "C" int a8_bias_rope_store(const void *qkv, int64_t s_qkv, const void *bi
     return set_error(A8_EINVAL, "bias_rope_store: bad sizes R=%d nq=%d nkv=%d ring=%d n_tab=%d", R, nq, nkv,
                      ring, n_tab);
   if (R == 0) return 0;
-  if (!qkv || !cos_tab || !sin_tab || !pos || !slot || !qo || !kc || !vc)
+  if (!qkv || !cos_tab || !sin_tab || !pos || !slot || !kc || !vc)
     return set_error(A8_EINVAL, "bias_rope_store: null pointer");
-  if (!al16(qkv) || !al16(cos_tab) || !al16(sin_tab) || !al16(qo) || !al16(kc) || !al16(vc) ||
+  if (!al16(qkv) || !al16(cos_tab) || !al16(sin_tab) || (qo && !al16(qo)) || !al16(kc) || !al16(vc) ||
       (bias && !al16(bias)) || (s_qkv | s_cs | s_qo_r | s_qo_h | s_kb | s_kh | s_ks) & 7)
     return set_error(A8_EALIGN, "bias_rope_store: pointers must be 16-byte aligned and strides multiples of 8");
-  const int64_t threads = (int64_t)R * (nq + 2 * nkv) * (hd / 16);
+  const int64_t threads = (int64_t)R * ((qo ? nq : 0) + 2 * nkv) * (hd / 16);
   if (threads >= (int64_t)1 << 31) return set_error(A8_EUNSUP, "bias_rope_store: %d rows x %d heads too many", R, nq + 2 * nkv);
   if (n_tab == 0) return 0;  // no position is inside the tables: nothing is written
   const unsigned grid = (unsigned)((threads + 255) / 256);

@@ -80,9 +80,10 @@ def _check_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv, hd
     _need(cos_tab.shape[1] >= hd, f"RoPE tables have {cos_tab.shape[1]} columns, {hd} needed")
     _check_i32("pos", pos, R)
     _check_i32("slot", slot, R)
-    _check_bf16("qo", qo, 3)
-    _need(qo.shape[0] >= R and qo.shape[1] == nq and qo.shape[2] == hd,
-          f"qo shape {tuple(qo.shape)} does not match [{R}, {nq}, {hd}]")
+    if qo is not None:
+        _check_bf16("qo", qo, 3)
+        _need(qo.shape[0] >= R and qo.shape[1] == nq and qo.shape[2] == hd,
+              f"qo shape {tuple(qo.shape)} does not match [{R}, {nq}, {hd}]")
     _check_cache(kc, vc, nkv, hd)
     _need(isinstance(ring, int) and 1 <= ring < 2 ** 31, f"ring must be an int in [1, 2^31) (got {ring})")
     _check_device(qkv=qkv, bias=bias, cos_tab=cos_tab, sin_tab=sin_tab, pos=pos, slot=slot, qo=qo, kc=kc, vc=vc)
@@ -91,7 +92,8 @@ def _check_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv, hd
 
 def bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv, hd, ring=1 << 30):
     """qkv: [R, (nq+2nkv)*hd]; bias: [(nq+2nkv)*hd] or None. Writes rotated q to qo [R, nq, hd] and k / v
-    into kc / vc [Bslots, nkv, S, hd] at [slot, :, pos % ring] (fast_kernels.py:179-187).
+    into kc / vc [Bslots, nkv, S, hd] at [slot, :, pos % ring] (fast_kernels.py:179-187). qo=None: k / v only
+    (for prefill_attention_qkv, which forms q from qkv itself).
 
     Per row r, head h: x = f32(qkv) + f32(bias); q / k get rotate_half RoPE from the bf16 cos / sin tables
     in fp32 and are rounded once to bf16; v is rounded from x. Rows whose position is outside the tables, or
@@ -104,7 +106,8 @@ def bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, slot, qo, kc, vc, nq, nkv,
         qkv.data_ptr(), qkv.stride(0), bias.data_ptr() if bias is not None else None,
         cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.stride(0), cos_tab.shape[0],
         pos.data_ptr(), slot.data_ptr(), R,
-        qo.data_ptr(), qo.stride(0), qo.stride(1),
+        qo.data_ptr() if qo is not None else None, qo.stride(0) if qo is not None else 0,
+        qo.stride(1) if qo is not None else 0,
         kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
         nq, nkv, hd, ring, _lib.stream_of(qkv))
     _lib.check(st, "bias_rope_store")
@@ -437,6 +440,52 @@ def prefill_attention(q, kc, vc, plan, out, group, scale=None):
         blocks.q0.data_ptr(), blocks.n.data_ptr(), blocks.slot.data_ptr(), blocks.pos0.data_ptr(), nblk, bm,
         nq, group, hd, float(scale), _lib.stream_of(q))
     _lib.check(st, "prefill_attention")
+    return out
+
+
+def prefill_attention_qkv(qkv, bias, cos_tab, sin_tab, kc, vc, plan, out, group, scale=None):
+    """prefill_attention with q formed from the qkv rows inside the launch (a8_prefill_attn_qkv): the q that
+    bias_rope_store(qkv, bias, cos_tab, sin_tab, pos, ...) would write, at each row's position = its block's
+    pos0 + the row's index in the block, with the store's arithmetic -- so, after
+    bias_rope_store(..., qo=None, ...), the two calls leave the same out bits as bias_rope_store then
+    prefill_attention, without writing or re-reading q. No counterpart in the reference (fast_engine.py:127-132
+    makes the two calls). qkv [R, (nq+2nkv)*hd]; out [R, nq, hd]; head_dim 64; other arguments as
+    prefill_attention. A query at a position outside the tables attends with q = 0."""
+    _check_bf16("qkv", qkv, 2)
+    _check_bf16("out", out, 3)
+    nq, hd = out.shape[1], out.shape[2]
+    _need(group >= 1 and nq % group == 0, f"group {group} does not divide nq {nq}")
+    nkv = nq // group
+    width = (nq + 2 * nkv) * hd
+    _need(qkv.shape[1] >= width, f"qkv has {qkv.shape[1]} columns, {width} needed")
+    _need(out.shape[0] >= qkv.shape[0], f"out has {out.shape[0]} rows, qkv {qkv.shape[0]}")
+    if bias is not None:
+        _check_bf16("bias", bias, 1)
+        _need(bias.shape[0] >= width, f"bias has {bias.shape[0]} entries, {width} needed")
+    _check_bf16("cos_tab", cos_tab, 2)
+    _check_bf16("sin_tab", sin_tab, 2)
+    _need(cos_tab.shape == sin_tab.shape and cos_tab.stride() == sin_tab.stride(),
+          "cos_tab and sin_tab must have the same shape and strides")
+    _need(cos_tab.shape[1] >= hd, f"RoPE tables have {cos_tab.shape[1]} columns, {hd} needed")
+    scale = scale if scale is not None else hd ** -0.5
+    _check_cache(kc, vc, nkv, hd)
+    bm = int(getattr(plan, "BM", PrefillPlan.BM))
+    nblk = int(plan.nblk)
+    blocks = getattr(plan, "dispatch", None) or plan
+    for name in ("q0", "n", "slot", "pos0"):
+        _check_i32(f"plan.{name}", getattr(blocks, name), nblk)
+    _check_device(qkv=qkv, bias=bias, cos_tab=cos_tab, sin_tab=sin_tab, kc=kc, vc=vc, out=out,
+                  **{f"plan.{k}": getattr(blocks, k) for k in ("q0", "n", "slot", "pos0")})
+    if nblk == 0 or qkv.shape[0] == 0:
+        return out
+    st = _lib.load().a8_prefill_attn_qkv(
+        qkv.data_ptr(), qkv.stride(0), bias.data_ptr() if bias is not None else None,
+        cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.stride(0), cos_tab.shape[0], qkv.shape[0],
+        kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[0], kc.shape[2],
+        out.data_ptr(), out.stride(0), out.stride(1),
+        blocks.q0.data_ptr(), blocks.n.data_ptr(), blocks.slot.data_ptr(), blocks.pos0.data_ptr(), nblk, bm,
+        nq, group, hd, float(scale), _lib.stream_of(qkv))
+    _lib.check(st, "prefill_attention_qkv")
     return out
 
 

@@ -478,14 +478,26 @@ def per_config(a8, torch, dev, steps, cpu_budget=4.0):
     bias = [randn(W, std=0.02) for _ in range(layers)]
     q = torch.empty(R, NQ, HD, dtype=torch.bfloat16, device=dev)
     outs = [torch.empty(R, NQ, HD, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
-    g = capture(torch, lambda: st.forward(qkv, bias, pos, slot, None, plan=plan, q=q, outs=outs))
+    # the engine's path: k / v stored, q formed inside the prefill (fuse=True); beside it the two-step form
+    # (q written by the store, then read by the prefill), which leaves the same bits
+    g = capture(torch, lambda: st.forward(qkv, bias, pos, slot, None, plan=plan, q=q, outs=outs, fuse=True))
     us = time_median(torch, g, steps, 10) * 1e3 / layers
+    del g
+    g = capture(torch, lambda: st.forward(qkv, bias, pos, slot, None, plan=plan, q=q, outs=outs))
+    us_unfused = time_median(torch, g, steps, 10) * 1e3 / layers
     del g
 
     def pf_only():
         for i in range(layers):
             a8.prefill_attention(q, st.kc[i], st.vc[i], plan, outs[i], NQ // NKV)
 
+    def pf_qkv_only():
+        for i in range(layers):
+            a8.prefill_attention_qkv(qkv[i], bias[i], st.cos, st.sin, st.kc[i], st.vc[i], plan, outs[i], NQ // NKV)
+
+    g = capture(torch, pf_qkv_only)
+    us_pf_qkv = time_median(torch, g, steps, 10) * 1e3 / layers
+    del g
     g = capture(torch, pf_only)
     us_pf = time_median(torch, g, steps, 10) * 1e3 / layers
     flops = ref_counts.prefill_flops(ns, [p0] * nreq, NQ, HD)
@@ -511,7 +523,8 @@ def per_config(a8, torch, dev, steps, cpu_budget=4.0):
     g = capture(torch, pcopy_torch)
     us_pc_torch = time_median(torch, g, steps, 10) * 1e3
     pc_bytes = 2 * layers * NKV * p0 * HD * 2 * (nreq + 4)  # K+V written into 64 slots + the 4 prefixes read
-    res["C4"] = {"us_per_layer": round(us, 3), "prefill_us_per_layer": round(us_pf, 3),
+    res["C4"] = {"us_per_layer": round(us, 3), "unfused_us_per_layer": round(us_unfused, 3),
+                 "prefill_us_per_layer": round(us_pf, 3), "prefill_qkv_us_per_layer": round(us_pf_qkv, 3),
                  "prefix_copy": {"us": round(us_pc, 3), "GB/s": round(pc_bytes / us_pc / 1e3, 1),
                                  "frac_hbm": round(pc_bytes / us_pc / 1e3 / HBM_PEAK_GBS, 4), "bytes": pc_bytes,
                                  "torch_index_put_us": round(us_pc_torch, 3),
@@ -519,7 +532,10 @@ def per_config(a8, torch, dev, steps, cpu_budget=4.0):
                  "prefill_TFLOP/s": round(flops / us_pf / 1e6, 1),
                  "frac_mfma_bf16": round(flops / us_pf / 1e6 / MFMA_BF16_TFLOPS, 4), "flops_per_layer": flops,
                  "rows": R, "blocks": plan.nblk,
-                 "note": "store + prefill per layer; the prefill's fp32 softmax VALU work bounds it before MFMA does"}
+                 "note": "us_per_layer: the k / v store + the prefill forming q from the qkv rows (fuse=True); "
+                         "unfused: the store writing q too, then the prefill reading it (same bits); prefill_*: the "
+                         "launch alone over a stored q / over the qkv rows; the prefill's fp32 softmax VALU work "
+                         "bounds it before MFMA does"}
     if cpu_budget > 0:  # the CPU oracle on layer 0: store, then the packed prefill (prefix already in the caches)
         kc_h, vc_h = st.kc[0].cpu(), st.vc[0].cpu()
         qkv_h, bias_h, pos_h, slot_h = qkv[0].cpu(), bias[0].cpu(), pos.cpu(), slot.cpu()
@@ -726,7 +742,8 @@ def slow_probe(a8, torch, dev, shapes=None):
 
 def prefill_probe(a8, torch, dev):
     """Counter target for the prefill: the C4 workload (64 requests, n ~ U[40, 400] after a 300-position
-    prefix, 13,745 packed rows) launched 3 times. Run under rocprofv3 --pmc with one counter group a pass."""
+    prefix, 13,745 packed rows) launched 3 times over a stored q, then 3 times forming q from qkv rows. Run
+    under rocprofv3 --pmc with one counter group a pass."""
     import numpy as np
     g = torch.Generator(device=dev).manual_seed(7)
     ns = torch.randint(40, 401, (64,), generator=torch.Generator().manual_seed(0)).tolist()
@@ -740,8 +757,15 @@ def prefill_probe(a8, torch, dev):
     plan = a8.PrefillPlan(r0s, ns, list(range(nreq)), [p0] * nreq, dev)
     for _ in range(3):
         a8.prefill_attention(q, kc, vc, plan, out, NQ // NKV)
+    # then the launch forming q from qkv rows (the k / v columns unused here), 3 times
+    W = (NQ + 2 * NKV) * HD
+    qkv = torch.randn(R, W, generator=g, device=dev).to(torch.bfloat16)
+    bias = (0.02 * torch.randn(W, generator=g, device=dev)).to(torch.bfloat16)
+    cos, sin = a8.rope_tables(10000.0, HD, S, dev)
+    for _ in range(3):
+        a8.prefill_attention_qkv(qkv, bias, cos, sin, kc, vc, plan, out, NQ // NKV)
     torch.cuda.synchronize()
-    print(f"prefill probe: 3 launches, {R} rows, {plan.nblk} blocks", flush=True)
+    print(f"prefill probe: 3 + 3 launches (q stored / q from qkv), {R} rows, {plan.nblk} blocks", flush=True)
 
 
 def main():

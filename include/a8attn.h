@@ -63,7 +63,9 @@ const char *a8_hip_runtime_path(void);
  * bias    [(nq + 2*nkv) * hd] or NULL
  * cos_tab, sin_tab [n_tab, hd] row stride s_cs (rotate_half tables, see a1 _rope_tables)
  * pos, slot [R] int32
- * qo      [R, nq, hd] strides (s_qo_r, s_qo_h, 1)            <- rotated q
+ * qo      [R, nq, hd] strides (s_qo_r, s_qo_h, 1)            <- rotated q; or NULL: no q (only the
+ *                                                               k / v heads run; for a8_prefill_attn_qkv,
+ *                                                               which forms q from qkv itself)
  * kc, vc  slot cache                                         <- rotated k / biased v at
  *                                                               [slot[r], h, pos[r] % ring, :]
  * Per row r and head h: x = f32(qkv) + f32(bias); q/k: o = bf16(x*cos + sign*x[(d+hd/2)%hd]*sin)
@@ -293,6 +295,28 @@ int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
                     const int32_t *bq0, const int32_t *bn, const int32_t *bslot,
                     const int32_t *bpos0, int nblk, int bm,
                     int nq, int group, int hd, float scale, void *stream);
+
+/*
+ * a8_prefill_attn with q formed from the qkv rows inside the launch: no counterpart in the reference, which
+ * writes q with bias_rope_store and reads it back in prefill_attention (serve/fast_engine.py:127-132 with
+ * fast_kernels.py:179-187 and 350-358). Paired with a8_bias_rope_store(qo = NULL), the admission step neither
+ * writes nor re-reads q. The query operands are exactly the q bias_rope_store would write: x = f32(qkv) +
+ * f32(bias), rotate_half RoPE from the tables' row at the query position (block start bpos0 + row within the
+ * block), rounded to bf16 with the store's arithmetic -- so the outputs are the bits of the two calls, for
+ * finite qkv / bias and query positions inside [0, n_tab) (a query at a position outside the tables attends
+ * with q = 0; the two-call path leaves its q unwritten).
+ * qkv     [R, (nq + 2*nkv) * hd] row stride s_qkv (columns contiguous); bias [(nq + 2*nkv) * hd] or NULL
+ * cos_tab, sin_tab [n_tab, hd] row stride s_cs (>= hd; n_tab * s_cs * 2 bytes below 2^32)
+ * Other arguments: those of a8_prefill_attn. hd 64 only.
+ */
+int a8_prefill_attn_qkv(const void *qkv, int64_t s_qkv, const void *bias,
+                        const void *cos_tab, const void *sin_tab, int64_t s_cs, int n_tab, int R,
+                        const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,
+                        int cache_rows, int cache_len,
+                        void *out, int64_t s_or, int64_t s_oh,
+                        const int32_t *bq0, const int32_t *bn, const int32_t *bslot,
+                        const int32_t *bpos0, int nblk, int bm,
+                        int nq, int group, int hd, float scale, void *stream);
 
 /*
  * A voice prefix's K and V into the cache rows of the requests that use it, one launch for all layers

@@ -22,7 +22,7 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     assert set(declared_functions()) == {"a8_version", "a8_last_error", "a8_hip_runtime_path", "a8_bias_rope_store",
                                          "a8_decode_attn", "a8_decode_attn_noalloc", "a8_decode_choose", "a8_decode_attn_stream",
-                                         "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn",
+                                         "a8_decode_choose_stream", "a8_store_decode_stream", "a8_prefill_attn", "a8_prefill_attn_qkv",
                                          "a8_decode_attn_flat", "a8_decode_choose_flat", "a8_store_decode_flat",
                                          "a8_store_decode_split", "a8_prefix_copy", "a8_rmsnorm", "a8_silu_mul", "a8_gemm_small", "a8_gemm_silu_small", "a8_gemm_small_norm", "a8_ru_cl", "a8_decode_attn_f32q",
                                          "a8_conv_cl", "a8_conv_cl_ws_bytes", "a8_snake_cat", "a8_conv_out_tanh", "a8_snake_cat_refresh", "a8_gemm_small_norm_pf"}
@@ -66,7 +66,7 @@ def test_store_rejects_before_launch(a8):
     assert lib.a8_bias_rope_store(*_store_args(ring=0)) == -1
     assert lib.a8_bias_rope_store(*_store_args(qkv=24)) == -2          # misaligned pointer
     assert lib.a8_bias_rope_store(*_store_args(s_qkv=1151)) == -2      # stride not a multiple of 8
-    assert lib.a8_bias_rope_store(*_store_args(qo=None)) == -1
+    assert lib.a8_bias_rope_store(*_store_args(kc=None)) == -1         # (qo may be null: k / v only)
     assert lib.a8_bias_rope_store(*_store_args(R=0)) == 0              # nothing to do, nothing launched
 
 
@@ -119,6 +119,31 @@ def test_prefill_rejects_before_launch(a8):
     assert lib.a8_prefill_attn(*_prefill_args(group=5)) == -1
     assert lib.a8_prefill_attn(*_prefill_args(s_qr=900)) == -2
     assert lib.a8_prefill_attn(*_prefill_args(nblk=0)) == 0
+
+
+def _prefill_qkv_args(**kw):
+    a = dict(qkv=16, s_qkv=1152, bias=None, cos=16, sin=16, s_cs=64, n_tab=8, R=4, kc=16, vc=16, s_kb=1024,
+             s_kh=512, s_ks=64, rows=1, S=8, out=16, s_or=896, s_oh=64, bq0=16, bn=16, bslot=16, bpos0=16,
+             nblk=1, bm=64, nq=14, group=7, hd=64, scale=0.125, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+def test_prefill_qkv_rejects_before_launch(a8):
+    """a8_prefill_attn_qkv refuses what a8_prefill_attn refuses, head_dim 128 (64 only), a missing table,
+    misaligned, short or oversized tables before any launch."""
+    lib = a8.load_library()
+    f = lib.a8_prefill_attn_qkv
+    assert f(*_prefill_qkv_args(bm=32)) == -3
+    assert f(*_prefill_qkv_args(hd=128)) == -3 and b"head_dim 128" in lib.a8_last_error()
+    assert f(*_prefill_qkv_args(group=5)) == -1
+    assert f(*_prefill_qkv_args(cos=None)) == -1
+    assert f(*_prefill_qkv_args(sin=24)) == -2
+    assert f(*_prefill_qkv_args(s_cs=68)) == -2                 # not a multiple of 8
+    assert f(*_prefill_qkv_args(s_cs=56)) == -1                 # rows shorter than head_dim
+    assert f(*_prefill_qkv_args(n_tab=-1)) == -1
+    assert f(*_prefill_qkv_args(n_tab=1 << 25)) == -3           # tables past 32-bit byte offsets
+    assert f(*_prefill_qkv_args(nblk=0)) == 0
 
 
 def _choose(lib, b, nkv=2, S=2048, req=1, nmax=16, cap=8192, n_cu=256):

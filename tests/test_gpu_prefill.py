@@ -311,3 +311,178 @@ def test_prefill_groups(a8, ref, dev, nq, nkv):
     assert torch.isfinite(got[:R].float()).all()
     assert err <= TOL
     assert (got[R:].float() == 7.0).all()
+
+
+def _bits(a, b):
+    return torch.equal(a.cpu().view(torch.int16), b.cpu().view(torch.int16))
+
+
+def _store_prefill_both(a8, dev, qkv, bias, cos, sin, pos, slot, kc, vc, plan, nq, nkv, R):
+    """bias_rope_store + prefill_attention against bias_rope_store(qo=None) + prefill_attention_qkv on copies of
+    the same caches: (out, kc, vc, q) of the first, (out, kc, vc) of the second."""
+    res = []
+    for fused in (False, True):
+        kd, vd = kc.clone(), vc.clone()
+        out = torch.full((R, nq, HD), 7.0, dtype=BF, device=dev)
+        if fused:
+            a8.bias_rope_store(qkv, bias, cos, sin, pos, slot, None, kd, vd, nq, nkv, HD)
+            a8.prefill_attention_qkv(qkv, bias, cos, sin, kd, vd, plan, out, nq // nkv)
+            res.append((out, kd, vd))
+        else:
+            q = torch.zeros(R, nq, HD, dtype=BF, device=dev)
+            a8.bias_rope_store(qkv, bias, cos, sin, pos, slot, q, kd, vd, nq, nkv, HD)
+            a8.prefill_attention(q, kd, vd, plan, out, nq // nkv)
+            res.append((out, kd, vd, q))
+    torch.cuda.synchronize()
+    return res
+
+
+def test_prefill_qkv_c4_matches_unfused(a8, ref, dev):
+    """Config 4 at full size: the store (k / v only) + the prefill forming q from the qkv rows leave the same
+    out and cache bits as the store (q, k, v) + the prefill over the stored q, and the out is within the bar of
+    the oracle's."""
+    say("case: fused-q prefill C4 full size vs store + prefill")
+    g = torch.Generator().manual_seed(36)
+    ns, S, pk, pv = _c4(g)
+    p0, nreq = 300, len(ns)
+    W = (NQ + 2 * NKV) * HD
+    R = sum(ns)
+    qkv, bias = randn_bf16(g, R, W), randn_bf16(g, W, std=0.02)
+    cos, sin = ref.rope_tables(10000.0, HD, 2048)
+    pos = torch.cat([p0 + torch.arange(n) for n in ns]).int()
+    slot = torch.cat([torch.full((n,), i) for i, n in enumerate(ns)]).int()
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    kc = torch.zeros(nreq + 1, NKV, S, HD, dtype=BF)
+    vc = torch.zeros_like(kc)
+    for i in range(nreq):
+        kc[i, :, :p0], vc[i, :, :p0] = pk[i % 4], pv[i % 4]
+    plan = a8.PrefillPlan(r0s, ns, list(range(nreq)), [p0] * nreq, dev)
+    (o1, k1, v1, q1), (o2, k2, v2) = _store_prefill_both(
+        a8, dev, qkv.to(dev), bias.to(dev), cos.to(dev), sin.to(dev), pos.to(dev), slot.to(dev), kc.to(dev),
+        vc.to(dev), plan, NQ, NKV, R)
+    assert _bits(o1, o2) and _bits(k1, k2) and _bits(v1, v2)
+    q_c = torch.empty(R, NQ, HD, dtype=BF)
+    ref.bias_rope_store(qkv, bias, cos, sin, pos, slot, q_c, kc, vc, NQ, NKV, HD)
+    want = torch.zeros(R, NQ, HD, dtype=BF)
+    ref.prefill_attention(q_c, kc, vc, *ref.prefill_plan(r0s, ns, list(range(nreq)), [p0] * nreq), want, 7)
+    err = maxabs(o2, want)
+    say(f"  R={R} blocks={plan.nblk} bits equal, max-abs vs oracle {err:.3e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("nq,nkv,with_bias", [(14, 2, True), (14, 2, False), (16, 1, True), (8, 2, True),
+                                              (4, 4, True), (10, 2, False), (12, 2, True)])
+def test_prefill_qkv_groups(a8, ref, dev, nq, nkv, with_bias):
+    """The fused-q prefill over every workgroup shape, with padding blocks (n = 0) in the plan, qkv rows wider
+    than the projection (row stride W + 64), and RoPE tables of 400 positions that end inside some requests
+    (the store writes nothing for those rows; the unfused q rows stay 0, the fused prefill attends with q = 0):
+    the same out and cache bits as the unfused pair, rows past the packed tokens untouched, and the out within
+    the bar of the oracle's."""
+    group = nq // nkv
+    say(f"case: fused-q prefill nq={nq} nkv={nkv} bias={with_bias}")
+    g = torch.Generator().manual_seed(60 + 3 * group + nkv + (7 if with_bias else 0))
+    S, n_tab = 704, 400
+    ns = torch.randint(1, 65, (40,), generator=g).tolist() + torch.randint(100, 301, (8,), generator=g).tolist()
+    p0s = torch.randint(0, 101, (40,), generator=g).tolist() + torch.randint(0, 301, (8,), generator=g).tolist()
+    ns, p0s = ns + [120], p0s + [350]  # a request running past the tables
+    nreq = len(ns)
+    slots = torch.randperm(nreq, generator=g).tolist()
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    R = sum(ns)
+    W = (nq + 2 * nkv) * HD
+    wide = randn_bf16(g, R, W + 64)
+    bias = randn_bf16(g, W, std=0.02) if with_bias else None
+    cos, sin = ref.rope_tables(10000.0, HD, n_tab)
+    pos = torch.cat([a + torch.arange(n) for a, n in zip(p0s, ns)]).int()
+    slot = torch.cat([torch.full((n,), s_) for s_, n in zip(slots, ns)]).int()
+    kc, vc = randn_bf16(g, nreq + 1, nkv, S, HD), randn_bf16(g, nreq + 1, nkv, S, HD)
+    plan = a8.PrefillPlan(r0s, ns, slots, p0s, dev)
+    cols = [t.cpu().tolist() for t in (plan.q0, plan.n, plan.slot, plan.pos0)]
+    blocks = []
+    for i, b in enumerate(zip(*cols)):
+        blocks.append(b)
+        if i % 8 == 7:
+            blocks.append((R, 0, nreq, 0))
+    t = torch.tensor(blocks, dtype=torch.int32).T.contiguous().to(dev)
+
+    class Plan:
+        BM, nblk = 64, len(blocks)
+        q0, n, slot, pos0 = t[0], t[1], t[2], t[3]
+
+    assert int(pos.max()) >= n_tab  # some rows past the tables
+    qkv_d = wide.to(dev)[:, :W]
+    (o1, k1, v1, q1), (o2, k2, v2) = _store_prefill_both(
+        a8, dev, qkv_d, bias.to(dev) if bias is not None else None, cos.to(dev), sin.to(dev), pos.to(dev),
+        slot.to(dev), kc.to(dev), vc.to(dev), Plan, nq, nkv, R)
+    assert _bits(o1, o2) and _bits(k1, k2) and _bits(v1, v2)
+    # the oracle's store on the rows inside the tables (it indexes the tables by position)
+    keep = pos < n_tab
+    q_in = torch.zeros(int(keep.sum()), nq, HD, dtype=BF)
+    kl, vl = kc.clone(), vc.clone()
+    ref.bias_rope_store(wide[keep][:, :W], bias, cos, sin, pos[keep], slot[keep], q_in, kl, vl, nq, nkv, HD)
+    q_c = torch.zeros(R, nq, HD, dtype=BF)
+    q_c[keep] = q_in
+    assert _bits(q1, q_c) and _bits(k2, kl) and _bits(v2, vl)
+    want = torch.zeros(R, nq, HD, dtype=BF)
+    ref.prefill_attention(q_c, kl, vl, *ref.prefill_plan(r0s, ns, slots, p0s), want, group)
+    err = maxabs(o2, want)
+    say(f"  R={R} blocks={len(blocks)} bits equal, max-abs vs oracle {err:.3e}")
+    assert torch.isfinite(o2.float()).all() and err <= TOL
+
+
+def test_attn_stack_prefill_fused_graph(a8, dev):
+    """AttnStack.forward with a plan and fuse=True (k / v stored, q formed inside the prefill), captured in a
+    graph over a PrefillMeta buffer and replayed for two admissions: every replay equals the unfused eager
+    forward (q written, then read) bit for bit in out and caches."""
+    say("case: stack prefill fused-q, graph replays vs unfused eager")
+    g = torch.Generator().manual_seed(37)
+    NT, NR, rows, S, layers = 512, 8, 9, 640, 2
+    W = (NQ + 2 * NKV) * HD
+    st = a8.AttnStack(layers, NQ, NKV, HD, 10000.0, max_rows=NT, cache_rows=rows, cache_len=S, max_pos=S, dev=dev)
+    meta = a8.PrefillMeta(NT, NR, rows - 1, dev)
+    nt = 512
+    qkv = [torch.zeros(NT, W, dtype=BF, device=dev) for _ in range(layers)]
+    bias = [randn_bf16(g, W, std=0.02).to(dev) for _ in range(layers)]
+    q = torch.zeros(NT, NQ, HD, dtype=BF, device=dev)
+    outs = [torch.zeros(NT, NQ, HD, dtype=BF, device=dev) for _ in range(layers)]
+    v = meta.v
+
+    def body(fuse):
+        st.forward(qkv, bias, v.pos[:nt], v.slot[:nt], None, plan=meta.plan(nt), q=q, outs=outs, fuse=fuse)
+
+    admissions = [([0, 3, 1], [130, 7, 64], [200, 0, 17]), ([7, 6, 4, 0, 1], [1, 64, 65, 100, 250],
+                                                             [300, 300, 0, 20, 300])]
+    meta.load(nt, *admissions[0])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body(True)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        body(True)
+    torch.cuda.synchronize()
+    for slots, ns, starts in admissions:
+        R = sum(ns)
+        kc0 = randn_bf16(g, layers, rows, NKV, S, HD).to(dev)
+        vc0 = randn_bf16(g, layers, rows, NKV, S, HD).to(dev)
+        x = [randn_bf16(g, R, W).to(dev) for _ in range(layers)]
+        res = []
+        for mode in ("graph", "unfused"):
+            st.kc_all.copy_(kc0)
+            st.vc_all.copy_(vc0)
+            meta.load(nt, slots, ns, starts)
+            for i in range(layers):
+                qkv[i].zero_()
+                qkv[i][:R].copy_(x[i])
+                outs[i].zero_()
+            if mode == "graph":
+                graph.replay()
+            else:
+                body(False)
+            torch.cuda.synchronize()
+            res.append(([o[:R].cpu() for o in outs], st.kc_all.cpu(), st.vc_all.cpu()))
+        (og, kg, vg), (oe, ke, ve) = res
+        assert all(_bits(a, b) for a, b in zip(og, oe))
+        assert _bits(kg, ke) and _bits(vg, ve)
+        say(f"  admission {slots}: graph replay == unfused eager")
