@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "liba8attn.so")
 SOURCES = ["capi.hip", "store.hip", "decode.hip", "decode_stream.hip", "decode_rows.hip", "decode_flat.hip", "prefill.hip",
-           "attn_cols.hip",
+           "prefill128.hip", "attn_cols.hip",
            "prefix_copy.hip", "layer_ops.hip", "gemm.hip", "decode_f32q.hip", "conv.hip"]
 
 HIPCC_FLAGS = [

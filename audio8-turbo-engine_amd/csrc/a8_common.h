@@ -267,15 +267,16 @@ __device__ __forceinline__ void transpose8x8_bf16(const u32x4 (&in)[8], u32x4 (&
 // (defined in capi.hip).
 int set_error(int code, const char *fmt, ...);
 
-// The generic-head attention kernel (attn_cols.hip): decode and packed prefill for head_dim 128, behind
-// the decode and prefill entry points (which check their arguments first).
+// The generic-head decode kernel (attn_cols.hip) for head_dim 128, behind the decode entry points (which check
+// their arguments first).
 int attn_cols_decode(const char *fn, const void *q, int64_t s_qb, int64_t s_qh, const void *kc, const void *vc,
                      int64_t s_kb, int64_t s_kh, int cache_rows, int cache_len, const int32_t *lens,
                      const int32_t *rowmap, void *out, int64_t s_ob, int64_t s_oh, int b, int nq, int nkv, int hd,
                      float scale, hipStream_t stream);
-int attn_cols_prefill(const void *q, int64_t s_qr, int64_t s_qh, int R, const void *kc, const void *vc, int64_t s_kb,
-                      int64_t s_kh, int cache_rows, int cache_len, void *out, int64_t s_or, int64_t s_oh,
-                      const int32_t *bq0, const int32_t *bn, const int32_t *bslot, const int32_t *bpos0, int nblk,
-                      int nq, int group, int hd, float scale, hipStream_t stream);
+// The head_dim-128 packed prefill (prefill128.hip), behind a8_prefill_attn (which checks its arguments first).
+int prefill128(const void *q, int64_t s_qr, int64_t s_qh, int R, const void *kc, const void *vc, int64_t s_kb,
+               int64_t s_kh, int cache_rows, int cache_len, void *out, int64_t s_or, int64_t s_oh, const int32_t *bq0,
+               const int32_t *bn, const int32_t *bslot, const int32_t *bpos0, int nblk, int nq, int group,
+               float scale, hipStream_t stream);
 
 }  // namespace a8

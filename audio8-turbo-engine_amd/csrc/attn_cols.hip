@@ -1,12 +1,11 @@
-// Attention for head dimensions other than 64 (head_dim 128): decode (a8_decode_attn*) and packed prefill
-// (a8_prefill_attn) through one kernel, for the reference's generic-HD kernels (serve/fast_kernels.py:190-290
-// decode, 296-358 prefill: HD is a compile-time constant there, any power of two).
+// Decode attention for head dimensions other than 64 (head_dim 128): a8_decode_attn* through one kernel, for
+// the reference's generic-HD decode kernels (serve/fast_kernels.py:190-290: HD is a compile-time constant
+// there, any power of two). The head_dim-128 packed prefill is prefill128.hip.
 //
 // One wave computes up to 16 attention columns that share a cache row and a kv head; column j (lane r16 = j of
-// each 16-lane group) is one (query row, q head) with its own key count L_j: it attends keys [0, L_j) of the
-// cache row, online softmax in fp32 (exp2 with the scale folded in, the weights rounded to bf16 for P.V as in
-// the reference, the row sum of the fp32 weights), out = bf16(acc / l). Decode: the group's q heads of one
-// query row (L = lens); prefill: 16 consecutive rows of one block and q head (L = position + 1, causal).
+// each 16-lane group) is q head kh * group + j of one query row, which attends keys [0, L) of the cache row
+// (L = lens), online softmax in fp32 (exp2 with the scale folded in, the weights rounded to bf16 for P.V as in
+// the reference, the row sum of the fp32 weights), out = bf16(acc / l).
 //
 // Per 64-key tile, with the MFMA layouts of the head_dim-64 kernels (v_mfma_f32_16x16x32_bf16):
 //   * S^T = K.Q^T: tile (c, t) rows 4g+i <-> key t0 + 32c + 8g + 4t + i; the K operand (lane (g, r16): key
@@ -16,105 +15,59 @@
 //     wave-private LDS tile, row r's 16-byte chunks permuted by chunk ^= 2 (r & 3) (the permutation goes into
 //     the DMA's source offsets), so the transposing reads of four consecutive rows hit distinct banks; it is
 //     read as V^T by ds_read_b64_tr_b16, HD/16 row blocks of 16 dims.
-// One wave per column group, NWV independent waves per workgroup. Decode: one wave per workgroup and two tile
-// buffers (PIPE), the next tile's K / V requests in flight while a tile is computed (four waves with one buffer
-// measured 105.8 us per layer at 192 rows x 2048 keys, 0.48 of HBM; this 73.4 us, 0.69). Prefill: four waves
-// per workgroup -- the four 16-row column groups of one (block, q head), whose K / V reads then meet in one
-// compute unit's cache -- and one buffer each (one-wave workgroups measured 237-240 us at C4 against 219 us).
+// One wave per workgroup and column group, two tile buffers: the next tile's K / V requests in flight while a
+// tile is computed (four waves with one buffer measured 105.8 us per layer at 192 rows x 2048 keys, 0.48 of
+// HBM; this 73.4 us, 0.69).
 #include "decode_tile.h"
 
 namespace a8 {
 namespace {
 
 
-// The column group of one wave: its columns' query / output rows, q heads and key counts (per lane), the
-// cache row and kv head (uniform), and the wave's largest and smallest key counts over its valid columns.
-struct ColGroup {
-  bool ok;          // the wave has work
-  int64_t crow;     // cache row
-  int kh;           // kv head
-  int lmax, lmin;   // over valid columns (uniform)
-  bool valid;       // this lane's column exists
-  int64_t qrow;     // this lane's query row (and output row)
-  int head;         // this lane's q head
-  int L;            // this lane's key count
-};
-
-template <int HD, bool PIPE, int NWV>
-__global__ __launch_bounds__(64 * NWV) void k_attn_cols(
-    const uint16_t *__restrict__ q, int64_t s_qr, int64_t s_qh, int R,
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_cols(
+    const uint16_t *__restrict__ q, int64_t s_qr, int64_t s_qh,
     const uint16_t *__restrict__ kc, const uint16_t *__restrict__ vc, int64_t s_kb, int64_t s_kh,
     int cache_rows, int cache_len, uint16_t *__restrict__ out, int64_t s_or, int64_t s_oh,
-    // decode (prefill = false): lens [b], rowmap [b] or null; prefill: the block plan
-    const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap, const int32_t *__restrict__ bq0,
-    const int32_t *__restrict__ bn, const int32_t *__restrict__ bslot, const int32_t *__restrict__ bpos0,
-    int ngroups, int nq, int nkv, int group, bool prefill, float sl2) {
+    const int32_t *__restrict__ lens, const int32_t *__restrict__ rowmap, int ngroups, int nkv, int group,
+    float sl2) {
   static_assert(HD % 32 == 0 && HD <= 128, "head dimension");
   constexpr int KS = HD / 32;   // reduction slices of S^T
   constexpr int DT = HD / 16;   // 16-dim row blocks of O^T
   constexpr int PITCH = HD * 2;  // bytes per key row of the LDS V tile
   constexpr int NCH = HD / 8;    // 16-byte chunks per key row
-  // each wave's V tile buffers (two when PIPE; separate arrays)
-  __shared__ __attribute__((aligned(16))) char vbufA[NWV][64 * PITCH];
-  __shared__ __attribute__((aligned(16))) char vbufB[NWV][PIPE ? 64 * PITCH : 16];
-  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  // the two V tile buffers (separate arrays)
+  __shared__ __attribute__((aligned(16))) char vbA[64 * PITCH];
+  __shared__ __attribute__((aligned(16))) char vbB[64 * PITCH];
+  const int lane = threadIdx.x & 63;
   const int r16 = lane & 15, g = lane >> 4;
-  const int gw = blockIdx.x * NWV + w;
-  if (gw >= ngroups) return;  // whole wave (the waves of a workgroup never meet at a barrier)
-  char *vbA = vbufA[w], *vbB = vbufB[w];
+  const int gw = blockIdx.x;
+  if (gw >= ngroups) return;
 
-  ColGroup cg{};
-  if (!prefill) {
-    // decode: group gw = (row b, kv head kh); column j = q head kh * group + j of row b
-    const int b = gw / nkv;
-    cg.kh = gw - b * nkv;
-    const int crow = rowmap ? rowmap[b] : b;
-    const int L = min(max(lens[b], 0), cache_len);
-    cg.ok = crow >= 0 && crow < cache_rows;
-    cg.crow = crow;
-    cg.lmax = cg.lmin = L;
-    cg.valid = r16 < group;
-    cg.qrow = b;
-    cg.head = cg.kh * group + r16;
-    cg.L = L;
-  } else {
-    // prefill: group gw = (block, q head h, 16-row sub-block sb); column j = row 16 sb + j of the block
-    const int per = nq * 4;
-    const int blk = gw / per, rem = gw - blk * per;
-    const int h = rem >> 2, sb = rem & 3;
-    const int n = bn[blk], q0 = bq0[blk], p0 = bpos0[blk];
-    const int64_t sl = bslot[blk];
-    const int nv = min(min(n, 64), R - q0);
-    const int hi = min(p0 + n, cache_len);
-    cg.ok = n > 0 && sl >= 0 && sl < cache_rows && p0 >= 0 && q0 >= 0 && q0 < R && 16 * sb < nv && hi > 0;
-    cg.crow = sl;
-    cg.kh = h / group;
-    const int last = min(16 * sb + 15, nv - 1);
-    cg.lmax = min(p0 + last + 1, hi);
-    cg.lmin = min(p0 + 16 * sb + 1, hi);
-    const int row = 16 * sb + r16;
-    cg.valid = row < nv;
-    cg.qrow = (int64_t)q0 + row;
-    cg.head = h;
-    cg.L = cg.valid ? min(p0 + row + 1, hi) : 0;
-  }
-  if (!cg.ok) return;
-  if (!cg.valid) cg.L = 0;
+  // group gw = (row b, kv head kh); column j = q head kh * group + j of row b
+  const int b = gw / nkv;
+  const int kh = gw - b * nkv;
+  const int crow = rowmap ? rowmap[b] : b;
+  const int L = min(max(lens[b], 0), cache_len);
+  if (crow < 0 || crow >= cache_rows) return;
+  const bool valid = r16 < group;  // this lane's column exists
+  const int head = kh * group + r16;
+  const int Lc = valid ? L : 0;    // this column's key count
 
   // Q^T operands: column r16, dims 32s + 8g..+7 (zeros for a missing column)
   u32x4 qb[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) qb[s] = u32x4{0u, 0u, 0u, 0u};
-  if (cg.valid) {  // (a missing column's address may lie past q)
-    const uint16_t *qp = q + cg.qrow * s_qr + (int64_t)cg.head * s_qh + 8 * g;
+  if (valid) {  // (a missing column's address may lie past q)
+    const uint16_t *qp = q + (int64_t)b * s_qr + (int64_t)head * s_qh + 8 * g;
 #pragma unroll
     for (int s = 0; s < KS; ++s) qb[s] = ld16(qp + 32 * s);
   }
-  // K / V of the cache row and kv head as buffers over keys [0, lmax): rows past it read as zeros
-  const int64_t cb = cg.crow * s_kb + (int64_t)cg.kh * s_kh;
+  // K / V of the cache row and kv head as buffers over keys [0, L): rows past it read as zeros
+  const int64_t cb = (int64_t)crow * s_kb + (int64_t)kh * s_kh;
   constexpr uint32_t kRowB = HD * 2;
-  const rsrc_t kr = make_rsrc(kc + cb, (uint32_t)cg.lmax * kRowB);
-  const rsrc_t vr = make_rsrc(vc + cb, (uint32_t)cg.lmax * kRowB);
+  const rsrc_t kr = make_rsrc(kc + cb, (uint32_t)L * kRowB);
+  const rsrc_t vr = make_rsrc(vc + cb, (uint32_t)L * kRowB);
   // K operand rows of this lane: key 32c + 8(r16/4) + 4t + r16%4 of the tile
   const uint32_t krow = (uint32_t)(8 * (r16 >> 2) + (r16 & 3));
   // V DMA: instruction i writes rows (16 i + lane) / NCH.., lane l's 16 bytes to LDS chunk l % NCH of its row,
@@ -133,8 +86,8 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_cols(
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // PIPE: two tile buffers (V in LDS, K in registers), the next tile's loads in flight while one is computed;
-  // a request past lmax reads zeros without memory traffic. Otherwise one buffer, loads then compute.
+  // Two tile buffers (V in LDS, K in registers), the next tile's loads in flight while one is computed; a
+  // request past L reads zeros without memory traffic.
   u32x4 kA[2][2][KS], kB[2][2][KS];
   auto load = [&](u32x4 (&ka)[2][2][KS], char *vtile, int t0) __attribute__((always_inline)) {
     // every earlier read of this buffer done before its DMA can land
@@ -151,12 +104,12 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_cols(
           ka[c][t][s] = bld16(kr, ((uint32_t)t0 + 32u * c + krow + 4u * t) * kRowB + (uint32_t)(32 * s + 8 * g) * 2u);
   };
   // consumes the tile at t0 (K in ka, V in vtile); the V reads wait for its DMA: after it went out, its own
-  // 4 KS K loads, and with PIPE the next tile's VDMA + 4 KS requests
+  // 4 KS K loads and the next tile's VDMA + 4 KS requests
   auto tile = [&](const u32x4 (&ka)[2][2][KS], const char *vtile, int t0) __attribute__((always_inline)) {
-    // scores, masked per column where the tile reaches past some column's key count
+    // scores, masked where the tile reaches past the key count (and for a missing column)
     f32x4 sc[2][2];
     float mt = kNegInf;
-    const bool mask = t0 + 64 > cg.lmin || !cg.valid;
+    const bool mask = t0 + 64 > L || !valid;
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -167,7 +120,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_cols(
         if (mask) {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (t0 + 32 * c + 8 * g + 4 * t + i >= cg.L) a[i] = kNegInf;
+            if (t0 + 32 * c + 8 * g + 4 * t + i >= Lc) a[i] = kNegInf;
         }
         mt = fmaxf(mt, fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3])));
         sc[c][t] = a;
@@ -197,7 +150,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_cols(
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
     }
-    wait_vmcnt<PIPE ? 8 * KS + VDMA : 4 * KS>();  // the V tile has landed
+    wait_vmcnt<8 * KS + VDMA>();  // the V tile has landed
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -207,28 +160,21 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_cols(
         o[dt] = mfma16x16x32(u32x4{lo[0], lo[1], hi2[0], hi2[1]}, pB[c], o[dt]);
       }
   };
-  if (PIPE) {
-    load(kA, vbA, 0);
-    for (int t0 = 0; t0 < cg.lmax; t0 += 128) {
-      load(kB, vbB, t0 + 64);
-      tile(kA, vbA, t0);
-      if (t0 + 64 >= cg.lmax) break;
-      load(kA, vbA, t0 + 128);
-      tile(kB, vbB, t0 + 64);
-    }
-  } else {
-    for (int t0 = 0; t0 < cg.lmax; t0 += 64) {
-      load(kA, vbA, t0);
-      tile(kA, vbA, t0);
-    }
+  load(kA, vbA, 0);
+  for (int t0 = 0; t0 < L; t0 += 128) {
+    load(kB, vbB, t0 + 64);
+    tile(kA, vbA, t0);
+    if (t0 + 64 >= L) break;
+    load(kA, vbA, t0 + 128);
+    tile(kB, vbB, t0 + 64);
   }
   // the request past the last tile still writes (zeros) into LDS: let it land before the wave ends
   wait_vmcnt<0>();
 
   // l = 0 (no key, decode lens = 0) gives 0 * inf = NaN, like the reference's 0 / 0
   const float rl = __builtin_amdgcn_rcpf(sum_over_groups(lsum));
-  if (!cg.valid) return;
-  uint16_t *op = out + cg.qrow * s_or + (int64_t)cg.head * s_oh + 4 * g;
+  if (!valid) return;
+  uint16_t *op = out + (int64_t)b * s_or + (int64_t)head * s_oh + 4 * g;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
     st8(op + 16 * dt, u32x2{pack_bf16x2(o[dt][0] * rl, o[dt][1] * rl), pack_bf16x2(o[dt][2] * rl, o[dt][3] * rl)});
@@ -250,30 +196,9 @@ int attn_cols_decode(const char *fn, const void *q, int64_t s_qb, int64_t s_qh, 
   if (ngroups > INT32_MAX / 2) return set_error(A8_EUNSUP, "%s: %d rows x %d kv heads too many", fn, b, nkv);
   if ((int64_t)cache_len * hd * 2 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "%s: cache of %d positions too long for 32-bit offsets", fn, cache_len);
-  hipLaunchKernelGGL((k_attn_cols<128, true, 1>), dim3((unsigned)ngroups), dim3(64), 0, stream, (const uint16_t *)q, s_qb, s_qh,
-                     b, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, cache_rows, cache_len,
-                     (uint16_t *)out, s_ob, s_oh, lens, rowmap, nullptr, nullptr, nullptr, nullptr, (int)ngroups, nq,
-                     nkv, group, false, scale * kLog2e);
-  return (int)hipGetLastError();
-}
-
-// Packed prefill over a block plan (a8_prefill_attn for head_dim 128).
-int attn_cols_prefill(const void *q, int64_t s_qr, int64_t s_qh, int R, const void *kc, const void *vc, int64_t s_kb,
-                      int64_t s_kh, int cache_rows, int cache_len, void *out, int64_t s_or, int64_t s_oh,
-                      const int32_t *bq0, const int32_t *bn, const int32_t *bslot, const int32_t *bpos0, int nblk,
-                      int nq, int group, int hd, float scale, hipStream_t stream) {
-  if (hd != 128) return set_error(A8_EUNSUP, "prefill_attn: head_dim %d not supported (64 or 128)", hd);
-  const int64_t ngroups = (int64_t)nblk * nq * 4;
-  if (ngroups == 0) return 0;
-  constexpr int kPfWaves = 4;
-  if (ngroups > INT32_MAX / 2) return set_error(A8_EUNSUP, "prefill_attn: %d blocks x %d heads too many", nblk, nq);
-  if ((int64_t)cache_len * hd * 2 >= ((int64_t)1 << 32))
-    return set_error(A8_EUNSUP, "prefill_attn: cache of %d positions too long for 32-bit offsets", cache_len);
-  hipLaunchKernelGGL((k_attn_cols<128, false, kPfWaves>), dim3((unsigned)((ngroups + kPfWaves - 1) / kPfWaves)),
-                     dim3(64 * kPfWaves), 0, stream, (const uint16_t *)q, s_qr, s_qh,
-                     R, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, cache_rows, cache_len,
-                     (uint16_t *)out, s_or, s_oh, nullptr, nullptr, bq0, bn, bslot, bpos0, (int)ngroups, nq,
-                     nq / group, group, true, scale * kLog2e);
+  hipLaunchKernelGGL((k_attn_cols<128>), dim3((unsigned)ngroups), dim3(64), 0, stream, (const uint16_t *)q, s_qb,
+                     s_qh, (const uint16_t *)kc, (const uint16_t *)vc, s_kb, s_kh, cache_rows, cache_len,
+                     (uint16_t *)out, s_ob, s_oh, lens, rowmap, (int)ngroups, nkv, group, scale * kLog2e);
   return (int)hipGetLastError();
 }
 

@@ -530,9 +530,9 @@ static int prefill_entry(const char *fn, const void *q, int64_t s_qr, int64_t s_
   if (s_ks != hd)
     return set_error(A8_EUNSUP, "%s: cache positions must be contiguous rows (s_ks %lld)", fn, (long long)s_ks);
   const int nkv = nq / group;
-  if (hd != 64)  // the generic-head kernel
-    return attn_cols_prefill(q, s_qr, s_qh, R, kc, vc, s_kb, s_kh, cache_rows, cache_len, out, s_or, s_oh, bq0, bn,
-                             bslot, bpos0, nblk, nq, group, hd, scale, (hipStream_t)stream);
+  if (hd != 64)  // head_dim 128 (prefill128.hip)
+    return prefill128(q, s_qr, s_qh, R, kc, vc, s_kb, s_kh, cache_rows, cache_len, out, s_or, s_oh, bq0, bn, bslot,
+                      bpos0, nblk, nq, group, scale, (hipStream_t)stream);
   const int hpw = group < kPfMaxHW ? group : kPfMaxHW;  // q heads (waves) per workgroup
   const int hsplit = (group + hpw - 1) / hpw;
   const int nh = nkv * hsplit;

@@ -286,7 +286,7 @@ int a8_store_decode_stream(const void *qkv, int64_t s_qkv, const void *bias,
  * bq0, bn, bslot, bpos0 [nblk] int32: block j covers packed rows [bq0, bq0 + bn) (bn <= bm) at
  *         positions [bpos0, bpos0 + bn) of cache row bslot; keys [0, bpos0 + bn) are attended with
  *         key <= query position. Blocks with bn <= 0 are no-ops (graph-mode padding).
- * group   q heads per kv head (nq / nkv); bm must be 64; hd 64, or 128 (the generic-head kernel).
+ * group   q heads per kv head (nq / nkv); bm must be 64; hd 64, or 128 (its own kernel: 32-key tiles, half blocks).
  */
 int a8_prefill_attn(const void *q, int64_t s_qr, int64_t s_qh, int R,
                     const void *kc, const void *vc, int64_t s_kb, int64_t s_kh, int64_t s_ks,

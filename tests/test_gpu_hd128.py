@@ -135,9 +135,11 @@ def test_decode_hd128_noalloc_and_fused(a8, ref, dev):
     assert maxabs(out2, want) <= TOL
 
 
-@pytest.mark.parametrize("nq,nkv", [(14, 2), (8, 8), (16, 1)])
+@pytest.mark.parametrize("nq,nkv", [(14, 2), (8, 8), (16, 1), (10, 2), (12, 2), (4, 4), (6, 2)])
 def test_prefill_hd128(a8, ref, dev, nq, nkv):
-    """Ragged requests after a prefix (one-tile to several-tile blocks), with a padding block (n = 0)."""
+    """Ragged requests after a prefix (one-tile to several-tile blocks, both halves of a block or only the first),
+    with a padding block (n = 0), at every workgroup shape (q heads per kv head 7 -> 4 + 3, 1, 16 -> 4 x 4,
+    5 -> 4 + 1, 6 -> 4 + 2, 3)."""
     group = nq // nkv
     say(f"case: prefill hd 128 nq={nq} nkv={nkv}")
     g = torch.Generator().manual_seed(70 + nq + nkv)
@@ -166,6 +168,36 @@ def test_prefill_hd128(a8, ref, dev, nq, nkv):
     err = maxabs(out, want)
     say(f"  R={R} blocks={len(blocks)} max-abs {err:.3e}")
     assert torch.isfinite(out.cpu().float()).all()
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("first,later", [(-4.5, 1.0), (4.5, -4.5), (-2.0, 3.0)])
+def test_prefill_hd128_extreme_scores(a8, ref, dev, first, later):
+    """Scores far from 0 in exp2 units (q . k x scale x log2 e up to about +-200 at 128 dims): keys 0..31 (the
+    first tile) `first` x ones, later keys `later` x ones, queries 3 x ones, plus noise. Covers the running
+    offset's underflow guard, the raise on the first tile and a first tile far above the rest."""
+    say(f"case: prefill hd 128 extreme scores, first tile {first}, later keys {later}")
+    g = torch.Generator().manual_seed(int(first * 10 + later * 100) & 0xffff)
+    nq, nkv = 14, 2
+    ns, p0s, slots = [64, 150, 40, 1, 33], [100, 0, 400, 511, 31], [0, 1, 2, 3, 4]
+    S, rows = 512, 5
+    R = sum(ns)
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    noise = lambda *shape: (torch.randn(*shape, generator=g) * 0.05)
+    kc = torch.full((rows, nkv, S, HD), later) + noise(rows, nkv, S, HD)
+    kc[:, :, :32] = first + noise(rows, nkv, 32, HD)
+    kc = kc.to(BF)
+    vc = randn_bf16(g, rows, nkv, S, HD)
+    q = (3.0 + noise(R, nq, HD)).to(BF)
+    want = torch.zeros(R, nq, HD, dtype=BF)
+    ref.prefill_attention(q, kc, vc, *ref.prefill_plan(r0s, ns, slots, p0s), want, nq // nkv)
+    out = torch.full((R, nq, HD), float("nan"), dtype=BF, device=dev)
+    a8.prefill_attention(q.to(dev), kc.to(dev), vc.to(dev), a8.PrefillPlan(r0s, ns, slots, p0s, dev), out, nq // nkv)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert torch.isfinite(got.float()).all()
+    err = maxabs(got, want)
+    say(f"  max-abs {err:.3e}")
     assert err <= TOL
 
 
