@@ -65,13 +65,15 @@ __global__ __launch_bounds__(64 * kPf128HW, 2) void k_prefill128(
   __shared__ __attribute__((aligned(16))) uint16_t vC[kTile128];
   // Q^T operands: [wave][group][dim slice][lane] x 16 bytes (8 KB per wave)
   __shared__ __attribute__((aligned(16))) uint16_t qs[kPf128HW * UPW2 * 4 * 64 * 8];
-  // Unit u = (block, half, kv head) in order, the hsplit head shares of a unit 8 workgroups apart (one XCD),
-  // the grid padded to whole runs of 8 units.
+  // Unit u = (block, kv head) in order; its 2 x hsplit workgroups (half block, head share) 8 apart, so all of
+  // them run on one XCD and share the unit's tiles in its L2 (C4's shape: 83.0 -> 82.5 us against the halves
+  // as separate units on neighbouring XCDs); the grid padded to whole runs of 8 units.
   const int nkv_ = nh / hsplit;
-  const int chunk = blockIdx.x / (8 * hsplit), rem = blockIdx.x - chunk * (8 * hsplit);
-  const int hs = rem >> 3, u = chunk * 8 + (rem & 7);
-  const int bh = u / nkv_, kh = u - bh * nkv_;
-  const int blk = bh >> 1, half = bh & 1;
+  const int nsh = 2 * hsplit;  // workgroups per (block, kv head): halves x head shares
+  const int chunk = blockIdx.x / (8 * nsh), rem = blockIdx.x - chunk * (8 * nsh);
+  const int sh = rem >> 3, u = chunk * 8 + (rem & 7);
+  const int half = sh >= hsplit ? 1 : 0, hs = sh - half * hsplit;
+  const int blk = u / nkv_, kh = u - blk * nkv_;
   if (blk >= nblk_) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -363,7 +365,7 @@ int prefill128(const void *q, int64_t s_qr, int64_t s_qh, int R, const void *kc,
     return set_error(A8_EUNSUP, "prefill_attn: q row stride %lld outside [128, 2^24)", (long long)s_qr);
   if ((int64_t)cache_len * kRow128 >= ((int64_t)1 << 32))
     return set_error(A8_EUNSUP, "prefill_attn: cache of %d positions too long for 32-bit offsets", cache_len);
-  const int64_t grid = ((int64_t)nblk * 2 * nkv + 7) / 8 * 8 * hsplit;
+  const int64_t grid = ((int64_t)nblk * nkv + 7) / 8 * 8 * 2 * hsplit;
   if (grid * 64 * hpw > (int64_t)UINT32_MAX)
     return set_error(A8_EUNSUP, "prefill_attn: too many blocks x heads (%d x %d)", nblk, nh);
   static_assert(kPf128HW == 4, "one instantiation per workgroup size");

@@ -742,8 +742,8 @@ def slow_probe(a8, torch, dev, shapes=None):
 
 def prefill_probe(a8, torch, dev):
     """Counter target for the prefill: the C4 workload (64 requests, n ~ U[40, 400] after a 300-position
-    prefix, 13,745 packed rows) launched 3 times over a stored q, then 3 times forming q from qkv rows. Run
-    under rocprofv3 --pmc with one counter group a pass."""
+    prefix, 13,745 packed rows) launched 3 times over a stored q, then 3 times forming q from qkv rows, then 3
+    times at head_dim 128. Run under rocprofv3 --pmc with one counter group a pass."""
     import numpy as np
     g = torch.Generator(device=dev).manual_seed(7)
     ns = torch.randint(40, 401, (64,), generator=torch.Generator().manual_seed(0)).tolist()
@@ -764,8 +764,16 @@ def prefill_probe(a8, torch, dev):
     cos, sin = a8.rope_tables(10000.0, HD, S, dev)
     for _ in range(3):
         a8.prefill_attention_qkv(qkv, bias, cos, sin, kc, vc, plan, out, NQ // NKV)
+    # and the same plan at head_dim 128 (k_prefill128), 3 times
+    kc2 = torch.randn(nreq + 1, NKV, S, 128, generator=g, device=dev).to(torch.bfloat16)
+    vc2 = torch.randn(nreq + 1, NKV, S, 128, generator=g, device=dev).to(torch.bfloat16)
+    q2 = torch.randn(R, NQ, 128, generator=g, device=dev).to(torch.bfloat16)
+    out2 = torch.empty_like(q2)
+    for _ in range(3):
+        a8.prefill_attention(q2, kc2, vc2, plan, out2, NQ // NKV)
     torch.cuda.synchronize()
-    print(f"prefill probe: 3 + 3 launches (q stored / q from qkv), {R} rows, {plan.nblk} blocks", flush=True)
+    print(f"prefill probe: 3 + 3 + 3 launches (q stored / q from qkv / head_dim 128), {R} rows, {plan.nblk} blocks",
+          flush=True)
 
 
 def main():
