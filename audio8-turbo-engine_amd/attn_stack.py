@@ -79,12 +79,12 @@ class AttnStack:
         2-token pass) must keep fuse=False. With a plan (the admission's packed prefill), fuse=True stores
         k / v only and the prefill forms q from qkv itself (prefill_attention_qkv; each row's position is its
         block's pos0 + its index in the block, as the plan of an admission has it): the same out bits, and q
-        is neither written nor read."""
+        is neither written nor read (head_dim 64; at 128 it makes the two calls)."""
         if plan is None and fuse:
             return self.attn.store_and_attend(qkv, bias, self.cos, self.sin, pos, slot, q, self.kc[i], self.vc[i],
                                               lens, o, nsplit=nsplit, rowmap=slot if rowmap else None,
                                               ring=self.ring, write_q=False)
-        if plan is not None and fuse:
+        if plan is not None and fuse and self.hd == 64:
             bias_rope_store(qkv, bias, self.cos, self.sin, pos, slot, None, self.kc[i], self.vc[i],
                             self.nq, self.nkv, self.hd, ring=self.ring)
             return prefill_attention_qkv(qkv, bias, self.cos, self.sin, self.kc[i], self.vc[i], plan, o,

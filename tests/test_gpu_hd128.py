@@ -201,6 +201,38 @@ def test_prefill_hd128_extreme_scores(a8, ref, dev, first, later):
     assert err <= TOL
 
 
+def test_attn_stack_prefill_hd128_fuse(a8, dev):
+    """AttnStack at head_dim 128 with a prefill plan: fuse=True (no q-forming prefill at this width: the store
+    writes q and the prefill reads it) gives the fuse=False bits."""
+    say("case: stack prefill hd 128, fuse=True vs fuse=False")
+    g = torch.Generator().manual_seed(77)
+    nq, nkv, layers, rows, S = 14, 2, 2, 4, 512
+    ns, p0s, slots = [100, 37, 64], [0, 200, 300], [2, 0, 1]
+    R = sum(ns)
+    W = (nq + 2 * nkv) * HD
+    st = a8.AttnStack(layers, nq, nkv, HD, 10000.0, max_rows=R, cache_rows=rows, cache_len=S, max_pos=S, dev=dev)
+    qkv = [randn_bf16(g, R, W).to(dev) for _ in range(layers)]
+    bias = [randn_bf16(g, W, std=0.02).to(dev) for _ in range(layers)]
+    pos = torch.cat([a + torch.arange(n) for a, n in zip(p0s, ns)]).int().to(dev)
+    slot = torch.cat([torch.full((n,), s_) for s_, n in zip(slots, ns)]).int().to(dev)
+    r0s = [int(x) for x in np.cumsum([0] + ns[:-1])]
+    plan = a8.PrefillPlan(r0s, ns, slots, p0s, dev)
+    kc0, vc0 = randn_bf16(g, layers, rows, nkv, S, HD).to(dev), randn_bf16(g, layers, rows, nkv, S, HD).to(dev)
+    res = []
+    for fuse in (False, True):
+        st.kc_all.copy_(kc0)
+        st.vc_all.copy_(vc0)
+        q = torch.zeros(R, nq, HD, dtype=BF, device=dev)
+        outs = [torch.zeros(R, nq, HD, dtype=BF, device=dev) for _ in range(layers)]
+        st.forward(qkv, bias, pos, slot, None, plan=plan, q=q, outs=outs, fuse=fuse)
+        torch.cuda.synchronize()
+        res.append(([o.cpu() for o in outs], st.kc_all.cpu(), st.vc_all.cpu()))
+    (o1, k1, v1), (o2, k2, v2) = res
+    assert all(torch.equal(a.view(torch.int16), b.view(torch.int16)) for a, b in zip(o1, o2))
+    assert torch.equal(k1.view(torch.int16), k2.view(torch.int16)) and torch.equal(v1.view(torch.int16), v2.view(torch.int16))
+    assert all(torch.isfinite(o.float()).all() for o in o2)
+
+
 def test_prefix_copy_hd128(a8, dev):
     say("case: prefix copy hd 128")
     g = torch.Generator().manual_seed(80)
